@@ -1,0 +1,165 @@
+"""ctypes wrapper of the CPU attention oracle (oracle/attn_ref.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py as the checker.  The product path
+(tokamak_amd/) never imports it.
+
+Input convention (shared by every parity test): one PCG32 stream per tensor,
+``seq`` = 1 for Q, 2 for K, 3 for V, 4 for dO; N(0,1) by Box-Muller, times
+``mul``, rounded to the compute dtype (ties to even).  Q, K and V are drawn in
+[B][S][H][D] order and packed as qkv[B][S][(Hq + 2*Hkv) * D] in Q | K | V
+head order (reference: src/tkm_registry.c:736-748).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libattn_ref.so")
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc + OpenMP)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.ar_pcg32_next.restype = ctypes.c_uint32
+        L.ar_fill_normal.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float]
+        L.ar_round_f16.argtypes = [_f32p, _u16p, ctypes.c_size_t]
+        L.ar_round_bf16.argtypes = [_f32p, _u16p, ctypes.c_size_t]
+        L.ar_widen_f16.argtypes = [_u16p, _f32p, ctypes.c_size_t]
+        L.ar_widen_bf16.argtypes = [_u16p, _f32p, ctypes.c_size_t]
+        L.ar_attn_fwd.argtypes = [_f32p, _f32p, _f32p, _i32p] + [ctypes.c_int] * 5 + [ctypes.c_float, ctypes.c_int, ctypes.c_int]
+        L.ar_attn_bwd.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i32p] + [ctypes.c_int] * 5 + [ctypes.c_float, ctypes.c_int, ctypes.c_int]
+        L.ar_set_threads.argtypes = [ctypes.c_int]
+        L.ar_get_threads.restype = ctypes.c_int
+        L.ar_online_cpus.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+class _Pcg32(ctypes.Structure):
+    _fields_ = [("state", ctypes.c_uint64), ("inc", ctypes.c_uint64)]
+
+
+def pcg32_sequence(initstate: int, initseq: int, n: int) -> np.ndarray:
+    L = lib()
+    rng = _Pcg32()
+    L.ar_pcg32_seed(ctypes.byref(rng), ctypes.c_uint64(initstate), ctypes.c_uint64(initseq))
+    return np.array([L.ar_pcg32_next(ctypes.byref(rng)) for _ in range(n)], dtype=np.uint32)
+
+
+def _fp(a):
+    return a.ctypes.data_as(_f32p)
+
+
+def normal(n: int, seed: int, seq: int, mul: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().ar_fill_normal(_fp(out), n, seed, seq, mul)
+    return out
+
+
+def round_to(x: np.ndarray, dtype: str):
+    """Round float32 array to fp16/bf16 (RNE); returns (rounded float32, uint16 bits)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    bits = np.empty(x.shape, dtype=np.uint16)
+    fn = {"f16": lib().ar_round_f16, "bf16": lib().ar_round_bf16}[dtype]
+    fn(_fp(x), bits.ctypes.data_as(_u16p), x.size)
+    return x, bits
+
+
+def widen(bits: np.ndarray, dtype: str) -> np.ndarray:
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, dtype=np.float32)
+    fn = {"f16": lib().ar_widen_f16, "bf16": lib().ar_widen_bf16}[dtype]
+    fn(bits.ctypes.data_as(_u16p), _fp(out), bits.size)
+    return out
+
+
+def make_inputs(B, S, Hq, Hkv, D, dtype="f16", seed_qkv=0, seed_do=1, mul=1.0, with_dout=True):
+    """Seeded packed qkv (and dO), rounded to dtype.
+
+    Returns dict with float32 views ``qkv``/``dout`` holding the rounded values
+    and ``qkv_bits``/``dout_bits`` (uint16) for upload, or fp32 arrays when
+    dtype == "f32"."""
+    q = normal(B * S * Hq * D, seed_qkv, 1, mul).reshape(B, S, Hq * D)
+    k = normal(B * S * Hkv * D, seed_qkv, 2, mul).reshape(B, S, Hkv * D)
+    v = normal(B * S * Hkv * D, seed_qkv, 3, mul).reshape(B, S, Hkv * D)
+    qkv = np.concatenate([q, k, v], axis=2)
+    out = {}
+    if dtype == "f32":
+        out["qkv"] = np.ascontiguousarray(qkv)
+    else:
+        out["qkv"], out["qkv_bits"] = round_to(qkv, dtype)
+    if with_dout:
+        do = normal(B * S * Hq * D, seed_do, 4, 1.0).reshape(B, S, Hq * D)
+        if dtype == "f32":
+            out["dout"] = do
+        else:
+            out["dout"], out["dout_bits"] = round_to(do, dtype)
+    return out
+
+
+def _kv(kv_len, B):
+    if kv_len is None:
+        return None, None
+    arr = np.ascontiguousarray(np.asarray(kv_len, dtype=np.int32).reshape(B))
+    return arr, arr.ctypes.data_as(_i32p)
+
+
+def set_threads(n: int) -> None:
+    lib().ar_set_threads(int(n))
+
+
+def threads() -> int:
+    return lib().ar_get_threads()
+
+
+def online_cpus() -> int:
+    return lib().ar_online_cpus()
+
+
+def fwd(qkv, B, S, Hq, Hkv, D, scale=None, causal=True, kv_len=None, f64=False):
+    """Returns (O [B][S][Hq*D], LSE [B][Hq][S]) as float32."""
+    qkv = np.ascontiguousarray(qkv, dtype=np.float32)
+    assert qkv.size == B * S * (Hq + 2 * Hkv) * D
+    scale = 1.0 / np.sqrt(np.float32(D)) if scale is None else scale
+    o = np.empty((B, S, Hq * D), dtype=np.float32)
+    lse = np.empty((B, Hq, S), dtype=np.float32)
+    keep, kvp = _kv(kv_len, B)
+    rc = lib().ar_attn_fwd(_fp(qkv), _fp(o), _fp(lse), kvp, B, S, Hq, Hkv, D, float(scale), int(causal), int(f64))
+    if rc != 0:
+        raise ValueError("ar_attn_fwd rejected its arguments")
+    return o, lse
+
+
+def bwd(qkv, o, dout, lse, B, S, Hq, Hkv, D, scale=None, causal=True, kv_len=None, f64=False):
+    """Returns dqkv [B][S][(Hq+2Hkv)*D] float32 (dQ | dK | dV)."""
+    qkv = np.ascontiguousarray(qkv, dtype=np.float32)
+    o = np.ascontiguousarray(o, dtype=np.float32)
+    dout = np.ascontiguousarray(dout, dtype=np.float32)
+    lse = np.ascontiguousarray(lse, dtype=np.float32)
+    scale = 1.0 / np.sqrt(np.float32(D)) if scale is None else scale
+    dqkv = np.empty_like(qkv)
+    keep, kvp = _kv(kv_len, B)
+    rc = lib().ar_attn_bwd(_fp(qkv), _fp(o), _fp(dout), _fp(lse), _fp(dqkv), kvp,
+                           B, S, Hq, Hkv, D, float(scale), int(causal), int(f64))
+    if rc != 0:
+        raise ValueError("ar_attn_bwd rejected its arguments")
+    return dqkv

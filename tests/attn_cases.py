@@ -1,0 +1,97 @@
+"""Shared helpers for the attention parity tests: seeded inputs, upload, comparison.
+
+Tolerances (element-wise, numpy allclose form |x - ref| <= atol + rtol*|ref|):
+  O, LSE      : atol 2e-3, rtol 1e-2
+  dQ, dK, dV  : atol 5e-3, rtol 2e-2
+against the CPU oracle run on the same rounded inputs.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+
+import oracle
+
+TOL_FWD = (2e-3, 1e-2)
+TOL_BWD = (5e-3, 2e-2)
+
+
+def log(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def to_device(bits: np.ndarray, dtype: str, device):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16))
+    return t.view(torch.float16 if dtype == "f16" else torch.bfloat16).to(device)
+
+
+def from_device(t) -> np.ndarray:
+    import torch
+    return t.detach().to(torch.float32).cpu().numpy()
+
+
+def compare(name: str, got: np.ndarray, ref: np.ndarray, tol) -> dict:
+    atol, rtol = tol
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    finite = np.isfinite(ref)
+    # equal infinities (LSE of fully masked rows) compare equal
+    inf_ok = np.all(got[~finite] == ref[~finite])
+    diff = np.abs(got[finite] - ref[finite])
+    bound = atol + rtol * np.abs(ref[finite])
+    bad = diff > bound
+    stats = {
+        "name": name,
+        "max_abs": float(diff.max()) if diff.size else 0.0,
+        "max_rel": float((diff / np.maximum(np.abs(ref[finite]), 1e-6)).max()) if diff.size else 0.0,
+        "n_bad": int(bad.sum()) + (0 if inf_ok else 1),
+        "n": int(ref.size),
+    }
+    if stats["n_bad"]:
+        idx = np.argwhere(np.abs(got - ref) > atol + rtol * np.abs(ref))[:5]
+        stats["examples"] = [(tuple(int(i) for i in ix), float(got[tuple(ix)]), float(ref[tuple(ix)]))
+                             for ix in idx]
+    return stats
+
+
+def split_dqkv(dqkv: np.ndarray, B, S, Hq, Hkv, D):
+    x = dqkv.reshape(B, S, Hq + 2 * Hkv, D)
+    return x[:, :, :Hq], x[:, :, Hq:Hq + Hkv], x[:, :, Hq + Hkv:]
+
+
+def run_gpu_case(device, B, S, Hq, Hkv, D, dtype="f16", causal=True, kv_len=None, mul=1.0,
+                 bwd=True, seed=0, f64=None):
+    """Runs the HIP forward (and backward) and the oracle; returns a list of compare() stats."""
+    import torch
+    from tokamak_amd import attn
+
+    tag = f"B{B} S{S} Hq{Hq} Hkv{Hkv} D{D} {dtype} causal={int(causal)} kv_len={kv_len} seed={seed}"
+    log(f"[case] {tag}")
+    inp = oracle.make_inputs(B, S, Hq, Hkv, D, dtype, seed_qkv=seed, seed_do=seed + 1, mul=mul,
+                             with_dout=bwd)
+    qkv = to_device(inp["qkv_bits"], dtype, device)
+    kvl = None if kv_len is None else torch.tensor(kv_len, dtype=torch.int32, device=device)
+    o, lse = attn.gqa_fwd(qkv, B, S, Hq, Hkv, D, causal=causal, kv_len=kvl)
+    if f64 is None:
+        f64 = B * Hq * S * S * D < 2e9
+    o_ref, lse_ref = oracle.fwd(inp["qkv"], B, S, Hq, Hkv, D, causal=causal, kv_len=kv_len, f64=f64)
+    res = [compare("O", from_device(o), o_ref, TOL_FWD), compare("LSE", from_device(lse), lse_ref, TOL_FWD)]
+    if bwd:
+        dout = to_device(inp["dout_bits"], dtype, device)
+        dqkv = attn.gqa_bwd(qkv, o, dout, lse, B, S, Hq, Hkv, D, causal=causal, kv_len=kvl)
+        torch.cuda.synchronize()
+        o_stored, _ = oracle.round_to(o_ref, dtype)  # the O a 16-bit forward stores
+        d_ref = oracle.bwd(inp["qkv"], o_stored, inp["dout"], lse_ref, B, S, Hq, Hkv, D,
+                           causal=causal, kv_len=kv_len, f64=f64)
+        got = split_dqkv(from_device(dqkv), B, S, Hq, Hkv, D)
+        ref = split_dqkv(d_ref, B, S, Hq, Hkv, D)
+        for nm, g, r in zip(("dQ", "dK", "dV"), got, ref):
+            res.append(compare(nm, g, r, TOL_BWD))
+    for st in res:
+        log(f"    {st['name']:>3}: max_abs={st['max_abs']:.3e} max_rel={st['max_rel']:.3e} "
+            f"bad={st['n_bad']}/{st['n']}" + (f" e.g. {st.get('examples')}" if st["n_bad"] else ""))
+    return res

@@ -1,0 +1,170 @@
+// attn_common.h -- device helpers shared by the CDNA4 (gfx950) attention kernels.
+//
+// MFMA operand layouts used throughout (v_mfma_f32_32x32x16_{f16,bf16}, wave64):
+//   lane l, l32 = l & 31, hi = l >> 5
+//   A (32 x 16) : lane holds A[m = l32][k = hi*8 + i],  i = 0..7   (one 128-bit VGPR quad)
+//   B (16 x 32) : lane holds B[k = hi*8 + i][n = l32],  i = 0..7
+//   C (32 x 32) : lane holds C[m = (r/4)*8 + hi*4 + (r%4)][n = l32], r = 0..15 (fp32)
+// An accumulator C[m][n] therefore feeds the next MFMA as a B operand (or, for
+// C[m=q][n=key], as an A operand of the transposed product) without any lane
+// exchange, provided the k index of that product is permuted the same way in
+// the other operand: k-slot (hi*8 + i) of a 16-wide k step ks stands for row
+//   kslot_row(ks, hi, i) = ks*16 + (i/4)*8 + hi*4 + (i%4)
+// of the accumulator.  Operands read from LDS that are indexed by such a
+// permuted k (V^T in the forward, Q^T/dO^T/K^T in the backward) are stored
+// with each 16-row group reordered by perm16 so one 128-bit read per lane
+// fetches the 8 slots in order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tkm {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+enum { DT_F16 = 0, DT_BF16 = 1 };
+
+// Position of row k (0..15) inside its 16-row group in LDS: swaps bits 2 and 3,
+// so that rows {0-3, 8-11} (k-slots of lanes 0-31) come first, then {4-7, 12-15}.
+__device__ __forceinline__ int perm16(int k) {
+    return (k & 3) | (((k >> 3) & 1) << 2) | (((k >> 2) & 1) << 3);
+}
+// Row of a 16-aligned block given its in-group index k; quads move as a unit.
+__device__ __forceinline__ int perm_row(int r) { return (r & ~15) | perm16(r & 15); }
+
+template <int DT>
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    if constexpr (DT == DT_F16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Two fp32 -> packed 16-bit (round to nearest even).
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float x, float y) {
+    if constexpr (DT == DT_F16) {
+        f16x2 h = {(_Float16)x, (_Float16)y};
+        return __builtin_bit_cast(uint32_t, h);
+    } else {
+        bf16x2 h = {(__bf16)x, (__bf16)y};
+        return __builtin_bit_cast(uint32_t, h);
+    }
+}
+
+// Sum of the two 16-bit values in w, accumulated in fp32.
+template <int DT>
+__device__ __forceinline__ float dot2_ones(uint32_t w, float acc) {
+    if constexpr (DT == DT_F16) {
+        const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
+    } else {
+        const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float to_f32(uint16_t bits) {
+    if constexpr (DT == DT_F16) return (float)__builtin_bit_cast(_Float16, bits);
+    else return __builtin_bit_cast(float, (uint32_t)bits << 16);
+}
+
+// Low / high 16-bit halves of two words, interleaved: (lo(a), lo(b)) and (hi(a), hi(b)).
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+    return (a & 0xffffu) | (b << 16);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+    return (a >> 16) | (b & 0xffff0000u);
+}
+
+__device__ __forceinline__ u32x4 ld_global16(const uint16_t* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ u32x4 ld_lds16(const uint16_t* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void st_lds16(uint16_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ void st_lds8(uint16_t* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+
+// ---------------------------------------------------------------------------
+// Tile movement HBM -> registers -> LDS.
+// A tile is ROWS consecutive sequence rows x D contiguous 16-bit values of one
+// head (row stride ld elements).  Thread t owns "quad chunks": 4 consecutive
+// rows x 8 columns (four 16-byte global loads), so a row-major LDS copy takes
+// 4 128-bit stores and a transposed copy takes 8 64-bit stores.
+template <int ROWS, int D, int NT>
+struct TileIO {
+    static constexpr int DC = D / 8;                 // 16-byte chunks per row
+    static constexpr int NCH = (ROWS / 4) * DC;      // quad chunks per tile
+    static constexpr int PER = (NCH + NT - 1) / NT;  // per thread
+    u32x4 r[PER][4];
+
+    // rows at or beyond row_end are zero-filled (never read).
+    __device__ __forceinline__ void load(const uint16_t* base, size_t ld, int row0, int row_end, int tid) {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            int c = tid + p * NT;
+            if (NCH % NT == 0 || c < NCH) {
+                int rg = c / DC, dc = c % DC;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    int row = row0 + rg * 4 + j;
+                    if (row < row_end)
+                        r[p][j] = ld_global16(base + (size_t)row * ld + dc * 8);
+                    else
+                        r[p][j] = u32x4{0u, 0u, 0u, 0u};
+                }
+            }
+        }
+    }
+    // row-major copy: lds[row * LDR + col]
+    template <int LDR>
+    __device__ __forceinline__ void store_rows(uint16_t* lds, int tid) const {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            int c = tid + p * NT;
+            if (NCH % NT == 0 || c < NCH) {
+                int rg = c / DC, dc = c % DC;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) st_lds16(lds + (rg * 4 + j) * LDR + dc * 8, r[p][j]);
+            }
+        }
+    }
+    // transposed copy with perm16 row order: lds[col * LDT + perm_row(row)]
+    template <int LDT>
+    __device__ __forceinline__ void store_cols(uint16_t* lds, int tid) const {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            int c = tid + p * NT;
+            if (NCH % NT == 0 || c < NCH) {
+                int rg = c / DC, dc = c % DC;
+                int prow = perm_row(rg * 4);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    // column dc*8 + 2w (low halves) and dc*8 + 2w + 1 (high halves)
+                    u32x2 lo = {pack_lo(r[p][0][w], r[p][1][w]), pack_lo(r[p][2][w], r[p][3][w])};
+                    u32x2 hi = {pack_hi(r[p][0][w], r[p][1][w]), pack_hi(r[p][2][w], r[p][3][w])};
+                    st_lds8(lds + (dc * 8 + 2 * w) * LDT + prow, lo);
+                    st_lds8(lds + (dc * 8 + 2 * w + 1) * LDT + prow, hi);
+                }
+            }
+        }
+    }
+};
+
+}  // namespace tkm

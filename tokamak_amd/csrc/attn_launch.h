@@ -1,0 +1,38 @@
+// attn_launch.h -- internal launch records passed from the C ABI layer to the kernels.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tkm {
+
+struct FwdArgs {
+    const void* qkv;
+    void* o;
+    float* lse;
+    const int32_t* kv_len;
+    int B, S, Hq, Hkv, D;
+    float scale;
+    int causal, dtype;
+    void* stream;
+};
+
+struct BwdArgs {
+    const void* qkv;
+    const void* o;
+    const void* dout;
+    const float* lse;
+    void* dqkv;
+    const int32_t* kv_len;
+    float* delta;  // workspace: B*Hq*S floats
+    int B, S, Hq, Hkv, D;
+    float scale;
+    int causal, dtype;
+    void* stream;
+};
+
+int launch_fwd(const FwdArgs& a);
+int launch_bwd_delta(const BwdArgs& a);
+int launch_bwd_dkdv(const BwdArgs& a);
+int launch_bwd_dq(const BwdArgs& a);
+
+}  // namespace tkm

@@ -1,0 +1,148 @@
+// tkm_attn_abi.hip -- the extern "C" entry points declared in include/tkm_attn.h:
+// argument validation, workspace checks and dispatch to the kernel launchers.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <hip/hip_runtime.h>
+
+#include "attn_launch.h"
+#include "tkm_attn.h"
+
+namespace {
+
+thread_local char g_err[256] = "";
+
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int status, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Shape checks shared by forward and backward (reference rules: tkm_core.c:392-404).
+int check_shape(int B, int S, int Hq, int Hkv, int D, int causal, int dtype) {
+    if (B < 1 || S < 1 || Hq < 1 || Hkv < 1)
+        return fail(TKM_ATTN_EINVAL, "sizes must be positive (B=%d S=%d Hq=%d Hkv=%d)", B, S, Hq, Hkv);
+    if (Hq % Hkv != 0) return fail(TKM_ATTN_EINVAL, "Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
+    if (D != 64 && D != 128) return fail(TKM_ATTN_EUNSUPPORTED, "head dim D=%d (supported: 64, 128)", D);
+    if (dtype != TKM_ATTN_F16 && dtype != TKM_ATTN_BF16)
+        return fail(TKM_ATTN_EUNSUPPORTED, "dtype %d (supported: TKM_ATTN_F16, TKM_ATTN_BF16)", dtype);
+    if (causal != 0 && causal != 1) return fail(TKM_ATTN_EINVAL, "causal must be 0 or 1, got %d", causal);
+    // Every element offset must fit in int64 and every grid dimension in 31 bits.
+    const double elems = (double)B * S * (Hq + 2.0 * Hkv) * D;
+    if (elems > 9.0e15) return fail(TKM_ATTN_EUNSUPPORTED, "tensor too large");
+    const double wgs = (double)B * Hq * ((S + 127) / 128 + 1);
+    if (wgs > 2147483647.0) return fail(TKM_ATTN_EUNSUPPORTED, "grid too large");
+    return TKM_ATTN_OK;
+}
+
+int run_bwd_stage(int stage, const tkm::BwdArgs& a) {
+    int rc = 0;
+    switch (stage) {
+        case TKM_ATTN_BWD_DELTA: rc = tkm::launch_bwd_delta(a); break;
+        case TKM_ATTN_BWD_DKDV: rc = tkm::launch_bwd_dkdv(a); break;
+        case TKM_ATTN_BWD_DQ: rc = tkm::launch_bwd_dq(a); break;
+        default: return fail(TKM_ATTN_EINVAL, "unknown backward stage %d", stage);
+    }
+    if (rc != 0) return fail(TKM_ATTN_ELAUNCH, "kernel launch failed in backward stage %d", stage);
+    return TKM_ATTN_OK;
+}
+
+int prepare_bwd(tkm::BwdArgs& a, const void* qkv, const void* o, const void* dout,
+                const float* lse, void* dqkv, const int32_t* kv_len, int B, int S, int Hq,
+                int Hkv, int D, float scale, int causal, int dtype, void* workspace,
+                size_t workspace_bytes, void* stream) {
+    if (!qkv || !o || !dout || !lse || !dqkv)
+        return fail(TKM_ATTN_EINVAL, "qkv, o, dout, lse and dqkv must be non-null");
+    int rc = check_shape(B, S, Hq, Hkv, D, causal, dtype);
+    if (rc) return rc;
+    if (!aligned(qkv, 16) || !aligned(o, 16) || !aligned(dout, 16) || !aligned(dqkv, 16) ||
+        !aligned(lse, 4) || (kv_len && !aligned(kv_len, 4)))
+        return fail(TKM_ATTN_EALIGN, "16-bit tensors must be 16-byte aligned, lse/kv_len 4-byte");
+    const size_t need = tkm_attn_bwd_workspace_bytes(B, S, Hq);
+    if (!workspace || workspace_bytes < need)
+        return fail(TKM_ATTN_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                    workspace ? workspace_bytes : (size_t)0);
+    if (!aligned(workspace, 16)) return fail(TKM_ATTN_EALIGN, "workspace must be 16-byte aligned");
+    if (!(scale == scale)) return fail(TKM_ATTN_EINVAL, "scale is NaN");
+    a = tkm::BwdArgs{qkv, o, dout, lse, dqkv, kv_len, (float*)workspace,
+                     B, S, Hq, Hkv, D, scale, causal, dtype, stream};
+    return TKM_ATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+TKM_ATTN_API int tkm_attn_fwd(const void* qkv, void* o, float* lse, const int32_t* kv_len, int B,
+                              int S, int Hq, int Hkv, int D, float scale, int causal, int dtype,
+                              void* stream) {
+    if (!qkv || !o) return fail(TKM_ATTN_EINVAL, "qkv and o must be non-null");
+    int rc = check_shape(B, S, Hq, Hkv, D, causal, dtype);
+    if (rc) return rc;
+    if (!aligned(qkv, 16) || !aligned(o, 16) || (lse && !aligned(lse, 4)) ||
+        (kv_len && !aligned(kv_len, 4)))
+        return fail(TKM_ATTN_EALIGN, "16-bit tensors must be 16-byte aligned, lse/kv_len 4-byte");
+    if (!(scale == scale)) return fail(TKM_ATTN_EINVAL, "scale is NaN");
+    tkm::FwdArgs a{qkv, o, lse, kv_len, B, S, Hq, Hkv, D, scale, causal, dtype, stream};
+    if (tkm::launch_fwd(a) != 0) return fail(TKM_ATTN_ELAUNCH, "forward kernel launch failed");
+    return TKM_ATTN_OK;
+}
+
+TKM_ATTN_API size_t tkm_attn_bwd_workspace_bytes(int B, int S, int Hq) {
+    if (B < 1 || S < 1 || Hq < 1) return 0;
+    const size_t n = (size_t)B * Hq * S * sizeof(float);
+    return (n + 255) & ~(size_t)255;
+}
+
+TKM_ATTN_API int tkm_attn_bwd(const void* qkv, const void* o, const void* dout, const float* lse,
+                              void* dqkv, const int32_t* kv_len, int B, int S, int Hq, int Hkv,
+                              int D, float scale, int causal, int dtype, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+    tkm::BwdArgs a;
+    int rc = prepare_bwd(a, qkv, o, dout, lse, dqkv, kv_len, B, S, Hq, Hkv, D, scale, causal,
+                         dtype, workspace, workspace_bytes, stream);
+    if (rc) return rc;
+    for (int stage : {TKM_ATTN_BWD_DELTA, TKM_ATTN_BWD_DKDV, TKM_ATTN_BWD_DQ}) {
+        rc = run_bwd_stage(stage, a);
+        if (rc) return rc;
+    }
+    return TKM_ATTN_OK;
+}
+
+TKM_ATTN_API int tkm_attn_bwd_stage(int stage, const void* qkv, const void* o, const void* dout,
+                                    const float* lse, void* dqkv, const int32_t* kv_len, int B,
+                                    int S, int Hq, int Hkv, int D, float scale, int causal,
+                                    int dtype, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+    if (stage < TKM_ATTN_BWD_DELTA || stage > TKM_ATTN_BWD_DQ)
+        return fail(TKM_ATTN_EINVAL, "unknown backward stage %d", stage);
+    tkm::BwdArgs a;
+    int rc = prepare_bwd(a, qkv, o, dout, lse, dqkv, kv_len, B, S, Hq, Hkv, D, scale, causal,
+                         dtype, workspace, workspace_bytes, stream);
+    if (rc) return rc;
+    return run_bwd_stage(stage, a);
+}
+
+TKM_ATTN_API const char* tkm_attn_status_string(int status) {
+    switch (status) {
+        case TKM_ATTN_OK: return "ok";
+        case TKM_ATTN_EINVAL: return "invalid argument";
+        case TKM_ATTN_EUNSUPPORTED: return "unsupported configuration";
+        case TKM_ATTN_EALIGN: return "misaligned pointer";
+        case TKM_ATTN_EWORKSPACE: return "workspace missing or too small";
+        case TKM_ATTN_ELAUNCH: return "kernel launch failed";
+        default: return "unknown status";
+    }
+}
+
+TKM_ATTN_API const char* tkm_attn_last_error(void) { return g_err; }
+
+TKM_ATTN_API int tkm_attn_version(void) { return 100; }
+
+}  // extern "C"
