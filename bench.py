@@ -1,0 +1,201 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (BASELINE.json metric).
+
+One step = one causal GQA attention forward + backward (tkm_attn_fwd, then the three
+backward kernels) over one batch of synthetic fp16 inputs already resident in HBM, at
+B=4, Hq=Hkv=16, S=2048, D=128, scale 1/sqrt(128).
+
+Prints one JSON line.  value = algorithmic fwd+bwd TFLOP/s (FlashAttention convention:
+F_fwd = 4*B*H*S^2*D/2 for causal, F_fwd+bwd = 3.5*F_fwd; recompute not credited).
+roofline = the dominant kernel (longest average duration inside the timed region, from
+HIP events recorded on the launch stream between the kernels), its algorithmic FLOPs per
+launch / its average duration, against MI355X dense fp16 MFMA peak 2516.6 TFLOP/s.
+cpu_baseline = the CPU oracle (oracle/attn_ref.c, fp32, OpenMP) timed on a bounded sample
+of the same workload on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3|cfg2|cfg5]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+PEAK_FP16_TFLOPS = 2516.6   # 256 CU x 4096 FLOP/clk x 2.4 GHz, dense
+PEAK_HBM_GBPS = 8000.0
+
+CONFIGS = {
+    # name: (B, S, Hq, Hkv, D, causal, kv_len, backward, qkv scale)
+    "cfg3": (4, 2048, 16, 16, 128, True, None, True, 1.0),
+    "cfg2": (4, 1024, 8, 8, 64, True, None, False, 0.5),
+    "cfg5": (2, 8192, 32, 32, 128, False, [8192, 5000], True, 1.0),
+}
+METRIC = "FlashAttn fwd+bwd TFLOP/s & % fp16 MFMA peak, B4 H16 S2048 D128 causal"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="threads for the CPU baseline (default: min(16, online CPUs))")
+    return ap.parse_args()
+
+
+def cpu_baseline(cfg, threads):
+    """Time the CPU oracle on a bounded sample: the workload restricted to its first
+    batch and at most 4 heads (all S x S positions), forward + backward, fp32."""
+    import numpy as np
+
+    import oracle
+    B, S, Hq, Hkv, D, causal, kv_len, backward, mul = cfg
+    hs = min(Hq, 4)
+    kvl = None if kv_len is None else kv_len[:1]
+    oracle.set_threads(threads)
+    inp = oracle.make_inputs(1, S, hs, hs, D, "f16", mul=mul, with_dout=backward)
+    t0 = time.perf_counter()
+    o, lse = oracle.fwd(inp["qkv"], 1, S, hs, hs, D, causal=causal, kv_len=kvl)
+    if backward:
+        oracle.bwd(inp["qkv"], o, inp["dout"], lse, 1, S, hs, hs, D, causal=causal, kv_len=kvl)
+    dt = time.perf_counter() - t0
+    skv = S if kvl is None else float(np.mean(kvl))
+    f = 4.0 * 1 * hs * S * skv * D * (0.5 if causal else 1.0) * (3.5 if backward else 1.0)
+    return {"value": round(f / dt / 1e12, 6), "unit": "TFLOP/s", "cores": oracle.threads(),
+            "kind": "port",
+            "sample": f"oracle/attn_ref.c fp32 {'fwd+bwd' if backward else 'fwd'} on B=1 H={hs} "
+                      f"S={S} D={D} causal={int(causal)} (1 batch, {hs} of {Hq} heads), "
+                      f"{dt:.2f} s wall"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build targets one GPU: the attention kernels run on one "
+                          "MI355X; multi-GPU sharding is design-only (run with --gpus 1)"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from tokamak_amd import attn
+
+    cfg = CONFIGS[args.config]
+    B, S, Hq, Hkv, D, causal, kv_len, backward, mul = cfg
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    qkv = (torch.randn((B, S, (Hq + 2 * Hkv) * D), generator=g, device=dev) * mul).half()
+    g.manual_seed(1)
+    dout = torch.randn((B, S, Hq * D), generator=g, device=dev).half()
+    o = torch.empty((B, S, Hq * D), dtype=torch.float16, device=dev)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
+    dqkv = torch.empty_like(qkv)
+    ws = torch.empty(attn.bwd_workspace_bytes(B, S, Hq), dtype=torch.uint8, device=dev)
+    kvl = None if kv_len is None else torch.tensor(kv_len, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+
+    stages = [("attn_fwd", lambda: attn.gqa_fwd(qkv, B, S, Hq, Hkv, D, causal, kvl, out=o, lse=lse))]
+    if backward:
+        for name, st in (("bwd_delta", attn.BWD_DELTA), ("bwd_dkdv", attn.BWD_DKDV),
+                         ("bwd_dq", attn.BWD_DQ)):
+            stages.append((name, (lambda st=st: attn.gqa_bwd(
+                qkv, o, dout, lse, B, S, Hq, Hkv, D, causal, kvl, dqkv=dqkv, workspace=ws,
+                stage=st))))
+
+    for _ in range(args.warmup):
+        for _, fn in stages:
+            fn()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(K)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    for k in range(K):
+        ev[k][0].record(stream)
+        for i, (_, fn) in enumerate(stages):
+            fn()
+            ev[k][i + 1].record(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t_start.elapsed_time(t_end)
+    ms_step = total_ms / K
+
+    per = {name: np.array([ev[k][i].elapsed_time(ev[k][i + 1]) for k in range(K)])
+           for i, (name, _) in enumerate(stages)}
+    step_ms = np.array([ev[k][0].elapsed_time(ev[k][len(stages)]) for k in range(K)])
+
+    f_fwd = attn.attention_flops(B, S, Hq, D, causal, kv_len, "fwd")
+    f_total = f_fwd * (3.5 if backward else 1.0)
+    # Algorithmic FLOPs credited to each kernel (sums to F_fwd + 2.5 F_fwd):
+    # dK/dV kernel: S, dP, dV, dK GEMMs = 2.0 F_fwd; dQ kernel: the dQ GEMM = 0.5 F_fwd
+    # (its S and dP recompute is not credited); the D pre-pass is HBM-bound.
+    credit = {"attn_fwd": f_fwd, "bwd_dkdv": 2.0 * f_fwd, "bwd_dq": 0.5 * f_fwd}
+    delta_bytes = 2.0 * B * S * Hq * D * 2 + 4.0 * B * Hq * S
+    kernels = {}
+    for name, t in per.items():
+        avg = float(t.mean())
+        k = {"avg_ms": round(avg, 5), "p10_ms": round(float(np.percentile(t, 10)), 5),
+             "p90_ms": round(float(np.percentile(t, 90)), 5)}
+        if name in credit:
+            k["tflops"] = round(credit[name] / (avg * 1e-3) / 1e12, 2)
+            k["frac_peak"] = round(k["tflops"] / PEAK_FP16_TFLOPS, 4)
+        else:
+            k["gbps"] = round(delta_bytes / (avg * 1e-3) / 1e9, 1)
+        kernels[name] = k
+    dom = max(per, key=lambda n: per[n].mean())
+    dom_avg = float(per[dom].mean())
+    if dom in credit:
+        ach = credit[dom] / (dom_avg * 1e-3) / 1e12
+        roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                "avg_ms": round(dom_avg, 5), "flops_per_launch": credit[dom]}
+    else:
+        ach = delta_bytes / (dom_avg * 1e-3) / 1e9
+        roof = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
+                "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4), "traffic": None,
+                "avg_ms": round(dom_avg, 5)}
+
+    value = f_total / (ms_step * 1e-3) / 1e12
+    fwd_ms = float(per["attn_fwd"].mean())
+    res = {
+        "metric": METRIC if args.config == "cfg3" else f"FlashAttn TFLOP/s ({args.config})",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: Q/K/V, dO ~ N(0,1) (torch.randn on device, seeds 0/1), fp16",
+        "config": {"workload": f"{args.config}: GQA attention {'fwd+bwd' if backward else 'fwd'}",
+                   "B": B, "S": S, "Hq": Hq, "Hkv": Hkv, "D": D, "causal": causal,
+                   "kv_len": kv_len, "scale": "1/sqrt(D)"},
+        "frac_peak": round(value / PEAK_FP16_TFLOPS, 4),
+        "fwd": {"ms": round(fwd_ms, 5), "tflops": kernels["attn_fwd"]["tflops"],
+                "frac_peak": kernels["attn_fwd"]["frac_peak"]},
+        "step_ms_p10_p50_p90": [round(float(np.percentile(step_ms, p)), 5) for p in (10, 50, 90)],
+        "kernels": kernels,
+        "roofline": roof,
+        "wall_s": round(wall, 3),
+    }
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        res["cpu_baseline"] = cpu_baseline(cfg, threads)
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

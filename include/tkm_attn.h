@@ -14,7 +14,8 @@
  *       lse  [B][Hq][S] fp32, natural log of the row sum of exp(scaled scores) (tkm_gpu.cu:430)
  *       dout [B][S][Hq * D],  dqkv has the layout of qkv and is overwritten
  *   - q-head h attends with kv-head h / (Hq / Hkv)                (tkm_gpu.cu:315-316)
- *   - scores are scale * <q_i, k_j>; the runtime passes scale = 1/sqrtf(D) (tkm_gpu.cu:1258)
+ *   - scores are scale * <q_i, k_j>; the runtime passes scale = 1/sqrtf(D) (tkm_gpu.cu:1258);
+ *     scale must be positive and finite
  *   - key j is visible from query i iff j < S and (!causal || j <= i) (tkm_gpu.cu:393)
  * Extension (reference has none, its GQA op has no key-length input):
  *   - kv_len: optional device array of B int32; keys j >= kv_len[b] are masked.  Values are

@@ -101,6 +101,52 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 
+// Reductions across the two lane halves (l, l ^ 32) with v_permlane32_swap: the swap
+// leaves x[l] and x[l ^ 32] in the two results, in an order that does not matter here.
+__device__ __forceinline__ float half_max(float x) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// ---------------------------------------------------------------------------
+// Buffer resources and HBM -> LDS DMA.
+// A raw buffer resource covering `bytes` bytes from `base`: loads at offsets beyond it
+// return zero, which is how partial tiles (rows >= S or >= kv_len) are zero-filled.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+// 16 bytes per lane from rsrc+voffset into LDS at lds + 16*lane (lds is wave-uniform).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voffset, 0, 0, 0);
+}
+// Wait until every memory operation of this wave, LDS DMA included, has completed.
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0); }
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element i%4 of the
+// 8-byte words read by lanes 4e + i/4 (e = 0..3).  With lane j of the group pointing at
+// row j/4, columns 4*(j%4)..+3 of a 4 x 16 block of 16-bit values, lane i gets column i.
+__device__ __forceinline__ u32x2 ld_lds_tr(const char* p) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+    return __builtin_bit_cast(u32x2, v);
+}
+
+// Tiles in LDS are stored row-major without padding, one row = D 16-bit values = D/8
+// 16-byte chunks; chunk c of row r is stored at slot c ^ swz<D>(r).  The swizzle makes
+// both access patterns conflict-free on the 64 x 4-byte LDS banks:
+//   128-bit reads of one chunk from 16 consecutive rows (MFMA operands along the row),
+//   transposed 64-bit reads of 4 consecutive rows x 4 consecutive chunks.
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+    if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+    else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+}
+
 // ---------------------------------------------------------------------------
 // Tile movement HBM -> registers -> LDS.
 // A tile is ROWS consecutive sequence rows x D contiguous 16-bit values of one

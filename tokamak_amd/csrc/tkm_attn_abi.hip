@@ -2,6 +2,7 @@
 // argument validation, workspace checks and dispatch to the kernel launchers.
 #include <stdarg.h>
 #include <stdio.h>
+#include <math.h>
 #include <string.h>
 
 #include <hip/hip_runtime.h>
@@ -38,6 +39,9 @@ int check_shape(int B, int S, int Hq, int Hkv, int D, int causal, int dtype) {
     if (elems > 9.0e15) return fail(TKM_ATTN_EUNSUPPORTED, "tensor too large");
     const double wgs = (double)B * Hq * ((S + 127) / 128 + 1);
     if (wgs > 2147483647.0) return fail(TKM_ATTN_EUNSUPPORTED, "grid too large");
+    // Tiles are addressed through 32-bit buffer offsets: 128 rows of qkv must span < 2^31 bytes.
+    if ((double)(Hq + 2 * Hkv) * D * 2.0 * 128.0 >= 2147483648.0)
+        return fail(TKM_ATTN_EUNSUPPORTED, "row of qkv too wide ((Hq+2*Hkv)*D = %d)", (Hq + 2 * Hkv) * D);
     return TKM_ATTN_OK;
 }
 
@@ -69,7 +73,7 @@ int prepare_bwd(tkm::BwdArgs& a, const void* qkv, const void* o, const void* dou
         return fail(TKM_ATTN_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
                     workspace ? workspace_bytes : (size_t)0);
     if (!aligned(workspace, 16)) return fail(TKM_ATTN_EALIGN, "workspace must be 16-byte aligned");
-    if (!(scale == scale)) return fail(TKM_ATTN_EINVAL, "scale is NaN");
+    if (!(scale > 0.f) || scale == INFINITY) return fail(TKM_ATTN_EINVAL, "scale must be positive and finite");
     a = tkm::BwdArgs{qkv, o, dout, lse, dqkv, kv_len, (float*)workspace,
                      B, S, Hq, Hkv, D, scale, causal, dtype, stream};
     return TKM_ATTN_OK;
@@ -88,7 +92,7 @@ TKM_ATTN_API int tkm_attn_fwd(const void* qkv, void* o, float* lse, const int32_
     if (!aligned(qkv, 16) || !aligned(o, 16) || (lse && !aligned(lse, 4)) ||
         (kv_len && !aligned(kv_len, 4)))
         return fail(TKM_ATTN_EALIGN, "16-bit tensors must be 16-byte aligned, lse/kv_len 4-byte");
-    if (!(scale == scale)) return fail(TKM_ATTN_EINVAL, "scale is NaN");
+    if (!(scale > 0.f) || scale == INFINITY) return fail(TKM_ATTN_EINVAL, "scale must be positive and finite");
     tkm::FwdArgs a{qkv, o, lse, kv_len, B, S, Hq, Hkv, D, scale, causal, dtype, stream};
     if (tkm::launch_fwd(a) != 0) return fail(TKM_ATTN_ELAUNCH, "forward kernel launch failed");
     return TKM_ATTN_OK;
