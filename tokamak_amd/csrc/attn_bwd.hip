@@ -11,7 +11,8 @@
 // a key block (looping over every query block and every q-head of the kv group) and
 // written once, so the backward uses no atomics and is deterministic.  dQ is produced by
 // a separate pass that owns a query block and loops over key blocks.  All three write
-// (never accumulate into) dqkv, which has the qkv layout.
+// (never accumulate into) dqkv, which has the qkv layout.  Tile movement, LDS layout and
+// operand conventions are those of the forward (attn_common.h).
 #include "attn_common.h"
 #include "attn_launch.h"
 
@@ -49,39 +50,42 @@ __global__ __launch_bounds__(256) void fa_bwd_delta_kernel(const uint16_t* __res
 
 // ---------------------------------------------------------------- dK, dV
 // Workgroup = 4 waves = one (batch, kv-head, block of 128 keys); each wave owns 32 keys,
-// keeps K and V of those keys in registers (B operands) and dK/dV in accumulators.
-// Query tiles of BM rows (Q, dO: row-major for S and dP, transposed for dK and dV; LSE
-// and D) are staged through LDS, double-buffered.  Per tile and wave:
-//   S = Q K^T, dP = dO V^T       (C[m = query][n = key]; lane = key)
+// keeps K and V of those keys in registers (B operands of S and dP) and dK^T, dV^T in
+// accumulators.  It walks every query tile of 32 rows of every q-head of its kv group
+// (causal: only tiles at or below its keys); Q and dO tiles plus their LSE and D values go
+// HBM -> LDS by buffer DMA, double-buffered, tiles stored with the same swizzle as the
+// forward.  Per tile and wave:
+//   S = Q K^T, dP = dO V^T         C[m = query][n = key]: lane = key, registers = queries
 //   P = exp2(S*scale*log2e - LSE*log2e), dS = P (dP - D)
-//   dV += P^T dO, dK += dS^T Q  (P, dS accumulators are the A operands in place)
-template <int D, int DT, int BM>
-__global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
-    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dqkv,
-    const int32_t* __restrict__ kv_len, int B, int S, int Hq, int Hkv, float scale,
-    float scale_log2, int causal) {
-    constexpr int NT = 256, BN = 128;
+//   dV^T += dO^T P,  dK^T += Q^T dS the P / dS accumulators are the B operands in place,
+//                                  dO^T and Q^T come from transposed LDS reads
+// dK (times scale) and dV are written once; no atomics.
+template <int D, int DT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ dout,
+                        const float* __restrict__ lse, const float* __restrict__ delta,
+                        uint16_t* __restrict__ dqkv, const int32_t* __restrict__ kv_len, int B,
+                        int S, int Hq, int Hkv, float scale, float sl2, int causal) {
+    constexpr int BN = 128, BM = 32;
     constexpr int KS = D / 16;    // k-steps over the head dim (S, dP)
-    constexpr int QBT = BM / 32;  // 32-query blocks per tile
     constexpr int NDB = D / 32;   // 32-wide head-dim blocks of dK, dV
     constexpr int PKS = BM / 16;  // k-steps over queries (dK, dV)
-    constexpr int LDQ = D + 8;    // padded row-major row
-    constexpr int LDT = BM + 8;   // padded transposed row
-    __shared__ __attribute__((aligned(16))) uint16_t sQ[2][BM * LDQ];
-    __shared__ __attribute__((aligned(16))) uint16_t sdO[2][BM * LDQ];
-    __shared__ __attribute__((aligned(16))) uint16_t sQt[2][D * LDT];
-    __shared__ __attribute__((aligned(16))) uint16_t sdOt[2][D * LDT];
-    __shared__ __attribute__((aligned(16))) float sL[2][BM];
-    __shared__ __attribute__((aligned(16))) float sD[2][BM];
+    constexpr int ROWB = D * 2, CPR = D / 8, TILEB = BM * ROWB;
+    constexpr int RPI = 64 / CPR;     // rows per DMA instruction
+    constexpr int NI = BM / RPI / 4;  // DMA instructions per wave, per tile and tensor
+    __shared__ __attribute__((aligned(1024))) char smem[2][2][TILEB];  // [buffer][Q, dO]
+    __shared__ __attribute__((aligned(1024))) char sV[4][32 * ROWB];   // V rows of each wave
+    __shared__ __attribute__((aligned(16))) float sLD[2][2][64];       // [buffer][LSE, D]
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int l32 = lane & 31, hi = lane >> 5;
     const int nh = B * Hkv;
     const int kblk = blockIdx.x / nh;  // ascending key block = most query tiles first (causal)
     const int bh = blockIdx.x % nh, b = bh / Hkv, kvh = bh % Hkv;
     const int g = Hq / Hkv;
     const size_t ld = (size_t)(Hq + 2 * Hkv) * D, ldo = (size_t)Hq * D;
+    const uint32_t ldb = (uint32_t)(ld * 2), ldob = (uint32_t)(ldo * 2);
     const uint16_t* bqkv = qkv + (size_t)b * S * ld;
     uint16_t* bd = dqkv + (size_t)b * S * ld;
     int kvl = S;
@@ -92,153 +96,164 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
     const int kb0 = kblk * BN, kw0 = kb0 + wave * 32;
     const int key = kw0 + l32;  // this lane's key (column of S)
 
-    f32x16 dk[NDB], dv[NDB];
+    f32x16 dk[NDB], dv[NDB];  // dK^T, dV^T: C[m = d][n = key]
 #pragma unroll
     for (int db = 0; db < NDB; ++db) dk[db] = dv[db] = f32x16{};
 
     if (kb0 < kvl) {
-        u32x4 kf[KS], vf[KS];
+        // K of this lane's key in registers; V rows of the wave's 32 keys in LDS (register
+        // budget of 2 waves per SIMD), both B operands indexed [key][head dim].
+        u32x4 kf[KS];
         {
             const uint16_t* kp = bqkv + (size_t)key * ld + (size_t)(Hq + kvh) * D + hi * 8;
-            const uint16_t* vp = bqkv + (size_t)key * ld + (size_t)(Hq + Hkv + kvh) * D + hi * 8;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
+            for (int ks = 0; ks < KS; ++ks)
                 kf[ks] = key < kvl ? ld_global16(kp + ks * 16) : u32x4{0u, 0u, 0u, 0u};
-                vf[ks] = key < kvl ? ld_global16(vp + ks * 16) : u32x4{0u, 0u, 0u, 0u};
+            const int vrows = max(0, min(32, kvl - kw0));
+            const auto rv = make_rsrc(bqkv + (size_t)kw0 * ld + (size_t)(Hq + Hkv + kvh) * D,
+                                      (uint32_t)vrows * ldb);
+#pragma unroll
+            for (int i = 0; i < 32 / RPI; ++i) {
+                const int r = i * RPI + lane / CPR;
+                dma16(rv, &sV[wave][i * RPI * ROWB],
+                      (uint32_t)r * ldb + (uint32_t)(((lane % CPR) ^ swz<D>(r)) << 4));
             }
         }
         const int qt_begin = causal ? kb0 / BM : 0;
-        const int n_qt = (S + BM - 1) / BM;
-        const int nq = n_qt - qt_begin;
+        const int nq = (S + BM - 1) / BM - qt_begin;
         const int iters = g * nq;
 
-        TileIO<BM, D, NT> qio, dio;
-        auto fetch = [&](int it) {
+        const int dma_r = lane / CPR, dma_p = lane % CPR;
+        auto issue = [&](int it, int buf) {
             const int h = kvh * g + it / nq, qr0 = (qt_begin + it % nq) * BM;
-            qio.load(bqkv + (size_t)h * D, ld, qr0, S, tid);
-            dio.load(dout + (size_t)b * S * ldo + (size_t)h * D, ldo, qr0, S, tid);
-        };
-        auto stash = [&](int it, int buf) {
-            const int h = kvh * g + it / nq, qr0 = (qt_begin + it % nq) * BM;
-            qio.template store_rows<LDQ>(sQ[buf], tid);
-            qio.template store_cols<LDT>(sQt[buf], tid);
-            dio.template store_rows<LDQ>(sdO[buf], tid);
-            dio.template store_cols<LDT>(sdOt[buf], tid);
-            if (tid < BM) {
-                const int row = qr0 + tid;
-                const size_t li = ((size_t)b * Hq + h) * S + row;
-                sL[buf][tid] = row < S ? lse[li] * 1.4426950408889634f : INFINITY;
-                sD[buf][tid] = row < S ? delta[li] : 0.f;
+            const uint32_t rows = (uint32_t)min(BM, S - qr0);
+            const auto rq = make_rsrc(bqkv + (size_t)qr0 * ld + (size_t)h * D, rows * ldb);
+            const auto ro = make_rsrc(dout + ((size_t)b * S + qr0) * ldo + (size_t)h * D, rows * ldob);
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int r0 = (wave * NI + i) * RPI, r = r0 + dma_r;
+                const uint32_t sw = (uint32_t)((dma_p ^ swz<D>(r)) << 4);
+                dma16(rq, &smem[buf][0][r0 * ROWB], (uint32_t)r * ldb + sw);
+                dma16(ro, &smem[buf][1][r0 * ROWB], (uint32_t)r * ldob + sw);
+            }
+            if (wave == 0) {
+                const size_t li = ((size_t)b * Hq + h) * S + qr0;
+                dma4(make_rsrc(lse + li, rows * 4), &sLD[buf][0][0], (uint32_t)l32 * 4);
+                dma4(make_rsrc(delta + li, rows * 4), &sLD[buf][1][0], (uint32_t)l32 * 4);
             }
         };
-        fetch(0);
-        stash(0, 0);
+
+        const int fq = swz<D>(l32);  // row l32 of a tile: S/dP A-operand reads
+        const int trow = (lane & 15) >> 2;
+        const int tcol = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+
+        issue(0, 0);
+        wait_dma();
         __syncthreads();
 
         for (int it = 0; it < iters; ++it) {
             const int buf = it & 1;
             const int qr0 = (qt_begin + it % nq) * BM;
-            if (it + 1 < iters) fetch(it + 1);
+            if (it + 1 < iters) issue(it + 1, buf ^ 1);
             const bool active = !causal || (qr0 + BM - 1 >= kw0);
             if (active) {
-                const bool need_mask = (causal && qr0 < kw0 + 31) || (kw0 + 32 > kvl);
-                f32x16 s[QBT], dp[QBT];
-#pragma unroll
-                for (int qb = 0; qb < QBT; ++qb) s[qb] = dp[qb] = f32x16{};
+                const char* qt = smem[buf][0];
+                const char* ot = smem[buf][1];
+                f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-                    for (int qb = 0; qb < QBT; ++qb) {
-                        const int off = (qb * 32 + l32) * LDQ + ks * 16 + hi * 8;
-                        s[qb] = mfma32<DT>(ld_lds16(sQ[buf] + off), kf[ks], s[qb]);
-                        dp[qb] = mfma32<DT>(ld_lds16(sdO[buf] + off), vf[ks], dp[qb]);
-                    }
+                    const int off = l32 * ROWB + (((ks * 2 + hi) ^ fq) << 4);
+                    const u32x4 vfk = ld_lds16((const uint16_t*)(sV[wave] + off));
+                    s = mfma32<DT>(ld_lds16((const uint16_t*)(qt + off)), kf[ks], s);
+                    dp = mfma32<DT>(ld_lds16((const uint16_t*)(ot + off)), vfk, dp);
                 }
+                const bool need_mask = (causal && qr0 < kw0 + 31) || (kw0 + 32 > kvl) || (qr0 + BM > S);
                 u32x4 pf[PKS], sf[PKS];
 #pragma unroll
-                for (int qb = 0; qb < QBT; ++qb) {
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const f32x4 L = *reinterpret_cast<const f32x4*>(&sLD[buf][0][g4 * 8 + hi * 4]);
+                    const f32x4 Dl = *reinterpret_cast<const f32x4*>(&sLD[buf][1][g4 * 8 + hi * 4]);
+                    float p[4], ds[4];
 #pragma unroll
-                    for (int g4 = 0; g4 < 4; ++g4) {
-                        const f32x4 L = *reinterpret_cast<const f32x4*>(&sL[buf][qb * 32 + g4 * 8 + hi * 4]);
-                        const f32x4 Dl = *reinterpret_cast<const f32x4*>(&sD[buf][qb * 32 + g4 * 8 + hi * 4]);
-                        float p[4], ds[4];
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int r = g4 * 4 + i;
-                            float pv = fast_exp2(s[qb][r] * scale_log2 - L[i]);
-                            if (need_mask) {
-                                const int qrow = qr0 + qb * 32 + g4 * 8 + hi * 4 + i;
-                                if (key >= kvl || (causal && key > qrow)) pv = 0.f;
-                            }
-                            p[i] = pv;
-                            ds[i] = pv * (dp[qb][r] - Dl[i]);
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = g4 * 4 + i;
+                        float pv = fast_exp2(__builtin_fmaf(s[r], sl2, -L[i] * 1.4426950408889634f));
+                        if (need_mask) {
+                            const int qrow = qr0 + g4 * 8 + hi * 4 + i;
+                            if (key >= kvl || (causal && key > qrow) || qrow >= S) pv = 0.f;
                         }
-                        // registers r = g4*4..g4*4+3 are k-slots (g4&1)*4.. of step qb*2 + g4/2
-                        const int ks = qb * 2 + (g4 >> 1), w = (g4 & 1) * 2;
-                        pf[ks][w] = pack2<DT>(p[0], p[1]);
-                        pf[ks][w + 1] = pack2<DT>(p[2], p[3]);
-                        sf[ks][w] = pack2<DT>(ds[0], ds[1]);
-                        sf[ks][w + 1] = pack2<DT>(ds[2], ds[3]);
+                        p[i] = pv;
+                        ds[i] = pv * (dp[r] - Dl[i]);
                     }
+                    // registers g4*4..+3 are k-slots (g4&1)*4..+3 of query step g4/2
+                    const int ks = g4 >> 1, w = (g4 & 1) * 2;
+                    pf[ks][w] = pack2<DT>(p[0], p[1]);
+                    pf[ks][w + 1] = pack2<DT>(p[2], p[3]);
+                    sf[ks][w] = pack2<DT>(ds[0], ds[1]);
+                    sf[ks][w + 1] = pack2<DT>(ds[2], ds[3]);
                 }
 #pragma unroll
                 for (int ks = 0; ks < PKS; ++ks) {
 #pragma unroll
                     for (int db = 0; db < NDB; ++db) {
-                        const int off = (db * 32 + l32) * LDT + ks * 16 + hi * 8;
-                        dv[db] = mfma32<DT>(pf[ks], ld_lds16(sdOt[buf] + off), dv[db]);
-                        dk[db] = mfma32<DT>(sf[ks], ld_lds16(sQt[buf] + off), dk[db]);
+                        u32x2 vo[2], vq[2];
+#pragma unroll
+                        for (int tt = 0; tt < 2; ++tt) {
+                            const int row = ks * 16 + tt * 8 + hi * 4 + trow;
+                            const int d = db * 32 + tcol;
+                            const int off = row * ROWB + (((d >> 3) ^ swz<D>(row)) << 4) + (d & 7) * 2;
+                            vo[tt] = ld_lds_tr(ot + off);
+                            vq[tt] = ld_lds_tr(qt + off);
+                        }
+                        dv[db] = mfma32<DT>(u32x4{vo[0][0], vo[0][1], vo[1][0], vo[1][1]}, pf[ks], dv[db]);
+                        dk[db] = mfma32<DT>(u32x4{vq[0][0], vq[0][1], vq[1][0], vq[1][1]}, sf[ks], dk[db]);
                     }
                 }
             }
-            if (it + 1 < iters) stash(it + 1, buf ^ 1);
+            wait_dma();
             __syncthreads();
         }
     }
 
-    // dK (scaled), dV: C[m = key][n = d]; lane holds d = db*32 + l32, keys (r/4)*8 + hi*4 + r%4.
-    uint16_t* dkp = bd + (size_t)(Hq + kvh) * D;
-    uint16_t* dvp = bd + (size_t)(Hq + Hkv + kvh) * D;
+    // dK^T (scaled), dV^T: lane holds key = kw0 + l32, d = db*32 + g4*8 + hi*4 + 0..3.
+    if (key < S) {
+        uint16_t* dkp = bd + (size_t)key * ld + (size_t)(Hq + kvh) * D;
+        uint16_t* dvp = bd + (size_t)key * ld + (size_t)(Hq + Hkv + kvh) * D;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
+        for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int kr = kw0 + (r >> 2) * 8 + hi * 4 + (r & 3);
-            if (kr < S) {
-                const int d = db * 32 + l32;
-                const uint32_t wk = pack2<DT>(dk[db][r] * scale, 0.f);
-                const uint32_t wv = pack2<DT>(dv[db][r], 0.f);
-                dkp[(size_t)kr * ld + d] = (uint16_t)(wk & 0xffffu);
-                dvp[(size_t)kr * ld + d] = (uint16_t)(wv & 0xffffu);
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = db * 32 + g4 * 8 + hi * 4;
+                u32x2 wk = {pack2<DT>(dk[db][g4 * 4 + 0] * scale, dk[db][g4 * 4 + 1] * scale),
+                            pack2<DT>(dk[db][g4 * 4 + 2] * scale, dk[db][g4 * 4 + 3] * scale)};
+                u32x2 wv = {pack2<DT>(dv[db][g4 * 4 + 0], dv[db][g4 * 4 + 1]),
+                            pack2<DT>(dv[db][g4 * 4 + 2], dv[db][g4 * 4 + 3])};
+                *reinterpret_cast<u32x2*>(dkp + d) = wk;
+                *reinterpret_cast<u32x2*>(dvp + d) = wv;
             }
-        }
     }
 }
 
 // ---------------------------------------------------------------- dQ
 // Workgroup = 4 waves = one (batch, q-head, block of 128 queries); each wave owns 32
-// queries with Q and dO in registers (B operands) and walks key tiles of BN keys staged
-// in LDS (K and V row-major, K transposed).  Per tile and wave:
+// queries with Q and dO in registers (B operands) and walks key tiles of 64 keys; K and V
+// tiles go HBM -> LDS by buffer DMA, double-buffered, as in the forward.  Per tile and wave:
 //   S^T = K Q^T, dP^T = V dO^T  (lane = query row: LSE and D are per-lane scalars)
-//   dS^T = P^T (dP^T - D),  dQ^T += K^T dS^T
-template <int D, int DT, int BN>
-__global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
-    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dqkv,
-    const int32_t* __restrict__ kv_len, int B, int S, int Hq, int Hkv, float scale,
-    float scale_log2, int causal, int n_qblk) {
-    constexpr int NT = 256, BM = 128;
-    constexpr int KS = D / 16;
-    constexpr int NKB = BN / 32;
-    constexpr int NDB = D / 32;
-    constexpr int PKS = BN / 16;
-    constexpr int LDK = D + 8;
-    constexpr int LDT = BN + 8;
-    __shared__ __attribute__((aligned(16))) uint16_t sK[2][BN * LDK];
-    __shared__ __attribute__((aligned(16))) uint16_t sV[2][BN * LDK];
-    __shared__ __attribute__((aligned(16))) uint16_t sKt[2][D * LDT];
+//   dS^T = P^T (dP^T - D),  dQ^T += K^T dS^T  (K^T from transposed LDS reads)
+template <int D, int DT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ dout,
+                      const float* __restrict__ lse, const float* __restrict__ delta,
+                      uint16_t* __restrict__ dqkv, const int32_t* __restrict__ kv_len, int B,
+                      int S, int Hq, int Hkv, float scale, float sl2, int causal, int n_qblk) {
+    constexpr int BM = 128, BN = 64;
+    constexpr int KS = D / 16, NKB = BN / 32, NDB = D / 32, PKS = BN / 16;
+    constexpr int ROWB = D * 2, CPR = D / 8, TILEB = BN * ROWB;
+    constexpr int RPI = 64 / CPR, NI = BN / RPI / 4;
+    __shared__ __attribute__((aligned(1024))) char smem[2][2][TILEB];  // [buffer][K, V]
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int l32 = lane & 31, hi = lane >> 5;
     const int nh = B * Hq;
     const int bid = blockIdx.x;
@@ -246,9 +261,10 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
     const int bh = bid % nh, b = bh / Hq, h = bh % Hq;
     const int kvh = h / (Hq / Hkv);
     const size_t ld = (size_t)(Hq + 2 * Hkv) * D, ldo = (size_t)Hq * D;
+    const uint32_t ldb = (uint32_t)(ld * 2);
     const uint16_t* bqkv = qkv + (size_t)b * S * ld;
-    const uint16_t* Kp = bqkv + (size_t)(Hq + kvh) * D;
-    const uint16_t* Vp = bqkv + (size_t)(Hq + Hkv + kvh) * D;
+    const char* Kb = (const char*)(bqkv + (size_t)(Hq + kvh) * D);
+    const char* Vb = (const char*)(bqkv + (size_t)(Hq + Hkv + kvh) * D);
     int kvl = S;
     if (kv_len) {
         kvl = kv_len[b];
@@ -257,7 +273,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
     const int q0 = qblk * BM + wave * 32;
     const int q = q0 + l32;
     u32x4 qf[KS], of[KS];
-    float L2 = INFINITY, Dl = 0.f;
+    float nl2 = 0.f, Dl = 0.f;  // -LSE*log2(e) and D of this lane's query row
     if (q < S) {
         const uint16_t* qp = bqkv + (size_t)q * ld + (size_t)h * D + hi * 8;
         const uint16_t* op = dout + ((size_t)b * S + q) * ldo + (size_t)h * D + hi * 8;
@@ -267,7 +283,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
             of[ks] = ld_global16(op + ks * 16);
         }
         const size_t li = ((size_t)b * Hq + h) * S + q;
-        L2 = lse[li] * 1.4426950408889634f;
+        nl2 = -lse[li] * 1.4426950408889634f;
         Dl = delta[li];
     } else {
 #pragma unroll
@@ -278,30 +294,40 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
     if (causal) kv_end = min(kv_end, qblk * BM + BM);
     const int ntiles = (kv_end + BN - 1) / BN;
 
+    const int dma_r = lane / CPR, dma_p = lane % CPR;
+    auto issue = [&](int t, int buf) {
+        const int k0 = t * BN;
+        const uint32_t bytes = (uint32_t)min(BN, kv_end - k0) * ldb;
+        const auto rk = make_rsrc(Kb + (size_t)k0 * ldb, bytes);
+        const auto rv = make_rsrc(Vb + (size_t)k0 * ldb, bytes);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int r0 = (wave * NI + i) * RPI, r = r0 + dma_r;
+            const uint32_t voff = (uint32_t)r * ldb + (uint32_t)((dma_p ^ swz<D>(r)) << 4);
+            dma16(rk, &smem[buf][0][r0 * ROWB], voff);
+            dma16(rv, &smem[buf][1][r0 * ROWB], voff);
+        }
+    };
+    const int fk = swz<D>(l32);
+    const int trow = (lane & 15) >> 2;
+    const int tcol = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+
     f32x16 dq[NDB];
 #pragma unroll
     for (int db = 0; db < NDB; ++db) dq[db] = f32x16{};
 
-    TileIO<BN, D, NT> kio, vio;
-    if (ntiles > 0) {
-        kio.load(Kp, ld, 0, kv_end, tid);
-        vio.load(Vp, ld, 0, kv_end, tid);
-        kio.template store_rows<LDK>(sK[0], tid);
-        kio.template store_cols<LDT>(sKt[0], tid);
-        vio.template store_rows<LDK>(sV[0], tid);
-    }
+    if (ntiles > 0) issue(0, 0);
+    wait_dma();
     __syncthreads();
 
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
         const int k0 = t * BN;
-        if (t + 1 < ntiles) {
-            kio.load(Kp, ld, k0 + BN, kv_end, tid);
-            vio.load(Vp, ld, k0 + BN, kv_end, tid);
-        }
+        if (t + 1 < ntiles) issue(t + 1, buf ^ 1);
         const bool active = !causal || (k0 <= q0 + 31);
         if (active) {
-            const bool need_mask = (causal && k0 + BN - 1 > q0) || (k0 + BN > kvl);
+            const char* kt = smem[buf][0];
+            const char* vt = smem[buf][1];
             f32x16 s[NKB], dp[NKB];
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb) s[kb] = dp[kb] = f32x16{};
@@ -309,11 +335,12 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
             for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
                 for (int kb = 0; kb < NKB; ++kb) {
-                    const int off = (kb * 32 + l32) * LDK + ks * 16 + hi * 8;
-                    s[kb] = mfma32<DT>(ld_lds16(sK[buf] + off), qf[ks], s[kb]);
-                    dp[kb] = mfma32<DT>(ld_lds16(sV[buf] + off), of[ks], dp[kb]);
+                    const int off = (kb * 32 + l32) * ROWB + (((ks * 2 + hi) ^ fk) << 4);
+                    s[kb] = mfma32<DT>(ld_lds16((const uint16_t*)(kt + off)), qf[ks], s[kb]);
+                    dp[kb] = mfma32<DT>(ld_lds16((const uint16_t*)(vt + off)), of[ks], dp[kb]);
                 }
             }
+            const bool need_mask = (causal && k0 + BN - 1 > q0) || (k0 + BN > kvl);
             u32x4 sf[PKS];
 #pragma unroll
             for (int ks = 0; ks < PKS; ++ks) {
@@ -322,7 +349,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const int r = r0 + i;
-                    float pv = fast_exp2(s[kb][r] * scale_log2 - L2);
+                    float pv = fast_exp2(__builtin_fmaf(s[kb][r], sl2, nl2));
                     if (need_mask) {
                         const int kr = k0 + kb * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
                         if (kr >= kvl || (causal && kr > q)) pv = 0.f;
@@ -336,16 +363,18 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
             for (int ks = 0; ks < PKS; ++ks) {
 #pragma unroll
                 for (int db = 0; db < NDB; ++db) {
-                    const u32x4 a = ld_lds16(sKt[buf] + (db * 32 + l32) * LDT + ks * 16 + hi * 8);
-                    dq[db] = mfma32<DT>(a, sf[ks], dq[db]);
+                    u32x2 v[2];
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) {
+                        const int row = ks * 16 + tt * 8 + hi * 4 + trow;
+                        const int d = db * 32 + tcol;
+                        v[tt] = ld_lds_tr(kt + row * ROWB + (((d >> 3) ^ swz<D>(row)) << 4) + (d & 7) * 2);
+                    }
+                    dq[db] = mfma32<DT>(u32x4{v[0][0], v[0][1], v[1][0], v[1][1]}, sf[ks], dq[db]);
                 }
             }
         }
-        if (t + 1 < ntiles) {
-            kio.template store_rows<LDK>(sK[buf ^ 1], tid);
-            kio.template store_cols<LDT>(sKt[buf ^ 1], tid);
-            vio.template store_rows<LDK>(sV[buf ^ 1], tid);
-        }
+        wait_dma();
         __syncthreads();
     }
 
@@ -355,9 +384,8 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
-                const f32x16& acc = dq[db];
-                u32x2 w = {pack2<DT>(acc[g4 * 4 + 0] * scale, acc[g4 * 4 + 1] * scale),
-                           pack2<DT>(acc[g4 * 4 + 2] * scale, acc[g4 * 4 + 3] * scale)};
+                u32x2 w = {pack2<DT>(dq[db][g4 * 4 + 0] * scale, dq[db][g4 * 4 + 1] * scale),
+                           pack2<DT>(dq[db][g4 * 4 + 2] * scale, dq[db][g4 * 4 + 3] * scale)};
                 *reinterpret_cast<u32x2*>(qrow + db * 32 + g4 * 8 + hi * 4) = w;
             }
     }
@@ -375,10 +403,10 @@ static int launch_delta_t(const BwdArgs& a) {
 
 template <int D, int DT>
 static int launch_dkdv_t(const BwdArgs& a) {
-    constexpr int BM = 64, BN = 128;
+    constexpr int BN = 128;
     const int n_kblk = (a.S + BN - 1) / BN;
     dim3 grid((unsigned)(a.B * a.Hkv * n_kblk)), block(256);
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, DT, BM>), grid, block, 0, (hipStream_t)a.stream,
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, DT>), grid, block, 0, (hipStream_t)a.stream,
                        (const uint16_t*)a.qkv, (const uint16_t*)a.dout, a.lse, (const float*)a.delta,
                        (uint16_t*)a.dqkv, a.kv_len, a.B, a.S, a.Hq, a.Hkv, a.scale,
                        a.scale * 1.4426950408889634f, a.causal);
@@ -387,10 +415,10 @@ static int launch_dkdv_t(const BwdArgs& a) {
 
 template <int D, int DT>
 static int launch_dq_t(const BwdArgs& a) {
-    constexpr int BN = 64, BM = 128;
+    constexpr int BM = 128;
     const int n_qblk = (a.S + BM - 1) / BM;
     dim3 grid((unsigned)(a.B * a.Hq * n_qblk)), block(256);
-    hipLaunchKernelGGL((fa_bwd_dq_kernel<D, DT, BN>), grid, block, 0, (hipStream_t)a.stream,
+    hipLaunchKernelGGL((fa_bwd_dq_kernel<D, DT>), grid, block, 0, (hipStream_t)a.stream,
                        (const uint16_t*)a.qkv, (const uint16_t*)a.dout, a.lse, (const float*)a.delta,
                        (uint16_t*)a.dqkv, a.kv_len, a.B, a.S, a.Hq, a.Hkv, a.scale,
                        a.scale * 1.4426950408889634f, a.causal, n_qblk);

@@ -116,8 +116,11 @@ __device__ __forceinline__ float half_sum(float x) {
 // Buffer resources and HBM -> LDS DMA.
 // A raw buffer resource covering `bytes` bytes from `base`: loads at offsets beyond it
 // return zero, which is how partial tiles (rows >= S or >= kv_len) are zero-filled.
+// Both arguments must be wave-uniform; readfirstlane makes that explicit so the descriptor
+// lives in SGPRs (a VGPR descriptor would need a waterfall loop around every load).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                             __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000);
 }
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // 16 bytes per lane from rsrc+voffset into LDS at lds + 16*lane (lds is wave-uniform).
@@ -125,6 +128,10 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const void* lds,
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voffset, 0, 0, 0);
 }
 // Wait until every memory operation of this wave, LDS DMA included, has completed.
+// 4 bytes per lane from rsrc+voffset into LDS at lds + 4*lane.
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 4, voffset, 0, 0, 0);
+}
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0); }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));

@@ -46,7 +46,8 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
     constexpr int NI = BN / RPI / 4;    // DMA instructions per wave, per tile and tensor
     __shared__ __attribute__((aligned(1024))) char smem[2][2][TILEB];  // [buffer][K, V]
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int l32 = lane & 31, hi = lane >> 5;
     const int nh = B * Hq;
     const int bid = blockIdx.x;
