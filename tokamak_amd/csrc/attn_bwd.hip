@@ -169,6 +169,7 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
                 }
                 const bool need_mask = (causal && qr0 < kw0 + 31) || (kw0 + 32 > kvl) || (qr0 + BM > S);
                 u32x4 pf[PKS], sf[PKS];
+                u32x4 pl[Split<DT>::on ? PKS : 1], sl[Split<DT>::on ? PKS : 1];
 #pragma unroll
                 for (int g4 = 0; g4 < 4; ++g4) {
                     const f32x4 L = *reinterpret_cast<const f32x4*>(&sLD[buf][0][g4 * 8 + hi * 4]);
@@ -187,10 +188,23 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
                     }
                     // registers g4*4..+3 are k-slots (g4&1)*4..+3 of query step g4/2
                     const int ks = g4 >> 1, w = (g4 & 1) * 2;
-                    pf[ks][w] = pack2<DT>(p[0], p[1]);
-                    pf[ks][w + 1] = pack2<DT>(p[2], p[3]);
-                    sf[ks][w] = pack2<DT>(ds[0], ds[1]);
-                    sf[ks][w + 1] = pack2<DT>(ds[2], ds[3]);
+                    if constexpr (Split<DT>::on) {
+                        const u32x2 p01 = pack_split_bf16(p[0], p[1]), p23 = pack_split_bf16(p[2], p[3]);
+                        const u32x2 s01 = pack_split_bf16(ds[0], ds[1]), s23 = pack_split_bf16(ds[2], ds[3]);
+                        pf[ks][w] = p01[0];
+                        pl[ks][w] = p01[1];
+                        pf[ks][w + 1] = p23[0];
+                        pl[ks][w + 1] = p23[1];
+                        sf[ks][w] = s01[0];
+                        sl[ks][w] = s01[1];
+                        sf[ks][w + 1] = s23[0];
+                        sl[ks][w + 1] = s23[1];
+                    } else {
+                        pf[ks][w] = pack2<DT>(p[0], p[1]);
+                        pf[ks][w + 1] = pack2<DT>(p[2], p[3]);
+                        sf[ks][w] = pack2<DT>(ds[0], ds[1]);
+                        sf[ks][w + 1] = pack2<DT>(ds[2], ds[3]);
+                    }
                 }
 #pragma unroll
                 for (int ks = 0; ks < PKS; ++ks) {
@@ -205,8 +219,14 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
                             vo[tt] = ld_lds_tr(ot + off);
                             vq[tt] = ld_lds_tr(qt + off);
                         }
-                        dv[db] = mfma32<DT>(u32x4{vo[0][0], vo[0][1], vo[1][0], vo[1][1]}, pf[ks], dv[db]);
-                        dk[db] = mfma32<DT>(u32x4{vq[0][0], vq[0][1], vq[1][0], vq[1][1]}, sf[ks], dk[db]);
+                        const u32x4 ao = {vo[0][0], vo[0][1], vo[1][0], vo[1][1]};
+                        const u32x4 aq = {vq[0][0], vq[0][1], vq[1][0], vq[1][1]};
+                        dv[db] = mfma32<DT>(ao, pf[ks], dv[db]);
+                        dk[db] = mfma32<DT>(aq, sf[ks], dk[db]);
+                        if constexpr (Split<DT>::on) {
+                            dv[db] = mfma32<DT>(ao, pl[ks], dv[db]);
+                            dk[db] = mfma32<DT>(aq, sl[ks], dk[db]);
+                        }
                     }
                 }
             }
@@ -341,7 +361,7 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
                 }
             }
             const bool need_mask = (causal && k0 + BN - 1 > q0) || (k0 + BN > kvl);
-            u32x4 sf[PKS];
+            u32x4 sf[PKS], sl[Split<DT>::on ? PKS : 1];
 #pragma unroll
             for (int ks = 0; ks < PKS; ++ks) {
                 const int kb = ks >> 1, r0 = (ks & 1) * 8;
@@ -357,7 +377,15 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
                     ds[i] = pv * (dp[kb][r] - Dl);
                 }
 #pragma unroll
-                for (int w = 0; w < 4; ++w) sf[ks][w] = pack2<DT>(ds[2 * w], ds[2 * w + 1]);
+                for (int w = 0; w < 4; ++w) {
+                    if constexpr (Split<DT>::on) {
+                        const u32x2 hl = pack_split_bf16(ds[2 * w], ds[2 * w + 1]);
+                        sf[ks][w] = hl[0];
+                        sl[ks][w] = hl[1];
+                    } else {
+                        sf[ks][w] = pack2<DT>(ds[2 * w], ds[2 * w + 1]);
+                    }
+                }
             }
 #pragma unroll
             for (int ks = 0; ks < PKS; ++ks) {
@@ -370,7 +398,9 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
                         const int d = db * 32 + tcol;
                         v[tt] = ld_lds_tr(kt + row * ROWB + (((d >> 3) ^ swz<D>(row)) << 4) + (d & 7) * 2);
                     }
-                    dq[db] = mfma32<DT>(u32x4{v[0][0], v[0][1], v[1][0], v[1][1]}, sf[ks], dq[db]);
+                    const u32x4 a = {v[0][0], v[0][1], v[1][0], v[1][1]};
+                    dq[db] = mfma32<DT>(a, sf[ks], dq[db]);
+                    if constexpr (Split<DT>::on) dq[db] = mfma32<DT>(a, sl[ks], dq[db]);
                 }
             }
         }

@@ -74,6 +74,22 @@ __device__ __forceinline__ float dot2_ones(uint32_t w, float acc) {
     }
 }
 
+// bf16 keeps 8 significant bits, too few for the probabilities P and dS that feed the
+// second GEMM of each pair at the stated tolerance.  In bf16 mode they are therefore split
+// into hi = bf16(x) and lo = bf16(x - hi) and both halves go through the MFMA (same A
+// operand), which carries ~16 significant bits; fp16 (11 bits) needs no split.
+template <int DT>
+struct Split {
+    static constexpr bool on = DT == DT_BF16;
+    static constexpr int n = on ? 1 : 0;
+};
+// Returns {hi, lo}, each two packed bf16 values.
+__device__ __forceinline__ u32x2 pack_split_bf16(float x, float y) {
+    const uint32_t hi = pack2<DT_BF16>(x, y);
+    const float xh = __uint_as_float(hi << 16), yh = __uint_as_float(hi & 0xffff0000u);
+    return u32x2{hi, pack2<DT_BF16>(x - xh, y - yh)};
+}
+
 template <int DT>
 __device__ __forceinline__ float to_f32(uint16_t bits) {
     if constexpr (DT == DT_F16) return (float)__builtin_bit_cast(_Float16, bits);

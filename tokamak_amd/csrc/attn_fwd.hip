@@ -160,7 +160,7 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
                 m = mnew;
             }
             const float msub = (m == -INFINITY) ? 0.0f : m;
-            u32x4 pf[PKS];
+            u32x4 pf[PKS], pl[Split<DT>::on ? PKS : 1];
 #pragma unroll
             for (int ks = 0; ks < PKS; ++ks) {
                 const int kb = ks >> 1, r0 = (ks & 1) * 8;
@@ -168,9 +168,16 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
                 for (int w = 0; w < 4; ++w) {
                     const float p0 = fast_exp2(__builtin_fmaf(s[kb][r0 + 2 * w], sl2, -msub));
                     const float p1 = fast_exp2(__builtin_fmaf(s[kb][r0 + 2 * w + 1], sl2, -msub));
-                    const uint32_t pw = pack2<DT>(p0, p1);
-                    pf[ks][w] = pw;
-                    lsum = dot2_ones<DT>(pw, lsum);
+                    if constexpr (Split<DT>::on) {
+                        const u32x2 hl = pack_split_bf16(p0, p1);
+                        pf[ks][w] = hl[0];
+                        pl[ks][w] = hl[1];
+                        lsum = dot2_ones<DT>(hl[1], dot2_ones<DT>(hl[0], lsum));
+                    } else {
+                        const uint32_t pw = pack2<DT>(p0, p1);
+                        pf[ks][w] = pw;
+                        lsum = dot2_ones<DT>(pw, lsum);
+                    }
                 }
             }
 
@@ -188,6 +195,7 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
                     }
                     const u32x4 a = {v[0][0], v[0][1], v[1][0], v[1][1]};
                     o[db] = mfma32<DT>(a, pf[ks], o[db]);
+                    if constexpr (Split<DT>::on) o[db] = mfma32<DT>(a, pl[ks], o[db]);
                 }
             }
         }
