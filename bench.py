@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="threads for the CPU baseline (default: min(16, online CPUs))")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="also run one plain device copy of this many MiB (calibrates the "
+                         "FETCH_SIZE / WRITE_SIZE counters of a profiling run)")
     return ap.parse_args()
 
 
@@ -106,6 +109,14 @@ def main():
             stages.append((name, (lambda st=st: attn.gqa_bwd(
                 qkv, o, dout, lse, B, S, Hq, Hkv, D, causal, kvl, dqkv=dqkv, workspace=ws,
                 stage=st))))
+
+    if args.copy_mib:
+        src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     for _ in range(args.warmup):
         for _, fn in stages:

@@ -82,3 +82,40 @@ def test_deterministic(gpu):
         outs.append((o.clone(), lse.clone(), d.clone()))
     for a, b in zip(outs[0], outs[1]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_growing_scores_redo_path(gpu, causal, dtype):
+    """Scores that grow by ~40 nats along the keys: the max from the first tile is stale by
+    far more than the 16-bit range, P overflows and the workgroup recomputes its rows with
+    the exact row max.  Must still match the oracle."""
+    import torch
+    from tokamak_amd import attn
+    B, S, H, D = 1, 700, 2, 128
+    rng = np.random.default_rng(7)
+    u = rng.standard_normal(D)
+    u /= np.linalg.norm(u)
+    x = np.zeros((B, S, 3 * H, D), dtype=np.float32)
+    ramp = np.linspace(0.0, 1.0, S)
+    for h in range(H):
+        x[0, :, h] = 8.0 * u + 0.3 * rng.standard_normal((S, D))                      # Q
+        x[0, :, H + h] = (ramp[:, None] * 40.0 * np.sqrt(D) / 8.0) * u \
+            + 0.3 * rng.standard_normal((S, D))                                        # K
+        x[0, :, 2 * H + h] = rng.standard_normal((S, D))                               # V
+    qkv_r, bits = oracle.round_to(x.reshape(B, S, -1), dtype)
+    log(f"[case] growing scores S{S} {dtype} causal={int(causal)}")
+    qkv = to_device(bits, dtype, gpu)
+    o, lse = attn.gqa_fwd(qkv, B, S, H, H, D, causal=causal)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = oracle.fwd(qkv_r, B, S, H, H, D, causal=causal, f64=True)
+    # the growth is real: some row's max score exceeds its max over keys 0..63 by > 20 nats
+    xs = qkv_r.reshape(B, S, 3 * H, D).astype(np.float64)
+    sc = np.einsum("sd,td->st", xs[0, :, 0], xs[0, :, H]) / np.sqrt(D)
+    if causal:
+        sc = np.where(np.tril(np.ones((S, S), dtype=bool)), sc, -np.inf)
+    assert float((sc.max(axis=1) - sc[:, :64].max(axis=1)).max()) > 20.0
+    res = [compare("O", from_device(o), o_ref, TOL_FWD), compare("LSE", from_device(lse), lse_ref, TOL_FWD)]
+    for st in res:
+        log(f"    {st['name']}: max_abs={st['max_abs']:.3e} bad={st['n_bad']}")
+    _assert_ok(res)

@@ -124,7 +124,7 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
         const int iters = g * nq;
 
         const int dma_r = lane / CPR, dma_p = lane % CPR;
-        auto issue = [&](int it, int buf) {
+        auto issue = [&](int it, int buf) __attribute__((always_inline)) {
             const int h = kvh * g + it / nq, qr0 = (qt_begin + it % nq) * BM;
             const uint32_t rows = (uint32_t)min(BM, S - qr0);
             const auto rq = make_rsrc(bqkv + (size_t)qr0 * ld + (size_t)h * D, rows * ldb);
@@ -315,7 +315,7 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
     const int ntiles = (kv_end + BN - 1) / BN;
 
     const int dma_r = lane / CPR, dma_p = lane % CPR;
-    auto issue = [&](int t, int buf) {
+    auto issue = [&](int t, int buf) __attribute__((always_inline)) {
         const int k0 = t * BN;
         const uint32_t bytes = (uint32_t)min(BN, kv_end - k0) * ldb;
         const auto rk = make_rsrc(Kb + (size_t)k0 * ldb, bytes);

@@ -90,6 +90,11 @@ __device__ __forceinline__ u32x2 pack_split_bf16(float x, float y) {
     return u32x2{hi, pack2<DT_BF16>(x - xh, y - yh)};
 }
 
+// Reinterpret one 32-bit word as two fp16.  The word is taken by value on purpose: with
+// this toolchain, __builtin_bit_cast applied directly to an ext-vector element lvalue
+// (v[i]) reads element 0's storage, so element words must be copied out first.
+__device__ __forceinline__ f16x2 as_f16x2(uint32_t w) { return __builtin_bit_cast(f16x2, w); }
+
 template <int DT>
 __device__ __forceinline__ float to_f32(uint16_t bits) {
     if constexpr (DT == DT_F16) return (float)__builtin_bit_cast(_Float16, bits);
@@ -126,6 +131,41 @@ __device__ __forceinline__ float half_max(float x) {
 __device__ __forceinline__ float half_sum(float x) {
     const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// ---------------------------------------------------------------------------
+// Instruction-schedule shaping (LLVM sched_group_barrier masks).  A stage that reads N LDS
+// operands and issues M MFMAs per read is ordered as: LEAD reads, then (M MFMAs, 1 read)
+// repeated, then the remaining MFMAs, so only LEAD reads are in flight ahead of the MFMAs
+// that consume them (bounds register pressure; without it the compiler hoists every read).
+enum : unsigned { SG_MFMA = 0x008, SG_VALU = 0x002, SG_DS_READ = 0x100, SG_TRANS = 0x400 };
+template <int N, int M, int LEAD, int READS_PER_STEP = 1>
+__device__ __forceinline__ void sched_reads_mfma() {
+    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, LEAD * READS_PER_STEP, 0);
+#pragma unroll
+    for (int i = 0; i < N - LEAD; ++i) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, M, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, READS_PER_STEP, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, M * LEAD, 0);
+}
+
+// Steady-state block of a software-pipelined attention loop: NM MFMAs, ND LDS operand reads
+// and NE exp2 (plus ~2 other VALU each).  Order: a batch of reads first, then per MFMA one
+// exp, two VALU and one or two reads, so the transcendentals sit between MFMAs of the same
+// wave (on gfx950 they overlap with MFMA only within a wave) and reads run ahead of use.
+template <int NM, int ND, int NE>
+__device__ __forceinline__ void sched_steady() {
+    constexpr int LEAD = 8;
+    constexpr int REST = ND - LEAD;
+    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, LEAD, 0);
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        if (i < NE) __builtin_amdgcn_sched_group_barrier(SG_TRANS, (NE + NM - 1) / NM, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_VALU, 2, 0);
+        if (i < REST) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, (REST + NM - 1) / NM, 0);
+    }
 }
 
 // ---------------------------------------------------------------------------

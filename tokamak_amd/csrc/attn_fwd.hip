@@ -7,34 +7,60 @@
 //   (!causal || j <= i).
 //
 // Work decomposition: one workgroup = 4 waves = one (batch, q-head, block of 128 query
-// rows); two workgroups share a CU (2 waves per SIMD), so one wave's softmax overlaps the
-// other's MFMAs.  Each wave keeps its 32 query rows of Q in registers and walks the key
-// range in tiles of 64 keys.  K and V tiles go HBM -> LDS by buffer DMA (no registers, rows
-// past the valid range read as zero), double-buffered: the DMA of tile t+1 is in flight
-// while tile t is consumed.  Tiles are stored row-major with an XOR chunk swizzle.
+// rows); two workgroups share a CU (2 waves per SIMD).  Each wave keeps its 32 query rows
+// of Q in registers and walks the key range in tiles of 64 keys that the workgroup moves
+// HBM -> LDS by buffer DMA (rows past the valid range read as zero), stored row-major with
+// an XOR chunk swizzle.
 //
 // Per tile and wave:
-//   S^T = K Q^T        32 keys x 32 queries per MFMA block; lane = query row, so the row
-//                      max is an in-register max plus one swap between lane halves.
-//   P^T = exp2(S^T * scale*log2e - m), m = running row max in the same units; the row sum
-//                      is accumulated per lane (fp32 dot of the rounded P) and the halves
-//                      are combined once at the end.  m (and O) is only rescaled when the
-//                      max grows by more than 8, so P <= 256 stays exact in fp16/bf16.
+//   S^T = K Q^T        32 keys x 32 queries per MFMA block; lane = query row.
+//   P^T = exp2(S^T * scale*log2e - m) with m the running row max (log2 units); the row sum
+//                      is an fp32 dot of the rounded P per lane, lane halves combined at the
+//                      end.
 //   O^T += V^T P^T     the P^T accumulator, rounded to 16 bits, is the B operand in place;
 //                      V^T comes from the row-major V tile through ds_read_b64_tr_b16.
-// Causal: tiles above the diagonal are neither loaded nor computed, only tiles crossing the
+//
+// Tiles are double-buffered: the DMA of tile t+1 is in flight while tile t is consumed;
+// the loop is unrolled by two so every LDS address is a per-lane constant plus an
+// immediate.  The two waves of a SIMD (different workgroups) overlap each other's softmax
+// with MFMAs.
+//
+// fp16: Q is multiplied by scale*log2e once (per element, rounded to fp16) and the S
+// accumulator starts at -m, so P = exp2(acc) needs no further arithmetic.  m is set from
+// the first tile and never moved: rows whose max later grows beyond the 16-bit range (an
+// overflowing P, i.e. a growth of more than 2^15 for fp16) make the workgroup redo its rows
+// with the exact row max from an extra pass.  bf16 keeps Q unscaled (its 8-bit mantissa
+// would perturb the scores) and applies scale and -m with one FMA per score.
+// Causal: tiles above the diagonal are neither loaded nor computed, tiles crossing the
 // diagonal (or the kv_len / S edge) are masked, heaviest query blocks are launched first.
+#include <type_traits>
+
 #include "attn_common.h"
 #include "attn_launch.h"
 
+#ifndef FWD_QB
+#define FWD_QB 1
+#endif
+#ifndef FWD_LEAD
+#define FWD_LEAD 2  // LDS operand reads in flight ahead of their MFMAs
+#endif
+
 namespace tkm {
 
-template <int D, int DT>
+template <int D, int DT, int QB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
                    float* __restrict__ lse, const int32_t* __restrict__ kv_len, int B, int S,
                    int Hq, int Hkv, float sl2, int causal, int n_qblk) {
-    constexpr int BM = 128, BN = 64;
+#ifdef TKM_DEBUG_NO_PRE
+    constexpr bool PRE = false;
+#else
+    constexpr bool PRE = (DT == DT_F16);  // scale folded into Q, -m into the accumulator
+#endif
+    constexpr bool SPL = Split<DT>::on;   // bf16: P as hi + lo
+    constexpr int NW = 4;                 // waves per workgroup (two workgroups per CU)
+    constexpr int WR = 32 * QB;           // query rows per wave
+    constexpr int BM = NW * WR, BN = 64;
     constexpr int KS = D / 16;    // k-steps over the head dim (S^T)
     constexpr int NKB = BN / 32;  // 32-key blocks per tile
     constexpr int NDB = D / 32;   // 32-wide head-dim blocks of O
@@ -42,9 +68,11 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
     constexpr int ROWB = D * 2;   // bytes per tile row in LDS
     constexpr int CPR = D / 8;    // 16-byte chunks per row
     constexpr int TILEB = BN * ROWB;
-    constexpr int RPI = 64 / CPR;       // rows per DMA instruction (64 lanes x 16 bytes)
-    constexpr int NI = BN / RPI / 4;    // DMA instructions per wave, per tile and tensor
-    __shared__ __attribute__((aligned(1024))) char smem[2][2][TILEB];  // [buffer][K, V]
+    constexpr int RPI = 64 / CPR;     // rows per DMA instruction (64 lanes x 16 bytes)
+    constexpr int NI = BN / RPI / NW;  // DMA instructions per wave, per tile and tensor
+    constexpr int NL = SPL ? PKS : 1;
+    __shared__ __attribute__((aligned(1024))) char smem[2][2][TILEB];  // [K, V][buffer]
+    __shared__ int redo;  // set when a P overflowed: recompute with the exact row max
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -65,168 +93,322 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
         kvl = kvl < 0 ? 0 : (kvl > S ? S : kvl);
     }
 
-    const int q0 = qblk * BM + wave * 32;  // first query row of this wave
-    const int q = q0 + l32;
-    u32x4 qf[KS];
-    {
+    const int q0 = qblk * BM + wave * WR;  // first query row of this wave
+    u32x4 qf[QB][KS];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const int q = q0 + qb * 32 + l32;
         const uint16_t* qp = bqkv + (size_t)q * ld + (size_t)h * D + hi * 8;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-            qf[ks] = q < S ? ld_global16(qp + ks * 16) : u32x4{0u, 0u, 0u, 0u};
+        for (int ks = 0; ks < KS; ++ks) {
+            const u32x4 raw = q < S ? ld_global16(qp + ks * 16) : u32x4{0u, 0u, 0u, 0u};
+            if constexpr (PRE) {
+                const f16x2 x0 = as_f16x2(raw[0]), x1 = as_f16x2(raw[1]);
+                const f16x2 x2 = as_f16x2(raw[2]), x3 = as_f16x2(raw[3]);
+                qf[qb][ks] = u32x4{pack2<DT>((float)x0[0] * sl2, (float)x0[1] * sl2),
+                                   pack2<DT>((float)x1[0] * sl2, (float)x1[1] * sl2),
+                                   pack2<DT>((float)x2[0] * sl2, (float)x2[1] * sl2),
+                                   pack2<DT>((float)x3[0] * sl2, (float)x3[1] * sl2)};
+            } else {
+                qf[qb][ks] = raw;
+            }
+        }
     }
 
     int kv_end = kvl;
     if (causal) kv_end = min(kv_end, qblk * BM + BM);
     const int ntiles = (kv_end + BN - 1) / BN;
+    // tiles [0, n_plain) need no mask for any row of this wave
+    const int n_plain = min(kvl / BN, causal ? (q0 + 1) / BN : ntiles);
+    // tiles [0, n_act) hold at least one key visible to this wave
+    const int n_act = causal ? min(ntiles, (q0 + WR - 1) / BN + 1) : ntiles;
 
-    // DMA geometry of this lane: row dma_r of each RPI-row group, LDS slot dma_p.
+    // DMA of one tile (tensor 0 = K, 1 = V) into buffer buf: wave w moves rows
+    // [w*NI*RPI, (w+1)*NI*RPI) of the BN-row tile.
     const int dma_r = lane / CPR, dma_p = lane % CPR;
-    auto issue = [&](int t, int buf) {
+    auto issue = [&](int t, int tensor, int buf) __attribute__((always_inline)) {
         const int k0 = t * BN;
-        const uint32_t bytes = (uint32_t)min(BN, kv_end - k0) * ldb;
-        const auto rk = make_rsrc(Kb + (size_t)k0 * ldb, bytes);
-        const auto rv = make_rsrc(Vb + (size_t)k0 * ldb, bytes);
+        const auto r = make_rsrc((tensor ? Vb : Kb) + (size_t)k0 * ldb,
+                                 (uint32_t)min(BN, kv_end - k0) * ldb);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const int r0 = (wave * NI + i) * RPI, r = r0 + dma_r;
-            const uint32_t voff = (uint32_t)r * ldb + (uint32_t)((dma_p ^ swz<D>(r)) << 4);
-            dma16(rk, &smem[buf][0][r0 * ROWB], voff);
-            dma16(rv, &smem[buf][1][r0 * ROWB], voff);
+            const int r0 = (wave * NI + i) * RPI, row = r0 + dma_r;
+            dma16(r, &smem[tensor][buf][r0 * ROWB],
+                  (uint32_t)row * ldb + (uint32_t)((dma_p ^ swz<D>(row)) << 4));
         }
     };
 
-    // LDS read geometry.  K (A operand of S^T): row kb*32 + l32, chunk ks*2 + hi.
+    // Per-lane LDS offsets.  K (A operand of S^T): row kb*32 + l32, chunk ks*2 + hi.
+    int koff[KS];
     const int fk = swz<D>(l32);
-    // V^T (A operand of PV) via transposed reads: row-in-block trow, column tcol of the
-    // 32-wide head-dim block.
-    const int trow = (lane & 15) >> 2;
-    const int tcol = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
-
-    f32x16 o[NDB];
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) o[db] = f32x16{};
-    float m = -INFINITY, lsum = 0.f;
+    for (int ks = 0; ks < KS; ++ks) koff[ks] = l32 * ROWB + (((ks * 2 + hi) ^ fk) << 4);
+    // V^T (A operand of PV) by transposed reads: rows ks*16 + tt*8 + hi*4 + trow, columns
+    // db*32 + tcol; the swizzle depends on the row only through tt (ks*16 keeps row & 15).
+    int voff[2][NDB];
+    {
+        const int trow = (lane & 15) >> 2;
+        const int tcol = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int row = tt * 8 + hi * 4 + trow;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const int d = db * 32 + tcol;
+                voff[tt][db] = row * ROWB + (((d >> 3) ^ swz<D>(row)) << 4) + (d & 7) * 2;
+            }
+        }
+    }
 
-    if (ntiles > 0) issue(0, 0);
-    wait_dma();
-    __syncthreads();
+    f32x16 o[NDB][QB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) o[db][qb] = f32x16{};
+    float m[QB], lsum[QB];      // m: running max (log2 units) once tile 0 is done
+    f32x16 cinit[QB];           // PRE: -m in every element (S accumulator init)
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        m[qb] = 0.f;
+        lsum[qb] = 0.f;
+        cinit[qb] = f32x16{};
+    }
+    f32x16 sr[1][NKB][QB];  // scores of the current tile
+    u32x4 pr[1][QB][PKS];   // its P (hi part for bf16)
+    u32x4 plr[1][QB][NL];   // bf16: lo part
 
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    // S(tile) into register set J: S^T = K Q^T (+ cinit = -m for PRE).
+    auto stage_s = [&](const char* kt, auto Jc) __attribute__((always_inline)) {
+        constexpr int J = decltype(Jc)::value;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                const u32x4 a = ld_lds16((const uint16_t*)(kt + kb * 32 * ROWB + koff[ks]));
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb)
+                    sr[J][kb][qb] = mfma32<DT>(a, qf[qb][ks], ks == 0 ? cinit[qb] : sr[J][kb][qb]);
+            }
+    };
+    auto stage_mask = [&](int t, auto Jc) __attribute__((always_inline)) {
+        constexpr int J = decltype(Jc)::value;
         const int k0 = t * BN;
-        if (t + 1 < ntiles) issue(t + 1, buf ^ 1);
-        const bool active = !causal || (k0 <= q0 + 31);
-        if (active) {
-            const char* kt = smem[buf][0];
-            const char* vt = smem[buf][1];
-            f32x16 s[NKB];
 #pragma unroll
-            for (int kb = 0; kb < NKB; ++kb) s[kb] = f32x16{};
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-                for (int kb = 0; kb < NKB; ++kb) {
-                    const u32x4 a = ld_lds16((const uint16_t*)(kt + (kb * 32 + l32) * ROWB +
-                                                               (((ks * 2 + hi) ^ fk) << 4)));
-                    s[kb] = mfma32<DT>(a, qf[ks], s[kb]);
-                }
-            }
-
-            // online softmax (lane = query row q; registers = keys)
-            const bool need_mask = (causal && k0 + BN - 1 > q0) || (k0 + BN > kvl);
-            if (need_mask) {
-#pragma unroll
-                for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = k0 + kb * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-                        if (key >= kvl || (causal && key > q)) s[kb][r] = -INFINITY;
-                    }
-            }
-            float mx = s[0][0];
+        for (int qb = 0; qb < QB; ++qb) {
+            const int q = q0 + qb * 32 + l32;
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-                for (int r = (kb == 0 ? 1 : 0); r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-            mx = half_max(mx) * sl2;  // scale > 0: max commutes with the scaling
-            const float mnew = fmaxf(m, mx);
-            if (__any(mnew > m + 8.0f)) {
-                const float alpha = (mnew == -INFINITY) ? 1.0f : fast_exp2(m - mnew);
+                for (int r = 0; r < 16; ++r) {
+                    const int key = k0 + kb * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
+                    if (key >= kvl || (causal && key > q)) sr[J][kb][qb][r] = -INFINITY;
+                }
+        }
+    };
+    // exp2 of the scores in set J (relative to mm[qb]), packed to 16 bits into P set J;
+    // lt[qb] = the lane's fp32 sum of the packed values.  PRE: scores are S*c - m already.
+    auto stage_exp = [&](auto Jc, const float (&mm)[QB], float (&lt)[QB]) __attribute__((always_inline)) {
+        constexpr int J = decltype(Jc)::value;
 #pragma unroll
-                for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-                lsum *= alpha;
-                m = mnew;
-            }
-            const float msub = (m == -INFINITY) ? 0.0f : m;
-            u32x4 pf[PKS], pl[Split<DT>::on ? PKS : 1];
+        for (int qb = 0; qb < QB; ++qb) {
+            lt[qb] = 0.f;
 #pragma unroll
             for (int ks = 0; ks < PKS; ++ks) {
                 const int kb = ks >> 1, r0 = (ks & 1) * 8;
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
-                    const float p0 = fast_exp2(__builtin_fmaf(s[kb][r0 + 2 * w], sl2, -msub));
-                    const float p1 = fast_exp2(__builtin_fmaf(s[kb][r0 + 2 * w + 1], sl2, -msub));
-                    if constexpr (Split<DT>::on) {
+                    float x0 = sr[J][kb][qb][r0 + 2 * w], x1 = sr[J][kb][qb][r0 + 2 * w + 1];
+                    if constexpr (PRE) {
+                        x0 -= mm[qb];
+                        x1 -= mm[qb];
+                    } else {
+                        x0 = __builtin_fmaf(x0, sl2, -mm[qb]);
+                        x1 = __builtin_fmaf(x1, sl2, -mm[qb]);
+                    }
+                    const float p0 = fast_exp2(x0), p1 = fast_exp2(x1);
+                    if constexpr (SPL) {
                         const u32x2 hl = pack_split_bf16(p0, p1);
-                        pf[ks][w] = hl[0];
-                        pl[ks][w] = hl[1];
-                        lsum = dot2_ones<DT>(hl[1], dot2_ones<DT>(hl[0], lsum));
+                        pr[J][qb][ks][w] = hl[0];
+                        plr[J][qb][ks][w] = hl[1];
+                        lt[qb] = dot2_ones<DT>(hl[1], dot2_ones<DT>(hl[0], lt[qb]));
                     } else {
                         const uint32_t pw = pack2<DT>(p0, p1);
-                        pf[ks][w] = pw;
-                        lsum = dot2_ones<DT>(pw, lsum);
+                        pr[J][qb][ks][w] = pw;
+                        lt[qb] = dot2_ones<DT>(pw, lt[qb]);
                     }
-                }
-            }
-
-            // O^T += V^T P^T
-#pragma unroll
-            for (int ks = 0; ks < PKS; ++ks) {
-#pragma unroll
-                for (int db = 0; db < NDB; ++db) {
-                    u32x2 v[2];
-#pragma unroll
-                    for (int tt = 0; tt < 2; ++tt) {
-                        const int key = ks * 16 + tt * 8 + hi * 4 + trow;
-                        const int d = db * 32 + tcol;
-                        v[tt] = ld_lds_tr(vt + key * ROWB + ((((d >> 3) ^ swz<D>(key))) << 4) + (d & 7) * 2);
-                    }
-                    const u32x4 a = {v[0][0], v[0][1], v[1][0], v[1][1]};
-                    o[db] = mfma32<DT>(a, pf[ks], o[db]);
-                    if constexpr (Split<DT>::on) o[db] = mfma32<DT>(a, pl[ks], o[db]);
                 }
             }
         }
+    };
+    // O^T += V^T P^T with P set J.
+    auto stage_pv = [&](const char* vt, auto Jc) __attribute__((always_inline)) {
+        constexpr int J = decltype(Jc)::value;
+#pragma unroll
+        for (int ks = 0; ks < PKS; ++ks)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const u32x2 v0 = ld_lds_tr(vt + ks * 16 * ROWB + voff[0][db]);
+                const u32x2 v1 = ld_lds_tr(vt + ks * 16 * ROWB + voff[1][db]);
+                const u32x4 a = {v0[0], v0[1], v1[0], v1[1]};
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    o[db][qb] = mfma32<DT>(a, pr[J][qb][ks], o[db][qb]);
+                    if constexpr (SPL) o[db][qb] = mfma32<DT>(a, plr[J][qb][ks], o[db][qb]);
+                }
+            }
+    };
+    auto row_max = [&](auto Jc, float (&mx)[QB]) __attribute__((always_inline)) {
+        constexpr int J = decltype(Jc)::value;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            float v = sr[J][0][qb][0];
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int r = (kb == 0 ? 1 : 0); r < 16; ++r) v = fmaxf(v, sr[J][kb][qb][r]);
+            mx[qb] = half_max(v);
+        }
+    };
+    auto set_cinit = [&]() __attribute__((always_inline)) {
+        if constexpr (PRE) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) cinit[qb][r] = -m[qb];
+        }
+    };
+    // Tile 0 (scores relative to 0: cinit is still 0): establishes m, which then stays fixed.
+    auto softmax_first = [&](auto Jc) __attribute__((always_inline)) {
+        float mx[QB];
+        row_max(Jc, mx);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            const float v = PRE ? mx[qb] : mx[qb] * sl2;
+            m[qb] = (v == -INFINITY) ? 0.f : v;
+        }
+        stage_exp(Jc, m, lsum);
+        set_cinit();
+    };
+    // Later tiles, against the fixed m.  An overflowing P (the row max grew beyond the
+    // 16-bit range) cannot be repaired in place without keeping O in VALU-addressable
+    // registers; the wave flags the workgroup instead, which redoes its rows with the exact
+    // row max (below).  lsum is not used once the flag is set.
+    auto softmax_next = [&](auto Jc) __attribute__((always_inline)) {
+        float lt[QB], mm[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) mm[qb] = PRE ? 0.f : m[qb];
+        stage_exp(Jc, mm, lt);
+        bool bad = false;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            bad |= !(lt[qb] < INFINITY);
+            lsum[qb] += lt[qb];
+        }
+        return bad;
+    };
+
+    // Tile loop.  Tile t: S(t), softmax, PV(t), with the DMA of K(t+1) and V(t+1) in flight
+    // into the other buffers (K(j), V(j) live in buffers j&1).  The loop is unrolled by two
+    // so buffer indices are constants.  The two waves sharing a SIMD (different workgroups)
+    // overlap each other's phases.
+    auto iteration = [&](auto Pc, int t, bool fixed) __attribute__((always_inline)) {
+        constexpr int P = decltype(Pc)::value;  // = t & 1
+        if (t + 1 < ntiles) {
+            issue(t + 1, 0, P ^ 1);
+            issue(t + 1, 1, P ^ 1);
+        }
+        if (t < n_act) {
+            stage_s(smem[0][P], I0{});
+            if (t >= n_plain) stage_mask(t, I0{});
+            bool bad = false;
+            if (t == 0 && !fixed) softmax_first(I0{});
+            else bad = softmax_next(I0{});
+            if (__any(bad) && lane == 0) redo = 1;
+            stage_pv(smem[1][P], I0{});
+        }
         wait_dma();
         __syncthreads();
+    };
+    auto main_loop = [&](bool fixed) __attribute__((always_inline)) {
+        if (ntiles > 0) {
+            issue(0, 0, 0);
+            issue(0, 1, 0);
+        }
+        wait_dma();
+        __syncthreads();
+        for (int t = 0; t < ntiles; t += 2) {
+            iteration(I0{}, t, fixed);
+            if (t + 1 < ntiles) iteration(I1{}, t + 1, fixed);
+        }
+    };
+
+    if (tid == 0) redo = 0;
+    main_loop(false);
+    if (redo) {
+        // Exact path (rare): pass 1 computes the row max over all visible keys, pass 2
+        // repeats the main loop with m fixed to it (every P <= 1, nothing can overflow).
+        float mx[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            mx[qb] = -INFINITY;
+            cinit[qb] = f32x16{};
+        }
+        for (int t = 0; t < ntiles; ++t) {
+            issue(t, 0, 0);
+            wait_dma();
+            __syncthreads();
+            if (t < n_act) {
+                stage_s(smem[0][0], I0{});
+                if (t >= n_plain) stage_mask(t, I0{});
+                float tm[QB];
+                row_max(I0{}, tm);
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) mx[qb] = fmaxf(mx[qb], PRE ? tm[qb] : tm[qb] * sl2);
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            m[qb] = (mx[qb] == -INFINITY) ? 0.f : mx[qb];
+            lsum[qb] = 0.f;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) o[db][qb] = f32x16{};
+        }
+        set_cinit();
+        main_loop(true);
     }
 
-    const float l = half_sum(lsum);
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
-    if (q < S) {
-        uint16_t* orow = out + ((size_t)b * S + q) * ((size_t)Hq * D) + (size_t)h * D;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+    for (int qb = 0; qb < QB; ++qb) {
+        const float l = half_sum(lsum[qb]);
+        const float inv = l > 0.f ? 1.0f / l : 0.f;
+        const int q = q0 + qb * 32 + l32;
+        if (q < S) {
+            uint16_t* orow = out + ((size_t)b * S + q) * ((size_t)Hq * D) + (size_t)h * D;
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-                u32x2 w = {pack2<DT>(o[db][g4 * 4 + 0] * inv, o[db][g4 * 4 + 1] * inv),
-                           pack2<DT>(o[db][g4 * 4 + 2] * inv, o[db][g4 * 4 + 3] * inv)};
-                *reinterpret_cast<u32x2*>(orow + db * 32 + g4 * 8 + hi * 4) = w;
-            }
-        if (lse && hi == 0)
-            lse[((size_t)b * Hq + h) * S + q] =
-                l > 0.f ? (m + __log2f(l)) * 0.69314718055994530942f : -INFINITY;
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    u32x2 w = {pack2<DT>(o[db][qb][g4 * 4 + 0] * inv, o[db][qb][g4 * 4 + 1] * inv),
+                               pack2<DT>(o[db][qb][g4 * 4 + 2] * inv, o[db][qb][g4 * 4 + 3] * inv)};
+                    *reinterpret_cast<u32x2*>(orow + db * 32 + g4 * 8 + hi * 4) = w;
+                }
+            if (lse && hi == 0)
+                lse[((size_t)b * Hq + h) * S + q] =
+                    l > 0.f ? (m[qb] + __log2f(l)) * 0.69314718055994530942f : -INFINITY;
+        }
     }
 }
 
 template <int D, int DT>
 static int launch_fwd_t(const FwdArgs& a) {
-    constexpr int BM = 128;
+    constexpr int QB = FWD_QB;
+    constexpr int BM = 128 * QB;
     const int n_qblk = (a.S + BM - 1) / BM;
     dim3 grid((unsigned)(a.B * a.Hq * n_qblk)), block(256);
-    hipLaunchKernelGGL((fa_fwd_kernel<D, DT>), grid, block, 0, (hipStream_t)a.stream,
+    hipLaunchKernelGGL((fa_fwd_kernel<D, DT, QB>), grid, block, 0, (hipStream_t)a.stream,
                        (const uint16_t*)a.qkv, (uint16_t*)a.o, a.lse, a.kv_len, a.B, a.S, a.Hq,
                        a.Hkv, a.scale * 1.4426950408889634f, a.causal, n_qblk);
     return hipGetLastError() == hipSuccess ? 0 : -1;
