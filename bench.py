@@ -50,29 +50,46 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(cfg, threads):
-    """Time the CPU oracle on a bounded sample: the workload restricted to its first
-    batch and at most 4 heads (all S x S positions), forward + backward, fp32."""
+def cpu_baseline(cfg, threads, max_heads):
+    """Time the CPU oracle (fp32, OpenMP) on a bounded sample of the same workload: all
+    batches and S x S positions of the first max_heads heads (the whole workload when Hq
+    <= max_heads), forward + backward, once."""
     import numpy as np
 
     import oracle
     B, S, Hq, Hkv, D, causal, kv_len, backward, mul = cfg
-    hs = min(Hq, 4)
-    kvl = None if kv_len is None else kv_len[:1]
+    hs = min(Hq, max_heads)
     oracle.set_threads(threads)
-    inp = oracle.make_inputs(1, S, hs, hs, D, "f16", mul=mul, with_dout=backward)
+    inp = oracle.make_inputs(B, S, hs, hs, D, "f16", mul=mul, with_dout=backward)
     t0 = time.perf_counter()
-    o, lse = oracle.fwd(inp["qkv"], 1, S, hs, hs, D, causal=causal, kv_len=kvl)
+    o, lse = oracle.fwd(inp["qkv"], B, S, hs, hs, D, causal=causal, kv_len=kv_len)
     if backward:
-        oracle.bwd(inp["qkv"], o, inp["dout"], lse, 1, S, hs, hs, D, causal=causal, kv_len=kvl)
+        oracle.bwd(inp["qkv"], o, inp["dout"], lse, B, S, hs, hs, D, causal=causal, kv_len=kv_len)
     dt = time.perf_counter() - t0
-    skv = S if kvl is None else float(np.mean(kvl))
-    f = 4.0 * 1 * hs * S * skv * D * (0.5 if causal else 1.0) * (3.5 if backward else 1.0)
+    skv = S if kv_len is None else float(np.mean(kv_len))
+    f = 4.0 * B * hs * S * skv * D * (0.5 if causal else 1.0) * (3.5 if backward else 1.0)
     return {"value": round(f / dt / 1e12, 6), "unit": "TFLOP/s", "cores": oracle.threads(),
             "kind": "port",
-            "sample": f"oracle/attn_ref.c fp32 {'fwd+bwd' if backward else 'fwd'} on B=1 H={hs} "
-                      f"S={S} D={D} causal={int(causal)} (1 batch, {hs} of {Hq} heads), "
-                      f"{dt:.2f} s wall"}
+            "sample": f"oracle/attn_ref.c fp32 {'fwd+bwd' if backward else 'fwd'} on B={B} "
+                      f"H={hs} of {Hq} S={S} D={D} causal={int(causal)}, "
+                      f"{f / 1e9:.1f} GFLOP in {dt:.2f} s wall"}
+
+
+def measured_traffic(name):
+    """HBM bytes per launch of a kernel at config 3, from the FETCH_SIZE / WRITE_SIZE counter
+    runs summarized in profiles/attn_cfg3_traffic.md (None if absent)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "attn_cfg3_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    for kv in line.split(":", 1)[1].split():
+                        k, v = kv.split("=")
+                        if k == name:
+                            return float(v)
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -168,12 +185,14 @@ def main():
     if dom in credit:
         ach = credit[dom] / (dom_avg * 1e-3) / 1e12
         roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(ach / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_FP16_TFLOPS, 4),
+                "traffic": measured_traffic(dom) if args.config == "cfg3" else None,
                 "avg_ms": round(dom_avg, 5), "flops_per_launch": credit[dom]}
     else:
         ach = delta_bytes / (dom_avg * 1e-3) / 1e9
         roof = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
-                "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4),
+                "traffic": measured_traffic(dom) if args.config == "cfg3" else None,
                 "avg_ms": round(dom_avg, 5)}
 
     value = f_total / (ms_step * 1e-3) / 1e12
@@ -204,7 +223,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        res["cpu_baseline"] = cpu_baseline(cfg, threads)
+        res["cpu_baseline"] = cpu_baseline(cfg, threads, 16 if args.config != "cfg5" else 1)
     print(json.dumps(res))
 
 
