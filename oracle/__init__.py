@@ -1,4 +1,5 @@
-"""ctypes wrapper of the CPU attention oracle (oracle/attn_ref.c).
+"""ctypes wrapper of the CPU oracles: attention (oracle/attn_ref.c) and the qkv-prep
+epilogue (oracle/qkv_prep_ref.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
 cpu_baseline leg of bench.py as the checker.  The product path
@@ -50,6 +51,13 @@ def lib():
         L.ar_set_threads.argtypes = [ctypes.c_int]
         L.ar_get_threads.restype = ctypes.c_int
         L.ar_online_cpus.restype = ctypes.c_int
+        _f64p = ctypes.POINTER(ctypes.c_double)
+        L.qp_round.argtypes = [ctypes.c_double, ctypes.c_int]
+        L.qp_round.restype = ctypes.c_double
+        L.qp_inv_freq.argtypes = [ctypes.c_float] * 5 + [ctypes.c_int, ctypes.c_int]
+        L.qp_inv_freq.restype = ctypes.c_float
+        L.qp_fwd.argtypes = [_f32p] * 4 + [ctypes.c_int] * 8 + [_f32p] * 3
+        L.qp_bwd.argtypes = [_f32p] * 6 + [ctypes.c_int] * 8 + [_f32p, _f64p, _f64p]
         _lib = L
     return _lib
 
@@ -163,3 +171,65 @@ def bwd(qkv, o, dout, lse, B, S, Hq, Hkv, D, scale=None, causal=True, kv_len=Non
     if rc != 0:
         raise ValueError("ar_attn_bwd rejected its arguments")
     return dqkv
+
+
+# ---- qkv-prep epilogue (oracle/qkv_prep_ref.c) -------------------------------------------
+
+PREP_DTYPES = {"f16": 0, "bf16": 1, "f32": 2}
+
+
+def _f32c(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _ptr(a, typ=_f32p):
+    return None if a is None else a.ctypes.data_as(typ)
+
+
+def prep_round(x: float, dtype: str) -> float:
+    return lib().qp_round(float(x), PREP_DTYPES[dtype])
+
+
+def prep_inv_freq(D, theta=10000.0, scale=1.0, low=1.0, high=4.0, ocl=8192.0) -> np.ndarray:
+    """fp32 RoPE inverse frequencies of pairs 0..D/2-1 (reference tkm_codegen.c:45-62)."""
+    L = lib()
+    return np.array([L.qp_inv_freq(theta, scale, low, high, ocl, D, i) for i in range(D // 2)],
+                    dtype=np.float32)
+
+
+def prep_fwd(x, bias, gamma, inv_freq, rows, S, Hq, Hkv, D, qknorm, rope, dtype="f16"):
+    """Returns (out [rows][C], xhat [rows][QK] or None, istd [rows][Hq+Hkv] or None), float32."""
+    C, QK, NH = (Hq + 2 * Hkv) * D, (Hq + Hkv) * D, Hq + Hkv
+    x, bias = _f32c(x).reshape(rows, C), _f32c(bias)
+    gamma = _f32c(gamma) if qknorm else None
+    inv_freq = _f32c(inv_freq) if rope else None
+    out = np.empty((rows, C), np.float32)
+    xhat = np.empty((rows, QK), np.float32) if qknorm else None
+    istd = np.empty((rows, NH), np.float32) if qknorm else None
+    rc = lib().qp_fwd(_ptr(x), _ptr(bias), _ptr(gamma), _ptr(inv_freq), rows, S, Hq, Hkv, D,
+                      int(qknorm), int(rope), PREP_DTYPES[dtype], _ptr(out), _ptr(xhat), _ptr(istd))
+    if rc:
+        raise ValueError("qp_fwd rejected its arguments")
+    return out, xhat, istd
+
+
+def prep_bwd(dout, xhat, istd, gamma, inv_freq, rows, S, Hq, Hkv, D, qknorm, rope, dtype="f16",
+             din_prev=None):
+    """Returns (din [rows][C] float32, dgamma [QK] float64 or None, dbias [C] float64)."""
+    C, QK = (Hq + 2 * Hkv) * D, (Hq + Hkv) * D
+    _f64p = ctypes.POINTER(ctypes.c_double)
+    dout = _f32c(dout).reshape(rows, C)
+    xhat = _f32c(xhat) if qknorm else None
+    istd = _f32c(istd) if qknorm else None
+    gamma = _f32c(gamma) if qknorm else None
+    inv_freq = _f32c(inv_freq) if rope else None
+    din_prev = None if din_prev is None else _f32c(din_prev).reshape(rows, C)
+    din = np.empty((rows, C), np.float32)
+    dgamma = np.empty(QK, np.float64) if qknorm else None
+    dbias = np.empty(C, np.float64)
+    rc = lib().qp_bwd(_ptr(dout), _ptr(xhat), _ptr(istd), _ptr(gamma), _ptr(inv_freq), _ptr(din_prev),
+                      rows, S, Hq, Hkv, D, int(qknorm), int(rope), PREP_DTYPES[dtype], _ptr(din),
+                      _ptr(dgamma, _f64p), _ptr(dbias, _f64p))
+    if rc:
+        raise ValueError("qp_bwd rejected its arguments")
+    return din, dgamma, dbias

@@ -25,8 +25,13 @@ def test_library_exports_header_functions():
     out = subprocess.run(["nm", "-D", "--defined-only", attn.LIB_PATH], capture_output=True, text=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
     assert set(names) <= exported
-    # nothing else with C linkage leaks out of the library
-    assert {e for e in exported if e.startswith("tkm_")} == set(names)
+    # nothing else with C linkage leaks out of the library: the exports are exactly the
+    # functions the two public headers declare
+    from tokamak_amd import prep
+    both = set(names) | set(prep.header_functions())
+    for n in both:
+        assert hasattr(L, n), n
+    assert {e for e in exported if e.startswith("tkm_")} == both
 
 
 def test_version_and_status_strings():

@@ -9,16 +9,15 @@
 
 #include "attn_launch.h"
 #include "tkm_attn.h"
+#include "tkm_prep_internal.h"
 
 namespace {
-
-thread_local char g_err[256] = "";
 
 int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int status, const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    tkm_vset_error(status, fmt, ap);
     va_end(ap);
     return status;
 }
@@ -141,11 +140,11 @@ TKM_ATTN_API const char* tkm_attn_status_string(int status) {
         case TKM_ATTN_EALIGN: return "misaligned pointer";
         case TKM_ATTN_EWORKSPACE: return "workspace missing or too small";
         case TKM_ATTN_ELAUNCH: return "kernel launch failed";
+        case TKM_ATTN_ECOMPILE: return "run-time compilation failed";
+        case TKM_ATTN_EDEVICE: return "device, module or graph error";
         default: return "unknown status";
     }
 }
-
-TKM_ATTN_API const char* tkm_attn_last_error(void) { return g_err; }
 
 TKM_ATTN_API int tkm_attn_version(void) { return 100; }
 

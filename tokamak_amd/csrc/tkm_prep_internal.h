@@ -1,0 +1,40 @@
+/* Internal declarations shared by the host sources of libtkm_attn.so (not installed). */
+#ifndef TKM_PREP_INTERNAL_H
+#define TKM_PREP_INTERNAL_H
+
+#include <stdarg.h>
+
+#include "tkm_prep.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TKM_HIDDEN __attribute__((visibility("hidden")))
+
+/* Records a formatted message as the calling thread's last error and returns status. */
+TKM_HIDDEN int tkm_set_error(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+TKM_HIDDEN int tkm_vset_error(int status, const char *fmt, va_list ap);
+
+/* Launch geometry of the generated qkv-prep kernels. */
+enum {
+    TKM_PREP_FWD_RPW = 4,          /* forward: rows per wave per block */
+    TKM_PREP_BWD_BATCH = 4,        /* backward: rows per wave loaded before the arithmetic */
+    TKM_PREP_BWD_MIN_BAND = 32,    /* backward: rows per block row, at least */
+    TKM_PREP_BWD_MAX_BANDS = 64    /* backward: block rows (= partial rows), at most */
+};
+
+typedef struct {
+    int D, C, QK, CH, QKCH, NH, G, part_width;
+} tkm_prep_geom;
+
+TKM_HIDDEN int tkm_prep_check_desc(const tkm_prep_desc *d);
+TKM_HIDDEN void tkm_prep_geometry(const tkm_prep_desc *d, tkm_prep_geom *g);
+TKM_HIDDEN int tkm_prep_bwd_bands(int rows);
+TKM_HIDDEN float tkm_rope_inv_freq(const tkm_prep_desc *d, int i);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
