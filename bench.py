@@ -34,13 +34,23 @@ CONFIGS = {
 }
 METRIC = "FlashAttn fwd+bwd TFLOP/s & % fp16 MFMA peak, B4 H16 S2048 D128 causal"
 
+# qkv-prep epilogue (generated, hipRTC): name -> (B, S, Hq, Hkv, D, qknorm, rope, rope args).
+# prep4 = config 4's group (QKNorm + RoPE, D64); prep3 = config 3's shape with llama3 RoPE
+# (the reference accepts QKNorm only with D = 64).
+PREP_CONFIGS = {
+    "prep4": (8, 512, 8, 8, 64, True, True, {}),
+    "prep3": (4, 2048, 16, 16, 128, False, True,
+              dict(theta=500000.0, scale=8.0, low_freq_factor=1.0, high_freq_factor=4.0,
+                   original_context_length=8192.0)),
+}
+
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + sorted(PREP_CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="threads for the CPU baseline (default: min(16, online CPUs))")
@@ -75,6 +85,118 @@ def cpu_baseline(cfg, threads, max_heads):
                       f"{f / 1e9:.1f} GFLOP in {dt:.2f} s wall"}
 
 
+def prep_bytes(rows, C, QK, NH, qknorm, accumulate, bands):
+    """Algorithmic HBM bytes of one qkv-prep forward and one backward (16-bit rows)."""
+    fwd = 2 * rows * C * 2 + C * 4
+    bwd = rows * C * 2 + rows * C * 2 * (2 if accumulate else 1) + C * 4 * (2 if accumulate else 1)
+    if qknorm:
+        fwd += rows * QK * 2 + rows * NH * 4 + QK * 4
+        bwd += rows * QK * 2 + rows * NH * 4 + QK * 4 * (3 if accumulate else 2)
+    bwd += 2 * bands * (C + (QK if qknorm else 0)) * 4          # partial sums written, then read
+    return fwd, bwd
+
+
+def cpu_baseline_prep(cfg, max_rows):
+    """The qkv-prep oracle (oracle/qkv_prep_ref.c, double, one thread) on the first max_rows rows."""
+    import numpy as np
+
+    import oracle
+    B, S, Hq, Hkv, D, qknorm, rope, rargs = cfg
+    rows = min(B * S, max_rows)
+    C, QK, NH = (Hq + 2 * Hkv) * D, (Hq + Hkv) * D, Hq + Hkv
+    rng = np.random.default_rng(0)
+    x, _ = oracle.round_to(rng.standard_normal((rows, C)).astype(np.float32), "f16")
+    g, _ = oracle.round_to(rng.standard_normal((rows, C)).astype(np.float32), "f16")
+    bias = np.zeros(C, np.float32)
+    gamma = np.ones(QK, np.float32)
+    f = oracle.prep_inv_freq(D, theta=rargs.get("theta", 10000.0), scale=rargs.get("scale", 1.0))
+    t0 = time.perf_counter()
+    out, xh, ist = oracle.prep_fwd(x, bias, gamma, f, rows, S, Hq, Hkv, D, qknorm, rope, "f16")
+    oracle.prep_bwd(g, xh, ist, gamma, f, rows, S, Hq, Hkv, D, qknorm, rope, "f16", din_prev=x)
+    dt = time.perf_counter() - t0
+    fb, bb = prep_bytes(rows, C, QK, NH, qknorm, True, 0)
+    return {"value": round((fb + bb) / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/qkv_prep_ref.c fwd+bwd on {rows} of {B * S} rows, "
+                      f"{(fb + bb) / 1e6:.1f} MB in {dt:.2f} s"}
+
+
+def run_prep(args):
+    """qkv-prep forward + backward (accumulating, as the reference's step) at a prep config."""
+    import numpy as np
+    import torch
+
+    from tokamak_amd import prep
+    cfg = PREP_CONFIGS[args.config]
+    B, S, Hq, Hkv, D, qknorm, rope, rargs = cfg
+    rows = B * S
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    P = prep.Prep(Hq, Hkv, D, S, qknorm=qknorm, rope=rope, **rargs)
+    C, QK, NH = P.C, P.QK, P.NH
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    x = torch.randn((rows, C), generator=g, device=dev).half()
+    dout = torch.randn((rows, C), generator=g, device=dev).half()
+    bias = torch.zeros(C, device=dev)
+    gamma = torch.ones(QK, device=dev)
+    out = torch.empty_like(x)
+    din = torch.zeros_like(x)
+    xhat = torch.empty((rows, QK), dtype=torch.float16, device=dev) if qknorm else None
+    istd = torch.empty((rows, NH), dtype=torch.float32, device=dev) if qknorm else None
+    dbias = torch.zeros(C, device=dev)
+    dgamma = torch.zeros(QK, device=dev) if qknorm else None
+    ws = torch.empty(P.bwd_workspace_bytes(rows), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def fwd():
+        P.fwd(x, bias, gamma, out=out, xhat=xhat, istd=istd)
+
+    def bwd():
+        P.bwd(dout, xhat, istd, gamma, din=din, dgamma=dgamma, dbias=dbias, accumulate=True, workspace=ws)
+
+    for _ in range(args.warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    K = args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for k in range(K):
+        ev[k][0].record(stream)
+        fwd()
+        ev[k][1].record(stream)
+        bwd()
+        ev[k][2].record(stream)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / K
+    tf = np.array([ev[k][0].elapsed_time(ev[k][1]) for k in range(K)])
+    tb = np.array([ev[k][1].elapsed_time(ev[k][2]) for k in range(K)])
+    bands = -(-rows // 32) if rows < 32 * 64 else 64
+    fb, bb = prep_bytes(rows, C, QK, NH, qknorm, True, bands)
+    gbs = {"qkv_prep_fwd": fb / (tf.mean() * 1e-3) / 1e9, "qkv_prep_bwd": bb / (tb.mean() * 1e-3) / 1e9}
+    dom = "qkv_prep_fwd" if tf.mean() >= tb.mean() else "qkv_prep_bwd"
+    res = {
+        "metric": f"qkv-prep fwd+bwd GB/s ({args.config})", "value": round((fb + bb) / (ms_step * 1e-3) / 1e9, 1),
+        "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic: x, dO ~ N(0,1) (torch.randn on device, seed 0), fp16",
+        "config": {"workload": f"{args.config}: qkv-prep fwd + bwd (accumulate)", "B": B, "S": S, "Hq": Hq,
+                   "Hkv": Hkv, "D": D, "qknorm": qknorm, "rope": rope, "rope_args": rargs},
+        "kernels": {"qkv_prep_fwd": {"avg_ms": round(float(tf.mean()), 5), "bytes": fb,
+                                     "gbps": round(gbs["qkv_prep_fwd"], 1)},
+                    "qkv_prep_bwd": {"avg_ms": round(float(tb.mean()), 5), "bytes": bb,
+                                     "gbps": round(gbs["qkv_prep_bwd"], 1)}},
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(gbs[dom], 1), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(gbs[dom] / PEAK_HBM_GBPS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline_prep(cfg, 2048)
+    print(json.dumps(res))
+
+
 def measured_traffic(name):
     """HBM bytes per launch of a kernel at config 3, from the FETCH_SIZE / WRITE_SIZE counter
     runs summarized in profiles/attn_cfg3_traffic.md (None if absent)."""
@@ -98,6 +220,9 @@ def main():
         print(json.dumps({"error": "this build targets one GPU: the attention kernels run on one "
                           "MI355X; multi-GPU sharding is design-only (run with --gpus 1)"}))
         sys.exit(2)
+    if args.config in PREP_CONFIGS:
+        run_prep(args)
+        return
     import numpy as np
     import torch
 
