@@ -1,5 +1,5 @@
-"""ctypes wrapper of the CPU oracles: attention (oracle/attn_ref.c) and the qkv-prep
-epilogue (oracle/qkv_prep_ref.c).
+"""ctypes wrapper of the CPU oracles: attention (oracle/attn_ref.c), the qkv-prep
+epilogue (oracle/qkv_prep_ref.c) and the plasma epilogues (oracle/plasma_ref.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
 cpu_baseline leg of bench.py as the checker.  The product path
@@ -58,6 +58,11 @@ def lib():
         L.qp_inv_freq.restype = ctypes.c_float
         L.qp_fwd.argtypes = [_f32p] * 4 + [ctypes.c_int] * 8 + [_f32p] * 3
         L.qp_bwd.argtypes = [_f32p] * 6 + [ctypes.c_int] * 8 + [_f32p, _f64p, _f64p]
+        L.pr_op_flags.argtypes = [ctypes.c_int]
+        L.pr_op_fwd.argtypes = [ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double]
+        L.pr_op_fwd.restype = ctypes.c_double
+        L.pr_op_grad.argtypes = [ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_double, _f64p]
+        L.pr_op_grad.restype = ctypes.c_double
         _lib = L
     return _lib
 
@@ -233,3 +238,113 @@ def prep_bwd(dout, xhat, istd, gamma, inv_freq, rows, S, Hq, Hkv, D, qknorm, rop
     if rc:
         raise ValueError("qp_bwd rejected its arguments")
     return din, dgamma, dbias
+
+
+# ---- plasma epilogues (oracle/plasma_ref.c) ------------------------------------------------
+
+class _PrNode(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_int), ("fval", ctypes.c_float)]
+
+
+class _PrParams(ctypes.Structure):
+    _fields_ = [("w", ctypes.POINTER(_f32p)), ("beta", ctypes.POINTER(_f32p)),
+                ("bias", ctypes.POINTER(_f32p)), ("branch", ctypes.POINTER(_f32p))]
+
+
+PR_W, PR_BETA, PR_BIAS, PR_NORM, PR_BRANCH = 1, 2, 4, 8, 16
+
+
+def plasma_flags(op: int) -> int:
+    return lib().pr_op_flags(op)
+
+
+def plasma_op(op, fv, x, w=0.0, b=0.0):
+    return lib().pr_op_fwd(op, fv, x, w, b)
+
+
+def plasma_op_grad(op, fv, p, w=0.0):
+    dw = ctypes.c_double()
+    d = lib().pr_op_grad(op, fv, p, w, ctypes.byref(dw))
+    return d, dw.value
+
+
+def _ptr_array(n, get):
+    arr = (_f32p * max(n, 1))()
+    keep = []
+    for k in range(n):
+        a = get(k)
+        if a is not None:
+            a = _f32c(a)
+            keep.append(a)
+            arr[k] = a.ctypes.data_as(_f32p)
+    return arr, keep
+
+
+def _params(nodes, params):
+    n = len(nodes)
+    P = _PrParams()
+    keep = []
+    for field in ("w", "beta", "bias", "branch"):
+        arr, kp = _ptr_array(n, lambda k, f=field: params.get((f, k)))
+        keep += kp + [arr]
+        setattr(P, field, ctypes.cast(arr, ctypes.POINTER(_f32p)))
+    return P, keep
+
+
+def plasma_fwd(x, rows, C, nodes, params, twin=False, n_left=0, n_right=0, dtype="f16"):
+    """nodes: [(op, fval)] (twin: left, right, then post); params: {("w"|"beta"|"bias"|"branch", k): array}.
+    Returns out [rows][C] and the saved state {k: xhat [rows][C]}, {k: istd [rows][ceil(C/64)]}."""
+    n = len(nodes)
+    NG = (C + 63) // 64
+    arr_nodes = (_PrNode * max(n, 1))(*[_PrNode(op, fv) for op, fv in nodes])
+    P, keep = _params(nodes, params)
+    xhat = {k: np.zeros((rows, C), np.float32) for k, (op, _) in enumerate(nodes) if plasma_flags(op) & PR_NORM}
+    istd = {k: np.zeros((rows, NG), np.float32) for k in xhat}
+    xa, _ = _ptr_array(n, lambda k: None)
+    ia, _ = _ptr_array(n, lambda k: None)
+    for k in xhat:
+        xa[k] = xhat[k].ctypes.data_as(_f32p)
+        ia[k] = istd[k].ctypes.data_as(_f32p)
+    x = _f32c(x)
+    out = np.empty((rows, C), np.float32)
+    n_main = n - (n_left + n_right if twin else 0)
+    rc = lib().pr_fwd(_ptr(x), rows, C, int(twin), arr_nodes, n_left, n_right, n_main, ctypes.byref(P),
+                      PREP_DTYPES[dtype], _ptr(out), xa, ia)
+    if rc:
+        raise ValueError("pr_fwd rejected its arguments")
+    return out, xhat, istd
+
+
+def plasma_bwd(dout, x, rows, C, nodes, params, xhat, istd, twin=False, n_left=0, n_right=0, dtype="f16",
+               acc_flags=0, din_prev=None, dbranch_prev=None, grads_prev=None):
+    """Returns din, {k: dbranch}, {("dw"|"dbeta"|"dbias", k): float64 array}."""
+    _f64p = ctypes.POINTER(ctypes.c_double)
+    n = len(nodes)
+    arr_nodes = (_PrNode * max(n, 1))(*[_PrNode(op, fv) for op, fv in nodes])
+    P, keep = _params(nodes, params)
+    W = 2 * C if twin else C
+    din = np.zeros((rows, W), np.float32) if din_prev is None else _f32c(din_prev).reshape(rows, W).copy()
+    xa, k1 = _ptr_array(n, lambda k: xhat.get(k))
+    ia, k2 = _ptr_array(n, lambda k: istd.get(k))
+    dbr = {}
+    da, _ = _ptr_array(n, lambda k: None)
+    grads = {}
+    ga = {f: (_f64p * max(n, 1))() for f in ("dw", "dbeta", "dbias")}
+    for k, (op, _) in enumerate(nodes):
+        fl = plasma_flags(op)
+        if fl & PR_BRANCH:
+            prev = None if dbranch_prev is None else dbranch_prev.get(k)
+            dbr[k] = np.zeros((rows, C), np.float32) if prev is None else _f32c(prev).copy()
+            da[k] = dbr[k].ctypes.data_as(_f32p)
+        for f, bit in (("dw", PR_W), ("dbeta", PR_BETA), ("dbias", PR_BIAS)):
+            if fl & bit:
+                prev = None if grads_prev is None else grads_prev.get((f, k))
+                grads[(f, k)] = np.zeros(C) if prev is None else np.array(prev, np.float64)
+                ga[f][k] = grads[(f, k)].ctypes.data_as(_f64p)
+    n_main = n - (n_left + n_right if twin else 0)
+    rc = lib().pr_bwd(_ptr(_f32c(dout)), _ptr(_f32c(x)), rows, C, int(twin), arr_nodes, n_left, n_right, n_main,
+                      ctypes.byref(P), xa, ia, PREP_DTYPES[dtype], acc_flags, _ptr(din), da,
+                      ga["dw"], ga["dbeta"], ga["dbias"])
+    if rc:
+        raise ValueError("pr_bwd rejected its arguments")
+    return din, dbr, grads

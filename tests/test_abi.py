@@ -26,9 +26,9 @@ def test_library_exports_header_functions():
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
     assert set(names) <= exported
     # nothing else with C linkage leaks out of the library: the exports are exactly the
-    # functions the two public headers declare
-    from tokamak_amd import prep
-    both = set(names) | set(prep.header_functions())
+    # functions the three public headers declare
+    from tokamak_amd import plasma, prep
+    both = set(names) | set(prep.header_functions()) | set(plasma.header_functions())
     for n in both:
         assert hasattr(L, n), n
     assert {e for e in exported if e.startswith("tkm_")} == both

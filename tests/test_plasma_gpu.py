@@ -1,0 +1,181 @@
+"""GPU parity of the generated plasma epilogues (hipRTC, launched through include/tkm_plasma.h)
+against the CPU oracle oracle/plasma_ref.c.
+
+Bars, element-wise against the oracle on the same rounded inputs:
+  out, xhat, din, dbranch (16-bit)  |gpu - ref| <= 2 ulp of the storage type at |ref| + 1e-4 * max(1, |ref|max)
+  istd (fp32)                       relative 1e-5
+  parameter gradients (fp32 sums)   |gpu - ref| <= 1e-4 * |ref| + 1e-6 * rows * max(1, |ref|max)
+The oracle computes in double and rounds once.  The kernels compute in fp32 with the
+registry's fast intrinsics (__expf, __sinf, tanhf, ...), and a chain of up to 8 ops
+accumulates a few fp32 ulps before the final rounding, hence 2 ulps.  The backward is
+checked on the state the GPU forward saved (xhat, istd).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from attn_cases import from_device, log, to_device
+
+pytestmark = pytest.mark.gpu
+
+
+def ulp(ref, dtype):
+    p, emin = (11, -14) if dtype == "f16" else (8, -126)
+    a = np.maximum(np.abs(ref.astype(np.float64)), 2.0 ** (emin - 30))
+    return 2.0 ** (np.maximum(np.floor(np.log2(a)), emin) - (p - 1))
+
+
+def check16(name, got, ref, dtype):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    bound = 2 * ulp(ref, dtype) + 1e-4 * max(1.0, float(np.abs(ref).max(initial=0.0)))
+    diff = np.abs(got - ref)
+    bad = diff > bound
+    log(f"    {name}: max_abs={diff.max(initial=0.0):.3e} n_bad={int(bad.sum())}/{ref.size}")
+    if bad.any():
+        i = tuple(np.argwhere(bad)[0])
+        pytest.fail(f"{name}: {int(bad.sum())} elements off, e.g. {i}: gpu {got[i]} ref {ref[i]}")
+
+
+CHAINS = [
+    dict(C=512, chain=["Bias", "Add", "RMSNorm"], acc=7),
+    dict(C=64, chain=["RMSNorm", ("SoftCap", 4.0), "LayerScale"], acc=7),
+    dict(C=96, chain=["LN", "GELU", "DyT", "PReLU", "xATLU"], acc=0),
+    dict(C=24, chain=["Bias", "L2Norm", "Mish", ("Snake", 1.2), "Softplus", "BN"], acc=3),
+    dict(C=128, chain=["SiLU", "ReLU2", ("LeakyReLU", 0.1), "ELU", "HardSwish", "HardSigmoid", "Tanh", "Sigmoid"],
+         acc=1),
+    dict(C=64, chain=[("SwishBeta", 1.5), ("Sin", 1.3), "CosGate", ("Clamp", 1.5), ("Scale", 0.7), "ReLU", "Add"],
+         acc=4),
+    dict(C=1536, twin=True, left=["SiLU"], right=[], chain=[("Scale", 0.5), "Add"], acc=6),
+    dict(C=64, twin=True, left=["Bias", "GELU"], right=["Bias", "LayerScale"], chain=["RMSNorm"], acc=2),
+    dict(C=32, twin=True, left=["Sigmoid"], right=["Tanh"], chain=[], acc=0),
+]
+
+
+def _nodes(c):
+    from tokamak_amd import plasma
+    def norm(lst):
+        return [(x, None) if isinstance(x, str) else x for x in lst]
+    items = (norm(c["left"]) + norm(c["right"]) + norm(c["chain"])) if c.get("twin") else norm(c["chain"])
+    L = plasma.lib()
+    return [(plasma.OPS[n], float(L.tkm_plasma_default_fval(plasma.OPS[n])) if fv is None else float(fv))
+            for n, fv in items]
+
+
+def run_chain(dev, c, rows, dtype, seed):
+    import torch
+    from tokamak_amd import plasma
+    C, twin = c["C"], bool(c.get("twin"))
+    nl, nr = (len(c["left"]), len(c["right"])) if twin else (0, 0)
+    acc = c["acc"]
+    log(f"[case] plasma C{C} twin={int(twin)} chain={c.get('left', [])}|{c.get('right', [])}|{c['chain']} "
+        f"{dtype} rows={rows} acc={acc} seed={seed}")
+    nodes = _nodes(c)
+    P = plasma.Plasma(C, c["chain"], twin, c.get("left", ()), c.get("right", ()), dtype, group_id=seed)
+    rng = np.random.default_rng(seed)
+    W = 2 * C if twin else C
+    x_r, x_b = oracle.round_to(rng.standard_normal((rows, W)).astype(np.float32), dtype)
+    g_r, g_b = oracle.round_to(rng.standard_normal((rows, C)).astype(np.float32), dtype)
+    t16 = torch.float16 if dtype == "f16" else torch.bfloat16
+    params, tens = {}, {"in": to_device(x_b, dtype, dev), "dout": to_device(g_b, dtype, dev)}
+    NG = (C + 63) // 64
+    for k, (op, _) in enumerate(nodes):
+        fl = oracle.plasma_flags(op)
+        for key, bit, scale in (("w", oracle.PR_W, 0.3), ("beta", oracle.PR_BETA, 0.2), ("bias", oracle.PR_BIAS, 0.2)):
+            if fl & bit:
+                a = ((1.0 if key == "w" else 0.0) + scale * rng.standard_normal(C)).astype(np.float32)
+                params[(key, k)] = a
+                tens[(key, k)] = torch.from_numpy(a).to(dev)
+        if fl & oracle.PR_BRANCH:
+            b_r, b_b = oracle.round_to(rng.standard_normal((rows, C)).astype(np.float32), dtype)
+            params[("branch", k)] = b_r
+            tens[("branch", k)] = to_device(b_b, dtype, dev)
+            p_r, p_b = oracle.round_to(rng.standard_normal((rows, C)).astype(np.float32), dtype)
+            params[("dbranch_prev", k)] = p_r
+            tens[("dbranch", k)] = to_device(p_b, dtype, dev)
+        if fl & oracle.PR_NORM:
+            tens[("xhat", k)] = torch.empty((rows, C), dtype=t16, device=dev)
+            tens[("istd", k)] = torch.empty((rows, NG), dtype=torch.float32, device=dev)
+        for key, bit in (("dw", oracle.PR_W), ("dbeta", oracle.PR_BETA), ("dbias", oracle.PR_BIAS)):
+            if fl & bit:
+                prev = (0.1 * rng.standard_normal(C)).astype(np.float32)
+                params[(key + "_prev", k)] = prev
+                tens[(key, k)] = torch.from_numpy(prev).to(dev)
+    tens["out"] = torch.empty((rows, C), dtype=t16, device=dev)
+    dp_r, dp_b = oracle.round_to(rng.standard_normal((rows, W)).astype(np.float32), dtype)
+    tens["din"] = to_device(dp_b, dtype, dev)
+
+    P.fwd(tens, rows)
+    torch.cuda.synchronize()
+    plain = {k: v for k, v in params.items() if k[0] in ("w", "beta", "bias", "branch")}
+    ro, rxh, ris = oracle.plasma_fwd(x_r, rows, C, nodes, plain, twin, nl, nr, dtype)
+    check16("out", from_device(tens["out"]), ro, dtype)
+    gxh, gis = {}, {}
+    for k in rxh:
+        check16(f"xhat{k}", from_device(tens[("xhat", k)]), rxh[k], dtype)
+        gis[k] = tens[("istd", k)].cpu().numpy()
+        np.testing.assert_allclose(gis[k], ris[k], rtol=1e-5)
+        gxh[k] = from_device(tens[("xhat", k)])
+
+    P.bwd(tens, rows, acc)
+    torch.cuda.synchronize()
+    din, dbr, grads = oracle.plasma_bwd(
+        g_r, x_r, rows, C, nodes, plain, gxh, gis, twin, nl, nr, dtype, acc_flags=acc, din_prev=dp_r,
+        dbranch_prev={k[1]: v for k, v in params.items() if k[0] == "dbranch_prev"},
+        grads_prev={(k[0][:-5], k[1]): v for k, v in params.items() if k[0].endswith("_prev") and k[0] != "dbranch_prev"})
+    check16("din", from_device(tens["din"]), din, dtype)
+    for k, v in dbr.items():
+        check16(f"dbranch{k}", from_device(tens[("dbranch", k)]), v, dtype)
+    for (kind, k), ref in grads.items():
+        got = tens[(kind, k)].cpu().numpy().astype(np.float64)
+        bound = 1e-4 * np.abs(ref) + 1e-6 * rows * max(1.0, float(np.abs(ref).max()))
+        diff = np.abs(got - ref)
+        log(f"    {kind}{k}: max_abs={diff.max():.3e}")
+        assert np.all(diff <= bound), (kind, k, float(diff.max()))
+    P.close()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("ci", range(len(CHAINS)), ids=lambda i: f"chain{i}_C{CHAINS[i]['C']}")
+def test_plasma_chain_parity(gpu, ci, dtype):
+    rows = {512: 300, 1536: 130}.get(CHAINS[ci]["C"], 777)
+    run_chain(gpu, CHAINS[ci], rows, dtype, seed=ci + 1)
+
+
+def test_plasma_config4_pre_attention(gpu):
+    """Config 4's residual + pre-norm group (d_model 512, 4096 rows): Add then RMSNorm (F7 groups)."""
+    run_chain(gpu, dict(C=512, chain=["Add", "RMSNorm"], acc=7), 4096, "f16", seed=40)
+
+
+def test_plasma_config4_swiglu(gpu):
+    """Config 4's gated FFN epilogue: SiLU(gate) * up over 4096 rows of 2 x 1536."""
+    run_chain(gpu, dict(C=1536, twin=True, left=["SiLU"], right=[], chain=[], acc=2), 4096, "f16", seed=41)
+
+
+def test_plasma_deterministic(gpu):
+    import torch
+    from tokamak_amd import plasma
+    C, rows = 512, 1000
+    P = plasma.Plasma(C, ["Bias", "RMSNorm", "LayerScale"])
+    rng = np.random.default_rng(0)
+    _, xb = oracle.round_to(rng.standard_normal((rows, C)).astype(np.float32), "f16")
+    _, gb = oracle.round_to(rng.standard_normal((rows, C)).astype(np.float32), "f16")
+    t = {"in": to_device(xb, "f16", gpu), "dout": to_device(gb, "f16", gpu),
+         "out": torch.empty((rows, C), dtype=torch.float16, device=gpu),
+         "din": torch.empty((rows, C), dtype=torch.float16, device=gpu),
+         ("bias", 0): torch.zeros(C, device=gpu), ("w", 1): torch.ones(C, device=gpu),
+         ("w", 2): torch.full((C,), 0.5, device=gpu),
+         ("xhat", 1): torch.empty((rows, C), dtype=torch.float16, device=gpu),
+         ("istd", 1): torch.empty((rows, 8), device=gpu),
+         ("dbias", 0): torch.empty(C, device=gpu), ("dw", 1): torch.empty(C, device=gpu),
+         ("dw", 2): torch.empty(C, device=gpu)}
+    runs = []
+    for _ in range(2):
+        P.fwd(t, rows)
+        P.bwd(t, rows, 0)
+        torch.cuda.synchronize()
+        runs.append({k: v.clone() for k, v in t.items()})
+    for k in runs[0]:
+        assert torch.equal(runs[0][k], runs[1][k]), k
+    P.close()

@@ -19,7 +19,8 @@ INCLUDE = os.path.join(ROOT, "include")
 LIB_NAME = "libtkm_attn.so"
 LIB_PATH = os.path.join(PKG, LIB_NAME)
 SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "tkm_attn_abi.hip"]
-C_SOURCES = ["tkm_error.c", "tkm_prelude.c", "tkm_prep_codegen.c", "tkm_rtc.c"]
+C_SOURCES = ["tkm_error.c", "tkm_prelude.c", "tkm_prep_codegen.c", "tkm_rtc.c", "tkm_plasma_codegen.c",
+             "tkm_plasma_rt.c"]
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 

@@ -216,7 +216,7 @@ static void emit_fwd(sbuf *s, const tkm_prep_desc *d, const tkm_prep_geom *g) {
     sb_add(s, "#pragma unroll\n");
     sb_add(s, "    for (int k = 0; k < %d; ++k) {\n", TKM_PREP_FWD_RPW);
     sb_add(s, "        const int r = r0 + 4 * k;\n");
-    sb_add(s, "        x[k] = (ok && r < rows) ? in[(size_t)r * TKM_CH + ch] : make_uint4(0u, 0u, 0u, 0u);\n");
+    sb_add(s, "        x[k] = (ok && r < rows) ? in[(size_t)r * TKM_CH + ch] : tkm_zero4();\n");
     sb_add(s, "    }\n");
     sb_add(s, "#pragma unroll\n");
     sb_add(s, "    for (int k = 0; k < %d; ++k) {\n", TKM_PREP_FWD_RPW);
@@ -269,10 +269,9 @@ static void emit_bwd(sbuf *s, const tkm_prep_desc *d, const tkm_prep_geom *g) {
     sb_add(s, "        for (int k = 0; k < %d; ++k) {\n", B);
     sb_add(s, "            const int r = rb + 4 * k;\n");
     sb_add(s, "            const bool live = ok && r < rend;\n");
-    sb_add(s, "            const uint4 z = make_uint4(0u, 0u, 0u, 0u);\n");
-    sb_add(s, "            dyr[k] = live ? dout[(size_t)r * TKM_CH + ch] : z;\n");
-    sb_add(s, "            pv[k] = (live && accumulate) ? din[(size_t)r * TKM_CH + ch] : z;\n");
-    if (d->has_qknorm) sb_add(s, "            xhr[k] = (live && qk) ? save_xhat[(size_t)r * TKM_QKCH + ch] : z;\n");
+    sb_add(s, "            dyr[k] = live ? dout[(size_t)r * TKM_CH + ch] : tkm_zero4();\n");
+    sb_add(s, "            pv[k] = (live && accumulate) ? din[(size_t)r * TKM_CH + ch] : tkm_zero4();\n");
+    if (d->has_qknorm) sb_add(s, "            xhr[k] = (live && qk) ? save_xhat[(size_t)r * TKM_QKCH + ch] : tkm_zero4();\n");
     sb_add(s, "        }\n");
     sb_add(s, "#pragma unroll\n");
     sb_add(s, "        for (int k = 0; k < %d; ++k) {\n", B);

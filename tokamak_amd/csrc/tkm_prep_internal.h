@@ -33,6 +33,13 @@ TKM_HIDDEN void tkm_prep_geometry(const tkm_prep_desc *d, tkm_prep_geom *g);
 TKM_HIDDEN int tkm_prep_bwd_bands(int rows);
 TKM_HIDDEN float tkm_rope_inv_freq(const tkm_prep_desc *d, int i);
 
+/* Checks that the current device is gfx950, compiles src with hipRTC and loads it; *module
+ * receives the hipModule_t. */
+TKM_HIDDEN int tkm_rtc_load(const char *src, const char *name, void **module);
+TKM_HIDDEN int tkm_rtc_function(void *module, const char *name, void **fn);
+TKM_HIDDEN void tkm_rtc_unload(void *module);
+TKM_HIDDEN int tkm_rtc_launch(void *fn, unsigned gx, unsigned gy, void **args, void *stream, const char *what);
+
 #ifdef __cplusplus
 }
 #endif

@@ -106,43 +106,69 @@ static int current_device_is_gfx950(void) {
     return TKM_ATTN_OK;
 }
 
+int tkm_rtc_load(const char *src, const char *name, void **module) {
+    *module = NULL;
+    int rc = current_device_is_gfx950();
+    if (rc) return rc;
+    void *code = NULL;
+    size_t code_bytes = 0;
+    rc = tkm_rtc_compile(src, name, &code, &code_bytes, NULL);
+    if (rc) return rc;
+    hipModule_t m = NULL;
+    hipError_t e = hipModuleLoadData(&m, code);
+    free(code);
+    if (e != hipSuccess) return hip_fail("hipModuleLoadData", e);
+    *module = (void *)m;
+    return TKM_ATTN_OK;
+}
+
+int tkm_rtc_function(void *module, const char *name, void **fn) {
+    hipFunction_t f = NULL;
+    hipError_t e = hipModuleGetFunction(&f, (hipModule_t)module, name);
+    if (e != hipSuccess) return hip_fail(name, e);
+    *fn = (void *)f;
+    return TKM_ATTN_OK;
+}
+
+void tkm_rtc_unload(void *module) {
+    if (module) hipModuleUnload((hipModule_t)module);
+}
+
+int tkm_rtc_launch(void *fn, unsigned gx, unsigned gy, void **args, void *stream, const char *what) {
+    hipError_t e = hipModuleLaunchKernel((hipFunction_t)fn, gx, gy, 1, 256, 1, 1, 0, (hipStream_t)stream, args, NULL);
+    if (e != hipSuccess) return tkm_set_error(TKM_ATTN_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return TKM_ATTN_OK;
+}
+
 int tkm_prep_create(const tkm_prep_desc *d, tkm_prep **out) {
     if (!out) return tkm_set_error(TKM_ATTN_EINVAL, "tkm_prep_create: out is NULL");
     *out = NULL;
     int rc = tkm_prep_check_desc(d);
     if (rc) return rc;
-    rc = current_device_is_gfx950();
-    if (rc) return rc;
     char *src = tkm_prep_source(d);
     if (!src) return TKM_ATTN_EINVAL;
-    void *code = NULL;
-    size_t code_bytes = 0;
-    rc = tkm_rtc_compile(src, "tkm_qkv_prep.hip", &code, &code_bytes, NULL);
+    void *module = NULL;
+    rc = tkm_rtc_load(src, "tkm_qkv_prep.hip", &module);
     free(src);
     if (rc) return rc;
     tkm_prep *p = (tkm_prep *)calloc(1, sizeof *p);
     if (!p) {
-        free(code);
+        tkm_rtc_unload(module);
         return tkm_set_error(TKM_ATTN_EINVAL, "out of host memory");
     }
     p->desc = *d;
     tkm_prep_geometry(d, &p->geom);
-    hipError_t e = hipModuleLoadData(&p->module, code);
-    free(code);
-    if (e != hipSuccess) {
-        free(p);
-        return hip_fail("hipModuleLoadData", e);
-    }
+    p->module = (hipModule_t)module;
     char name[96];
     hipFunction_t *fns[3] = {&p->fwd, &p->bwd, &p->reduce};
     const char *fmt[3] = {"tkm_plasma_fwd_g%d", "tkm_plasma_bwd_g%d", "tkm_plasma_bwd_g%d_reduce"};
     for (int i = 0; i < 3; ++i) {
         snprintf(name, sizeof name, fmt[i], d->group_id);
-        e = hipModuleGetFunction(fns[i], p->module, name);
-        if (e != hipSuccess) {
-            hipModuleUnload(p->module);
+        rc = tkm_rtc_function(module, name, (void **)fns[i]);
+        if (rc) {
+            tkm_rtc_unload(module);
             free(p);
-            return hip_fail(name, e);
+            return rc;
         }
     }
     *out = p;
@@ -158,9 +184,7 @@ void tkm_prep_destroy(tkm_prep *p) {
 static int aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 static int launch(hipFunction_t f, unsigned gx, unsigned gy, void **args, void *stream, const char *what) {
-    hipError_t e = hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, (hipStream_t)stream, args, NULL);
-    if (e != hipSuccess) return tkm_set_error(TKM_ATTN_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
-    return TKM_ATTN_OK;
+    return tkm_rtc_launch((void *)f, gx, gy, args, stream, what);
 }
 
 static int check_rows(int rows) {
