@@ -50,7 +50,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + sorted(PREP_CONFIGS))
+    ap.add_argument("--config", default="cfg3",
+                    choices=sorted(CONFIGS) + sorted(PREP_CONFIGS) + sorted(PLASMA_CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="threads for the CPU baseline (default: min(16, online CPUs))")
@@ -85,14 +86,15 @@ def cpu_baseline(cfg, threads, max_heads):
                       f"{f / 1e9:.1f} GFLOP in {dt:.2f} s wall"}
 
 
-def prep_bytes(rows, C, QK, NH, qknorm, accumulate, bands):
-    """Algorithmic HBM bytes of one qkv-prep forward and one backward (16-bit rows)."""
+def prep_bytes(rows, C, QK, NH, qknorm, accumulate, part_bytes):
+    """Algorithmic HBM bytes of one qkv-prep forward and one backward (16-bit rows); part_bytes
+    is the backward's partial-sum buffer, written once and read once."""
     fwd = 2 * rows * C * 2 + C * 4
     bwd = rows * C * 2 + rows * C * 2 * (2 if accumulate else 1) + C * 4 * (2 if accumulate else 1)
     if qknorm:
         fwd += rows * QK * 2 + rows * NH * 4 + QK * 4
         bwd += rows * QK * 2 + rows * NH * 4 + QK * 4 * (3 if accumulate else 2)
-    bwd += 2 * bands * (C + (QK if qknorm else 0)) * 4          # partial sums written, then read
+    bwd += 2 * part_bytes
     return fwd, bwd
 
 
@@ -174,8 +176,7 @@ def run_prep(args):
     ms_step = t0.elapsed_time(t1) / K
     tf = np.array([ev[k][0].elapsed_time(ev[k][1]) for k in range(K)])
     tb = np.array([ev[k][1].elapsed_time(ev[k][2]) for k in range(K)])
-    bands = -(-rows // 32) if rows < 32 * 64 else 64
-    fb, bb = prep_bytes(rows, C, QK, NH, qknorm, True, bands)
+    fb, bb = prep_bytes(rows, C, QK, NH, qknorm, True, P.bwd_workspace_bytes(rows))
     gbs = {"qkv_prep_fwd": fb / (tf.mean() * 1e-3) / 1e9, "qkv_prep_bwd": bb / (tb.mean() * 1e-3) / 1e9}
     dom = "qkv_prep_fwd" if tf.mean() >= tb.mean() else "qkv_prep_bwd"
     res = {
@@ -195,6 +196,151 @@ def run_prep(args):
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline_prep(cfg, 2048)
     print(json.dumps(res))
+
+
+# plasma epilogues: name -> list of (label, C, rows, plasma kwargs, acc flags); config 4's groups
+PLASMA_CONFIGS = {
+    "plasma4": [("residual_rmsnorm", 512, 4096, dict(chain=["Add", "RMSNorm"]), 7),
+                ("swiglu", 1536, 4096, dict(twin=True, left=["SiLU"]), 2)],
+}
+
+
+def plasma_bytes(P, rows, acc):
+    """Algorithmic HBM bytes of one forward and one backward of a plasma group, from its
+    argument lists (16-bit rows, fp32 parameters and istd, partial sums written and read)."""
+    C, W, NG = P.C, (2 * P.C if P.twin else P.C), P.norm_groups()
+    size = {"in": rows * W * 2, "out": rows * C * 2, "dout": rows * C * 2, "xhat": rows * C * 2,
+            "istd": rows * NG * 4, "branch": rows * C * 2, "w": C * 4, "beta": C * 4, "bias": C * 4,
+            "dw": C * 4, "dbeta": C * 4, "dbias": C * 4}
+    fwd = sum(size[k] for k, _ in P.fwd_args)
+    bwd = 0
+    for k, _ in P.bwd_args:
+        if k == "din":
+            bwd += rows * W * 2 * (2 if acc & 1 else 1)
+        elif k == "dbranch":
+            bwd += rows * C * 2 * (2 if acc & 4 else 1)
+        elif k in ("dw", "dbeta", "dbias"):
+            bwd += C * 4 * (2 if acc & 2 else 1)
+        else:
+            bwd += size[k]
+    bwd += 2 * P.bwd_workspace_bytes(rows)
+    return fwd, bwd
+
+
+def run_plasma(args):
+    """Forward + backward of config 4's plasma groups (generated, hipRTC)."""
+    import numpy as np
+    import torch
+
+    from tokamak_amd import plasma
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    groups = []
+    for label, C, rows, kw, acc in PLASMA_CONFIGS[args.config]:
+        P = plasma.Plasma(C, group_id=len(groups), **kw)
+        W = 2 * C if P.twin else C
+        t = {"in": torch.randn((rows, W), generator=g, device=dev).half(),
+             "dout": torch.randn((rows, C), generator=g, device=dev).half(),
+             "out": torch.empty((rows, C), dtype=torch.float16, device=dev),
+             "din": torch.zeros((rows, W), dtype=torch.float16, device=dev)}
+        for kind, node in P.fwd_args + P.bwd_args:
+            if node < 0 or (kind, node) in t:
+                continue
+            if kind in ("w", "dw"):
+                t[(kind, node)] = torch.ones(C, device=dev) if kind == "w" else torch.zeros(C, device=dev)
+            elif kind in ("beta", "bias", "dbeta", "dbias"):
+                t[(kind, node)] = torch.zeros(C, device=dev)
+            elif kind in ("branch", "dbranch"):
+                t[(kind, node)] = torch.randn((rows, C), generator=g, device=dev).half()
+            elif kind == "xhat":
+                t[(kind, node)] = torch.empty((rows, C), dtype=torch.float16, device=dev)
+            elif kind == "istd":
+                t[(kind, node)] = torch.empty((rows, P.norm_groups()), device=dev)
+        ws = torch.empty(max(P.bwd_workspace_bytes(rows), 1), dtype=torch.uint8, device=dev)
+        groups.append((label, P, t, rows, acc, ws))
+    stream = torch.cuda.current_stream()
+
+    def step(evs=None):
+        for i, (label, P, t, rows, acc, ws) in enumerate(groups):
+            P.fwd(t, rows)
+            if evs is not None:
+                evs[2 * i].record(stream)
+            P.bwd(t, rows, acc, workspace=ws)
+            if evs is not None:
+                evs[2 * i + 1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    K = args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(groups) + 1)] for _ in range(K)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for k in range(K):
+        ev[k][0].record(stream)
+        step(ev[k][1:])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / K
+    kernels, total = {}, 0
+    for i, (label, P, t, rows, acc, ws) in enumerate(groups):
+        fb, bb = plasma_bytes(P, rows, acc)
+        total += fb + bb
+        tf = np.array([ev[k][2 * i].elapsed_time(ev[k][2 * i + 1]) for k in range(K)])
+        tb = np.array([ev[k][2 * i + 1].elapsed_time(ev[k][2 * i + 2]) for k in range(K)])
+        kernels[label + "_fwd"] = {"avg_ms": round(float(tf.mean()), 5), "bytes": fb,
+                                   "gbps": round(fb / (tf.mean() * 1e-3) / 1e9, 1)}
+        kernels[label + "_bwd"] = {"avg_ms": round(float(tb.mean()), 5), "bytes": bb,
+                                   "gbps": round(bb / (tb.mean() * 1e-3) / 1e9, 1)}
+    dom = max(kernels, key=lambda n: kernels[n]["avg_ms"])
+    res = {
+        "metric": f"plasma epilogues fwd+bwd GB/s ({args.config})",
+        "value": round(total / (ms_step * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic: torch.randn on device (seed 0), fp16",
+        "config": {"workload": f"{args.config}: config 4's residual+RMSNorm (C512) and SwiGLU (2x1536) groups, "
+                               "4096 rows, fwd + bwd"},
+        "kernels": kernels,
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": kernels[dom]["gbps"], "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(kernels[dom]["gbps"] / PEAK_HBM_GBPS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline_plasma(args.config, 1024)
+    print(json.dumps(res))
+
+
+def cpu_baseline_plasma(name, max_rows):
+    """The plasma oracle (oracle/plasma_ref.c, double, one thread) on the first max_rows rows."""
+    import numpy as np
+
+    import oracle
+    from tokamak_amd import plasma
+    total, t = 0, 0.0
+    for label, C, rows, kw, acc in PLASMA_CONFIGS[name]:
+        r = min(rows, max_rows)
+        twin = kw.get("twin", False)
+        items = kw.get("left", []) + kw.get("right", []) + kw.get("chain", [])
+        nodes = [(plasma.OPS[n], float(plasma.lib().tkm_plasma_default_fval(plasma.OPS[n]))) for n in items]
+        rng = np.random.default_rng(0)
+        x = rng.standard_normal((r, 2 * C if twin else C)).astype(np.float32)
+        params = {}
+        for k, (op, _) in enumerate(nodes):
+            fl = oracle.plasma_flags(op)
+            if fl & oracle.PR_W:
+                params[("w", k)] = np.ones(C, np.float32)
+            if fl & oracle.PR_BRANCH:
+                params[("branch", k)] = rng.standard_normal((r, C)).astype(np.float32)
+        t0 = time.perf_counter()
+        out, xh, ist = oracle.plasma_fwd(x, r, C, nodes, params, twin, len(kw.get("left", [])), 0, "f16")
+        oracle.plasma_bwd(out, x, r, C, nodes, params, xh, ist, twin, len(kw.get("left", [])), 0, "f16", acc)
+        t += time.perf_counter() - t0
+        W = 2 * C if twin else C
+        total += r * (W + C) * 2 * 3
+    return {"value": round(total / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/plasma_ref.c fwd+bwd of both groups on {max_rows} of 4096 rows "
+                      f"(bytes counted as 3 x (in + out) rows), {t:.2f} s"}
 
 
 def measured_traffic(name):
@@ -222,6 +368,9 @@ def main():
         sys.exit(2)
     if args.config in PREP_CONFIGS:
         run_prep(args)
+        return
+    if args.config in PLASMA_CONFIGS:
+        run_plasma(args)
         return
     import numpy as np
     import torch

@@ -10,9 +10,10 @@
  *     its sums are DPP adds inside the lane row; every lane runs the reductions (lanes past
  *     the row end hold zeros), only loads and stores are predicated;
  *   - forward: 4 rows per lane slot, loads first;
- *   - backward: rows in bands; parameter-gradient sums stay in registers over the band, the
- *     block's lane slots combine through LDS in a fixed order into one partial row per band,
- *     and a reduce kernel adds the bands in order (no atomics).
+ *   - backward: rows in bands (about 2048 blocks in all, at least 16 rows per band);
+ *     parameter-gradient sums stay in registers over the band, the block's lane slots combine
+ *     through LDS in a fixed order into one partial row per band, and a reduce kernel (16
+ *     waves per column group) adds the bands in order (no atomics).
  */
 #include <math.h>
 #include <stdarg.h>
@@ -200,12 +201,6 @@ void tkm_plasma_geometry(const tkm_plasma_desc *d, tkm_plasma_geom *g) {
     g->n_fwd = nf;
     g->n_bwd = nb;
     g->part_width = g->n_par * g->C;
-}
-
-int tkm_plasma_bwd_bands(int rows) {
-    int bands = (rows + TKM_PLASMA_MIN_BAND - 1) / TKM_PLASMA_MIN_BAND;
-    if (bands > TKM_PLASMA_MAX_BANDS) bands = TKM_PLASMA_MAX_BANDS;
-    return bands < 1 ? 1 : bands;
 }
 
 /* ---- emission -------------------------------------------------------------------------- */
@@ -577,7 +572,7 @@ static void emit_bwd(sbuf *s, const tkm_plasma_desc *d, const tkm_plasma_geom *g
     sb_add(s, "}\n\n");
 
     if (g->n_par > 0) {
-        sb_add(s, "extern \"C\" __global__ __launch_bounds__(256) void tkm_plasma_bwd_g%d_reduce(\n", d->group_id);
+        sb_add(s, "extern \"C\" __global__ __launch_bounds__(1024) void tkm_plasma_bwd_g%d_reduce(\n", d->group_id);
         sb_add(s, "    const float *__restrict__ part, int bands, int acc_params");
         for (int p = 0; p < g->n_par; ++p) sb_add(s, ", float *__restrict__ dst%d", p);
         sb_add(s, ")\n{\n");
@@ -585,14 +580,15 @@ static void emit_bwd(sbuf *s, const tkm_plasma_desc *d, const tkm_plasma_geom *g
         sb_add(s, "    const int c = blockIdx.x * 64 + lane;\n");
         sb_add(s, "    float acc = 0.f;\n");
         sb_add(s, "    if (c < TKM_PW) {\n");
-        sb_add(s, "#pragma unroll 8\n");
-        sb_add(s, "        for (int b = wave; b < bands; b += 4) acc += part[(size_t)b * TKM_PW + c];\n");
+        sb_add(s, "#pragma unroll 4\n");
+        sb_add(s, "        for (int b = wave; b < bands; b += 16) acc += part[(size_t)b * TKM_PW + c];\n");
         sb_add(s, "    }\n");
-        sb_add(s, "    __shared__ float red[4][64];\n");
+        sb_add(s, "    __shared__ float red[16][64];\n");
         sb_add(s, "    red[wave][lane] = acc;\n");
         sb_add(s, "    __syncthreads();\n");
         sb_add(s, "    if (wave != 0 || c >= TKM_PW) return;\n");
-        sb_add(s, "    const float t = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];\n");
+        sb_add(s, "    float t = red[0][lane];\n");
+        sb_add(s, "    for (int q = 1; q < 16; ++q) t += red[q][lane];\n");
         sb_add(s, "    const int p = c / %d, o = c - p * %d;\n", g->C, g->C);
         sb_add(s, "    float *dst = ");
         for (int p = 0; p < g->n_par; ++p) sb_add(s, "%sp == %d ? dst%d", p ? " : " : "", p, p);

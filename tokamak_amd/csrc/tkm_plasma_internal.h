@@ -11,8 +11,6 @@ extern "C" {
 
 enum {
     TKM_PLASMA_FWD_RPI = 4,        /* forward: rows per lane slot per block */
-    TKM_PLASMA_MIN_BAND = 32,      /* backward: rows per band, at least */
-    TKM_PLASMA_MAX_BANDS = 64,     /* backward: bands (= partial rows), at most */
     TKM_PLASMA_MAX_ARGS = 4 + 7 * 3 * TKM_PLASMA_MAX_NODES
 };
 
@@ -32,7 +30,6 @@ typedef struct {
 
 TKM_HIDDEN int tkm_plasma_check_desc(const tkm_plasma_desc *d);
 TKM_HIDDEN void tkm_plasma_geometry(const tkm_plasma_desc *d, tkm_plasma_geom *g);
-TKM_HIDDEN int tkm_plasma_bwd_bands(int rows);
 
 #ifdef __cplusplus
 }

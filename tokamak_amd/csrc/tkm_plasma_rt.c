@@ -115,13 +115,13 @@ int tkm_plasma_fwd(const tkm_plasma *p, void *const *args, int rows, void *strea
     for (int i = 0; i < g->n_fwd; ++i) kargs[i] = (void *)&args[i];
     kargs[g->n_fwd] = (void *)&rows;
     const int rpb = TKM_PLASMA_FWD_RPI * 4 * g->RW;
-    return tkm_rtc_launch(p->fwd, (unsigned)g->XB, (unsigned)((rows + rpb - 1) / rpb), kargs, stream,
+    return tkm_rtc_launch(p->fwd, (unsigned)g->XB, (unsigned)((rows + rpb - 1) / rpb), 256, kargs, stream,
                           "plasma forward");
 }
 
 size_t tkm_plasma_bwd_workspace_bytes(const tkm_plasma *p, int rows) {
     if (!p || rows < 0 || p->geom.n_par == 0) return 0;
-    size_t b = (size_t)tkm_plasma_bwd_bands(rows) * (size_t)p->geom.part_width * sizeof(float);
+    size_t b = (size_t)tkm_bwd_bands(rows, p->geom.XB) * (size_t)p->geom.part_width * sizeof(float);
     return (b + 255) & ~(size_t)255;
 }
 
@@ -143,7 +143,7 @@ int tkm_plasma_bwd(const tkm_plasma *p, void *const *args, int rows, int acc_fla
     if (need && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15u)))
         return tkm_set_error(TKM_ATTN_EWORKSPACE, "tkm_plasma_bwd: a 16-byte aligned workspace of %zu bytes is needed",
                              need);
-    const int bands = tkm_plasma_bwd_bands(rows);
+    const int bands = tkm_bwd_bands(rows, p->geom.XB);
     int band = (rows + bands - 1) / bands;
     float *part = (float *)workspace;
     if (rows > 0 || g->n_par > 0) {
@@ -153,7 +153,7 @@ int tkm_plasma_bwd(const tkm_plasma *p, void *const *args, int rows, int acc_fla
         kargs[g->n_bwd + 1] = (void *)&rows;
         kargs[g->n_bwd + 2] = (void *)&band;
         kargs[g->n_bwd + 3] = (void *)&acc_flags;
-        rc = tkm_rtc_launch(p->bwd, (unsigned)g->XB, (unsigned)bands, kargs, stream, "plasma backward");
+        rc = tkm_rtc_launch(p->bwd, (unsigned)g->XB, (unsigned)bands, 256, kargs, stream, "plasma backward");
         if (rc) return rc;
     }
     if (g->n_par == 0) return TKM_ATTN_OK;
@@ -163,6 +163,6 @@ int tkm_plasma_bwd(const tkm_plasma *p, void *const *args, int rows, int acc_fla
     rargs[1] = (void *)&bands;
     rargs[2] = (void *)&acc_params;
     for (int i = 0; i < g->n_par; ++i) rargs[3 + i] = (void *)&args[g->n_bwd + i];
-    return tkm_rtc_launch(p->reduce, (unsigned)((g->part_width + 63) / 64), 1, rargs, stream,
+    return tkm_rtc_launch(p->reduce, (unsigned)((g->part_width + 63) / 64), 1, 64 * TKM_REDUCE_WAVES, rargs, stream,
                           "plasma backward reduction");
 }

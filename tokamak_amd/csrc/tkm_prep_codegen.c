@@ -12,9 +12,10 @@
  *     are DPP reductions inside a lane row (tkm_sum_lanes8/16), no LDS;
  *   - bias, gamma and the RoPE frequencies of the chunk are loaded once per lane;
  *   - forward: 4 rows per wave, all loads issued before the arithmetic;
- *   - backward: the d(bias) / d(gamma) sums stay in registers over the band, then the 4
- *     waves combine through LDS in a fixed order into one partial per block row; a second
- *     kernel adds the partials in block order.  No atomics: bitwise reproducible.
+ *   - backward: the d(bias) / d(gamma) sums stay in registers over the band (about 2048
+ *     blocks in all, at least 16 rows per band), then the 4 waves combine through LDS in a
+ *     fixed order into one partial per band; a second kernel (16 waves per column group)
+ *     adds the partials in band order.  No atomics: bitwise reproducible.
  * The RoPE inverse frequencies are computed here, on the host, in fp32 with the reference's
  * expression, and baked into the source as exact hexadecimal literals.
  */
@@ -125,9 +126,10 @@ void tkm_prep_geometry(const tkm_prep_desc *d, tkm_prep_geom *g) {
     g->part_width = g->C + (d->has_qknorm ? g->QK : 0);
 }
 
-int tkm_prep_bwd_bands(int rows) {
-    int bands = (rows + TKM_PREP_BWD_MIN_BAND - 1) / TKM_PREP_BWD_MIN_BAND;
-    if (bands > TKM_PREP_BWD_MAX_BANDS) bands = TKM_PREP_BWD_MAX_BANDS;
+int tkm_bwd_bands(int rows, int xblocks) {
+    int bands = (TKM_BWD_TARGET_BLOCKS + xblocks - 1) / xblocks;
+    const int most = (rows + TKM_BWD_MIN_BAND - 1) / TKM_BWD_MIN_BAND;
+    if (bands > most) bands = most;
     return bands < 1 ? 1 : bands;
 }
 
@@ -336,8 +338,8 @@ static void emit_bwd(sbuf *s, const tkm_prep_desc *d, const tkm_prep_geom *g) {
     sb_add(s, "    }\n}\n\n");
 
     /* partial rows -> dbias | dgamma: column c of the partials, summed over the bands in order.
-     * 4 waves split the bands round-robin and combine in wave order. */
-    sb_add(s, "extern \"C\" __global__ __launch_bounds__(256) void tkm_plasma_bwd_g%d_reduce(\n", d->group_id);
+     * 16 waves split the bands round-robin and combine in wave order. */
+    sb_add(s, "extern \"C\" __global__ __launch_bounds__(1024) void tkm_plasma_bwd_g%d_reduce(\n", d->group_id);
     sb_add(s, "    const float *__restrict__ part, float *__restrict__ dbias, float *__restrict__ dgamma,\n");
     sb_add(s, "    int bands, int accumulate)\n{\n");
     if (!d->has_qknorm) sb_add(s, "    (void)dgamma;\n");
@@ -345,14 +347,15 @@ static void emit_bwd(sbuf *s, const tkm_prep_desc *d, const tkm_prep_geom *g) {
     sb_add(s, "    const int c = blockIdx.x * 64 + lane;\n");
     sb_add(s, "    float acc = 0.f;\n");
     sb_add(s, "    if (c < TKM_PW) {\n");
-    sb_add(s, "#pragma unroll 8\n");
-    sb_add(s, "        for (int b = wave; b < bands; b += 4) acc += part[(size_t)b * TKM_PW + c];\n");
+    sb_add(s, "#pragma unroll 4\n");
+    sb_add(s, "        for (int b = wave; b < bands; b += 16) acc += part[(size_t)b * TKM_PW + c];\n");
     sb_add(s, "    }\n");
-    sb_add(s, "    __shared__ float red[4][64];\n");
+    sb_add(s, "    __shared__ float red[16][64];\n");
     sb_add(s, "    red[wave][lane] = acc;\n");
     sb_add(s, "    __syncthreads();\n");
     sb_add(s, "    if (wave != 0 || c >= TKM_PW) return;\n");
-    sb_add(s, "    const float t = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];\n");
+    sb_add(s, "    float t = red[0][lane];\n");
+    sb_add(s, "    for (int q = 1; q < 16; ++q) t += red[q][lane];\n");
     if (d->has_qknorm)
         sb_add(s, "    float *dst = c < TKM_C ? dbias + c : dgamma + (c - TKM_C);\n");
     else

@@ -20,8 +20,9 @@ TKM_HIDDEN int tkm_vset_error(int status, const char *fmt, va_list ap);
 enum {
     TKM_PREP_FWD_RPW = 4,          /* forward: rows per wave per block */
     TKM_PREP_BWD_BATCH = 4,        /* backward: rows per wave loaded before the arithmetic */
-    TKM_PREP_BWD_MIN_BAND = 32,    /* backward: rows per block row, at least */
-    TKM_PREP_BWD_MAX_BANDS = 64    /* backward: block rows (= partial rows), at most */
+    TKM_BWD_TARGET_BLOCKS = 2048,  /* backward: bands are chosen to give about this many blocks */
+    TKM_BWD_MIN_BAND = 16,         /* backward: rows per band, at least */
+    TKM_REDUCE_WAVES = 16          /* partial-row reduction: waves per block (1024 threads) */
 };
 
 typedef struct {
@@ -30,7 +31,10 @@ typedef struct {
 
 TKM_HIDDEN int tkm_prep_check_desc(const tkm_prep_desc *d);
 TKM_HIDDEN void tkm_prep_geometry(const tkm_prep_desc *d, tkm_prep_geom *g);
-TKM_HIDDEN int tkm_prep_bwd_bands(int rows);
+/* Bands (block rows of a backward with per-band parameter partials) for `rows` rows and
+ * `xblocks` blocks across a row: about TKM_BWD_TARGET_BLOCKS blocks, at least
+ * TKM_BWD_MIN_BAND rows per band. */
+TKM_HIDDEN int tkm_bwd_bands(int rows, int xblocks);
 TKM_HIDDEN float tkm_rope_inv_freq(const tkm_prep_desc *d, int i);
 
 /* Checks that the current device is gfx950, compiles src with hipRTC and loads it; *module
@@ -38,7 +42,8 @@ TKM_HIDDEN float tkm_rope_inv_freq(const tkm_prep_desc *d, int i);
 TKM_HIDDEN int tkm_rtc_load(const char *src, const char *name, void **module);
 TKM_HIDDEN int tkm_rtc_function(void *module, const char *name, void **fn);
 TKM_HIDDEN void tkm_rtc_unload(void *module);
-TKM_HIDDEN int tkm_rtc_launch(void *fn, unsigned gx, unsigned gy, void **args, void *stream, const char *what);
+TKM_HIDDEN int tkm_rtc_launch(void *fn, unsigned gx, unsigned gy, unsigned block, void **args, void *stream,
+                              const char *what);
 
 #ifdef __cplusplus
 }

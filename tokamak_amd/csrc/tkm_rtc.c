@@ -134,8 +134,8 @@ void tkm_rtc_unload(void *module) {
     if (module) hipModuleUnload((hipModule_t)module);
 }
 
-int tkm_rtc_launch(void *fn, unsigned gx, unsigned gy, void **args, void *stream, const char *what) {
-    hipError_t e = hipModuleLaunchKernel((hipFunction_t)fn, gx, gy, 1, 256, 1, 1, 0, (hipStream_t)stream, args, NULL);
+int tkm_rtc_launch(void *fn, unsigned gx, unsigned gy, unsigned block, void **args, void *stream, const char *what) {
+    hipError_t e = hipModuleLaunchKernel((hipFunction_t)fn, gx, gy, 1, block, 1, 1, 0, (hipStream_t)stream, args, NULL);
     if (e != hipSuccess) return tkm_set_error(TKM_ATTN_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
     return TKM_ATTN_OK;
 }
@@ -183,8 +183,9 @@ void tkm_prep_destroy(tkm_prep *p) {
 
 static int aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-static int launch(hipFunction_t f, unsigned gx, unsigned gy, void **args, void *stream, const char *what) {
-    return tkm_rtc_launch((void *)f, gx, gy, args, stream, what);
+static int launch(hipFunction_t f, unsigned gx, unsigned gy, unsigned block, void **args, void *stream,
+                  const char *what) {
+    return tkm_rtc_launch((void *)f, gx, gy, block, args, stream, what);
 }
 
 static int check_rows(int rows) {
@@ -208,13 +209,13 @@ int tkm_prep_fwd(const tkm_prep *p, const void *in, void *out, const float *bias
     void *args[] = {(void *)&in, (void *)&out, (void *)&bias, (void *)&gamma, (void *)&save_istd,
                     (void *)&save_xhat, (void *)&rows};
     const int rpb = 4 * TKM_PREP_FWD_RPW;
-    return launch(p->fwd, (unsigned)((p->geom.CH + 63) / 64), (unsigned)((rows + rpb - 1) / rpb), args, stream,
+    return launch(p->fwd, (unsigned)((p->geom.CH + 63) / 64), (unsigned)((rows + rpb - 1) / rpb), 256, args, stream,
                   "qkv-prep forward");
 }
 
 size_t tkm_prep_bwd_workspace_bytes(const tkm_prep *p, int rows) {
     if (!p || rows < 0) return 0;
-    size_t b = (size_t)tkm_prep_bwd_bands(rows) * (size_t)p->geom.part_width * sizeof(float);
+    size_t b = (size_t)tkm_bwd_bands(rows, (p->geom.CH + 63) / 64) * (size_t)p->geom.part_width * sizeof(float);
     return (b + 255) & ~(size_t)255;
 }
 
@@ -240,15 +241,15 @@ int tkm_prep_bwd(const tkm_prep *p, const void *dout, void *din, const void *sav
     if (!workspace || workspace_bytes < need)
         return tkm_set_error(TKM_ATTN_EWORKSPACE, "tkm_prep_bwd: workspace of %zu bytes needed, %zu given", need,
                              workspace ? workspace_bytes : (size_t)0);
-    int bands = tkm_prep_bwd_bands(rows);
+    int bands = tkm_bwd_bands(rows, (p->geom.CH + 63) / 64);
     int band = (rows + bands - 1) / bands;
     float *part = (float *)workspace;
     void *a1[] = {(void *)&dout, (void *)&din, (void *)&save_xhat, (void *)&save_istd, (void *)&gamma,
                   (void *)&part, (void *)&rows, (void *)&band, (void *)&accumulate};
-    rc = launch(p->bwd, (unsigned)((p->geom.CH + 63) / 64), (unsigned)bands, a1, stream, "qkv-prep backward");
+    rc = launch(p->bwd, (unsigned)((p->geom.CH + 63) / 64), (unsigned)bands, 256, a1, stream, "qkv-prep backward");
     if (rc) return rc;
     void *a2[] = {(void *)&part, (void *)&dbias, (void *)&dgamma, (void *)&bands, (void *)&accumulate};
-    return launch(p->reduce, (unsigned)((p->geom.part_width + 63) / 64), 1, a2, stream,
+    return launch(p->reduce, (unsigned)((p->geom.part_width + 63) / 64), 1, 64 * TKM_REDUCE_WAVES, a2, stream,
                   "qkv-prep backward reduction");
 }
 
