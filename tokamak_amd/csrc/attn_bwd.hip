@@ -167,7 +167,12 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
                     s = mfma32<DT>(ld_lds16((const uint16_t*)(qt + off)), kf[ks], s);
                     dp = mfma32<DT>(ld_lds16((const uint16_t*)(ot + off)), vfk, dp);
                 }
-                const bool need_mask = (causal && qr0 < kw0 + 31) || (kw0 + 32 > kvl) || (qr0 + BM > S);
+                // Branch-free causal mask: query row qr0 + hi*4 + c (c = g4*8 + i) is hidden from
+                // this lane's key iff c < tk, so the tile stays one basic block and the softmax
+                // VALU work can overlap MFMAs.  Rows past S need no mask (their Q, dO, LSE and D
+                // are zero-filled: P = 1, dS = 0, both multiplying zero rows); keys past kv_len
+                // are zeroed when dK, dV are written.
+                const int tk = causal ? key - qr0 - hi * 4 : -BM;
                 u32x4 pf[PKS], sf[PKS];
                 u32x4 pl[Split<DT>::on ? PKS : 1], sl[Split<DT>::on ? PKS : 1];
 #pragma unroll
@@ -179,10 +184,7 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
                     for (int i = 0; i < 4; ++i) {
                         const int r = g4 * 4 + i;
                         float pv = fast_exp2(__builtin_fmaf(s[r], sl2, -L[i] * 1.4426950408889634f));
-                        if (need_mask) {
-                            const int qrow = qr0 + g4 * 8 + hi * 4 + i;
-                            if (key >= kvl || (causal && key > qrow) || qrow >= S) pv = 0.f;
-                        }
+                        pv = (g4 * 8 + i < tk) ? 0.f : pv;
                         p[i] = pv;
                         ds[i] = pv * (dp[r] - Dl[i]);
                     }
@@ -236,6 +238,11 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
     }
 
     // dK^T (scaled), dV^T: lane holds key = kw0 + l32, d = db*32 + g4*8 + hi*4 + 0..3.
+    // Keys at or past kv_len get zero gradients.
+    if (key >= kvl) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) dk[db] = dv[db] = f32x16{};
+    }
     if (key < S) {
         uint16_t* dkp = bd + (size_t)key * ld + (size_t)(Hq + kvh) * D;
         uint16_t* dvp = bd + (size_t)key * ld + (size_t)(Hq + Hkv + kvh) * D;
@@ -360,7 +367,10 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
                     dp[kb] = mfma32<DT>(ld_lds16((const uint16_t*)(vt + off)), of[ks], dp[kb]);
                 }
             }
-            const bool need_mask = (causal && k0 + BN - 1 > q0) || (k0 + BN > kvl);
+            // Branch-free causal mask: key k0 + hi*4 + c (c = kb*32 + (r/4)*8 + r%4) is hidden
+            // from this lane's query iff c > tq, so the tile stays one basic block.  Keys past
+            // kv_len need no mask: their K rows are zero-filled, so they add nothing to dQ.
+            const int tq = causal ? q - k0 - hi * 4 : BN;
             u32x4 sf[PKS], sl[Split<DT>::on ? PKS : 1];
 #pragma unroll
             for (int ks = 0; ks < PKS; ++ks) {
@@ -370,10 +380,7 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
                 for (int i = 0; i < 8; ++i) {
                     const int r = r0 + i;
                     float pv = fast_exp2(__builtin_fmaf(s[kb][r], sl2, nl2));
-                    if (need_mask) {
-                        const int kr = k0 + kb * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-                        if (kr >= kvl || (causal && kr > q)) pv = 0.f;
-                    }
+                    pv = (kb * 32 + (r >> 2) * 8 + (r & 3) > tq) ? 0.f : pv;
                     ds[i] = pv * (dp[kb][r] - Dl);
                 }
 #pragma unroll
