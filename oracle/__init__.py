@@ -105,8 +105,10 @@ def widen(bits: np.ndarray, dtype: str) -> np.ndarray:
     return out
 
 
-def make_inputs(B, S, Hq, Hkv, D, dtype="f16", seed_qkv=0, seed_do=1, mul=1.0, with_dout=True):
-    """Seeded packed qkv (and dO), rounded to dtype.
+def make_inputs(B, S, Hq, Hkv, D, dtype="f16", seed_qkv=0, seed_do=1, mul=1.0, with_dout=True,
+                transform=None):
+    """Seeded packed qkv (and dO), rounded to dtype.  ``transform(q, k, v)`` may reshape the
+    fp32 draws ([B, S, H*D] each) before rounding and returns the new (q, k, v).
 
     Returns dict with float32 views ``qkv``/``dout`` holding the rounded values
     and ``qkv_bits``/``dout_bits`` (uint16) for upload, or fp32 arrays when
@@ -114,7 +116,9 @@ def make_inputs(B, S, Hq, Hkv, D, dtype="f16", seed_qkv=0, seed_do=1, mul=1.0, w
     q = normal(B * S * Hq * D, seed_qkv, 1, mul).reshape(B, S, Hq * D)
     k = normal(B * S * Hkv * D, seed_qkv, 2, mul).reshape(B, S, Hkv * D)
     v = normal(B * S * Hkv * D, seed_qkv, 3, mul).reshape(B, S, Hkv * D)
-    qkv = np.concatenate([q, k, v], axis=2)
+    if transform is not None:
+        q, k, v = transform(q, k, v)
+    qkv = np.concatenate([q, k, v], axis=2).astype(np.float32)
     out = {}
     if dtype == "f32":
         out["qkv"] = np.ascontiguousarray(qkv)

@@ -64,7 +64,7 @@ def split_dqkv(dqkv: np.ndarray, B, S, Hq, Hkv, D):
 
 
 def run_gpu_case(device, B, S, Hq, Hkv, D, dtype="f16", causal=True, kv_len=None, mul=1.0,
-                 bwd=True, seed=0, f64=None):
+                 bwd=True, seed=0, f64=None, transform=None):
     """Runs the HIP forward (and backward) and the oracle; returns a list of compare() stats."""
     import torch
     from tokamak_amd import attn
@@ -72,7 +72,7 @@ def run_gpu_case(device, B, S, Hq, Hkv, D, dtype="f16", causal=True, kv_len=None
     tag = f"B{B} S{S} Hq{Hq} Hkv{Hkv} D{D} {dtype} causal={int(causal)} kv_len={kv_len} seed={seed}"
     log(f"[case] {tag}")
     inp = oracle.make_inputs(B, S, Hq, Hkv, D, dtype, seed_qkv=seed, seed_do=seed + 1, mul=mul,
-                             with_dout=bwd)
+                             with_dout=bwd, transform=transform)
     qkv = to_device(inp["qkv_bits"], dtype, device)
     kvl = None if kv_len is None else torch.tensor(kv_len, dtype=torch.int32, device=device)
     o, lse = attn.gqa_fwd(qkv, B, S, Hq, Hkv, D, causal=causal, kv_len=kvl)

@@ -52,6 +52,29 @@ def test_kv_len(gpu, kv_len, causal, S, D, dtype):
     _assert_ok(run_gpu_case(gpu, 2, S, 4, 2, D, dtype=dtype, causal=causal, kv_len=kv_len))
 
 
+def _negative_scores(D):
+    """Every visible score near -20 (q = a*u + noise, k = -a*u + noise, |u| = 1): each row's
+    LSE is about -20 + log(visible keys), so exp(s - LSE) for a zero key past kv_len (s = 0)
+    is ~1e7, above the fp16 range.  Keys past kv_len must get P = dS = 0 exactly."""
+    a = np.sqrt(20.0 * np.sqrt(D))
+    def fn(q, k, v):
+        B, S = q.shape[:2]
+        u = np.full(D, 1.0 / np.sqrt(D), np.float32)
+        q = (q.reshape(B, S, -1, D) * 0.3 + a * u).reshape(B, S, -1)
+        k = (k.reshape(B, S, -1, D) * 0.3 - a * u).reshape(B, S, -1)
+        return q, k, v
+    return fn
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_kv_len_negative_scores(gpu, causal, D, dtype):
+    res = run_gpu_case(gpu, 2, 200, 4, 2, D, dtype=dtype, causal=causal, kv_len=[61, 137],
+                       transform=_negative_scores(D))
+    _assert_ok(res)
+
+
 def test_config2_fwd(gpu):
     """fp16 causal B4 H8 S1024 D64, Q/K/V scaled by 0.5, forward."""
     _assert_ok(run_gpu_case(gpu, 4, 1024, 8, 8, 64, dtype="f16", causal=True, mul=0.5, bwd=False))

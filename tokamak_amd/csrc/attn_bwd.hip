@@ -167,12 +167,12 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
                     s = mfma32<DT>(ld_lds16((const uint16_t*)(qt + off)), kf[ks], s);
                     dp = mfma32<DT>(ld_lds16((const uint16_t*)(ot + off)), vfk, dp);
                 }
-                // Branch-free causal mask: query row qr0 + hi*4 + c (c = g4*8 + i) is hidden from
-                // this lane's key iff c < tk, so the tile stays one basic block and the softmax
-                // VALU work can overlap MFMAs.  Rows past S need no mask (their Q, dO, LSE and D
-                // are zero-filled: P = 1, dS = 0, both multiplying zero rows); keys past kv_len
-                // are zeroed when dK, dV are written.
-                const int tk = causal ? key - qr0 - hi * 4 : -BM;
+                // Branch-free mask: query row qr0 + hi*4 + c (c = g4*8 + i) is hidden from this
+                // lane's key iff c < tk (causal, or every row for keys past kv_len), so the tile
+                // stays one basic block and the softmax VALU work can overlap MFMAs.  Rows past S
+                // need no mask: their Q, dO, LSE and D are zero-filled (P = 1, dS = 0, both
+                // multiplying zero rows).
+                const int tk = key >= kvl ? BM : (causal ? key - qr0 - hi * 4 : -BM);
                 u32x4 pf[PKS], sf[PKS];
                 u32x4 pl[Split<DT>::on ? PKS : 1], sl[Split<DT>::on ? PKS : 1];
 #pragma unroll
@@ -238,11 +238,7 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
     }
 
     // dK^T (scaled), dV^T: lane holds key = kw0 + l32, d = db*32 + g4*8 + hi*4 + 0..3.
-    // Keys at or past kv_len get zero gradients.
-    if (key >= kvl) {
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) dk[db] = dv[db] = f32x16{};
-    }
+    // Keys at or past kv_len had P = dS = 0 in every tile: their gradients are zero.
     if (key < S) {
         uint16_t* dkp = bd + (size_t)key * ld + (size_t)(Hq + kvh) * D;
         uint16_t* dvp = bd + (size_t)key * ld + (size_t)(Hq + Hkv + kvh) * D;
@@ -367,10 +363,11 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
                     dp[kb] = mfma32<DT>(ld_lds16((const uint16_t*)(vt + off)), of[ks], dp[kb]);
                 }
             }
-            // Branch-free causal mask: key k0 + hi*4 + c (c = kb*32 + (r/4)*8 + r%4) is hidden
-            // from this lane's query iff c > tq, so the tile stays one basic block.  Keys past
-            // kv_len need no mask: their K rows are zero-filled, so they add nothing to dQ.
-            const int tq = causal ? q - k0 - hi * 4 : BN;
+            // Branch-free mask: key k0 + hi*4 + c (c = kb*32 + (r/4)*8 + r%4) is hidden from
+            // this lane's query iff c > tq (causal, or the key is past kv_len), so the tile stays
+            // one basic block.  Masked entries get P = dS = 0 exactly: no inf * 0 from the
+            // zero-filled K and V rows past kv_len when a row's LSE is very negative.
+            const int tq = min(causal ? q - k0 - hi * 4 : BN, kvl - 1 - k0 - hi * 4);
             u32x4 sf[PKS], sl[Split<DT>::on ? PKS : 1];
 #pragma unroll
             for (int ks = 0; ks < PKS; ++ks) {
