@@ -395,8 +395,8 @@ def main():
 
     stages = [("attn_fwd", lambda: attn.gqa_fwd(qkv, B, S, Hq, Hkv, D, causal, kvl, out=o, lse=lse))]
     if backward:
-        for name, st in (("bwd_delta", attn.BWD_DELTA), ("bwd_dkdv", attn.BWD_DKDV),
-                         ("bwd_dq", attn.BWD_DQ)):
+        # tkm_attn_bwd's schedule: dQ (computing D on the way), then dK/dV.
+        for name, st in (("bwd_dq", attn.BWD_DQ_DELTA), ("bwd_dkdv", attn.BWD_DKDV)):
             stages.append((name, (lambda st=st: attn.gqa_bwd(
                 qkv, o, dout, lse, B, S, Hq, Hkv, D, causal, kvl, dqkv=dqkv, workspace=ws,
                 stage=st))))
@@ -440,7 +440,7 @@ def main():
     f_total = f_fwd * (3.5 if backward else 1.0)
     # Algorithmic FLOPs credited to each kernel (sums to F_fwd + 2.5 F_fwd):
     # dK/dV kernel: S, dP, dV, dK GEMMs = 2.0 F_fwd; dQ kernel: the dQ GEMM = 0.5 F_fwd
-    # (its S and dP recompute is not credited); the D pre-pass is HBM-bound.
+    # (its S and dP recompute, and the D = <O, dO> it computes on the way, are not credited).
     credit = {"attn_fwd": f_fwd, "bwd_dkdv": 2.0 * f_fwd, "bwd_dq": 0.5 * f_fwd}
     delta_bytes = 2.0 * B * S * Hq * D * 2 + 4.0 * B * Hq * S
     kernels = {}

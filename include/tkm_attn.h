@@ -57,9 +57,12 @@ enum {
     TKM_ATTN_ELAUNCH = -5       /* the HIP runtime rejected a kernel launch */
 };
 
-/* Backward stages, in dependency order: DELTA must complete before DKDV and DQ, which are
- * independent of each other and may run on two streams. */
-enum { TKM_ATTN_BWD_DELTA = 0, TKM_ATTN_BWD_DKDV = 1, TKM_ATTN_BWD_DQ = 2 };
+/* Backward stages.  Two valid schedules:
+ *   DELTA, then DKDV and DQ (independent of each other: they may run on two streams);
+ *   DQ_DELTA, then DKDV (one stream, one pass over O and dO fewer; what tkm_attn_bwd runs).
+ * DELTA writes D = <O, dO> per row into the workspace; DQ_DELTA computes D inside the dQ
+ * pass and writes it there; DKDV and DQ read it. */
+enum { TKM_ATTN_BWD_DELTA = 0, TKM_ATTN_BWD_DKDV = 1, TKM_ATTN_BWD_DQ = 2, TKM_ATTN_BWD_DQ_DELTA = 3 };
 
 /* Forward: O and (if lse != NULL) LSE.
  * Replaces k_gqa_flash_attn_tc_fwd + dispatch, reference src/tkm_gpu.cu:302-438, 1252-1265. */

@@ -87,7 +87,7 @@ def test_bwd_rejects():
     assert bwd(ws=ctypes.c_void_p(0x10004)) == EALIGN
     assert bwd(D=80) == EUNSUPPORTED
     assert bwd(scale=0.0) == EINVAL
-    assert bwd(stage=3) == EINVAL and b"stage" in L.tkm_attn_last_error()
+    assert bwd(stage=4) == EINVAL and b"stage" in L.tkm_attn_last_error()
     assert bwd(stage=-1) == EINVAL
 
 

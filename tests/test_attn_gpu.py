@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle
-from attn_cases import TOL_BWD, TOL_FWD, compare, from_device, log, run_gpu_case, to_device
+from attn_cases import TOL_BWD, TOL_FWD, compare, from_device, log, run_gpu_case, split_dqkv, to_device
 
 pytestmark = pytest.mark.gpu
 
@@ -87,6 +87,46 @@ def test_config3_fwdbwd(gpu):
 
 def test_config3_bf16(gpu):
     _assert_ok(run_gpu_case(gpu, 4, 2048, 16, 16, 128, dtype="bf16", causal=True, f64=False))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_stage_schedules(gpu, D, dtype):
+    """Both backward schedules: DELTA -> DKDV -> DQ and DQ_DELTA -> DKDV (tkm_attn_bwd's).
+    Each matches the oracle; their D vectors agree to fp32 rounding (the two kernels sum the
+    same products in different orders)."""
+    import torch
+    from tokamak_amd import attn
+    B, S, Hq, Hkv = 2, 300, 4, 2
+    log(f"[case] stage schedules B{B} S{S} Hq{Hq} Hkv{Hkv} D{D} {dtype}")
+    inp = oracle.make_inputs(B, S, Hq, Hkv, D, dtype, seed_qkv=11, seed_do=12)
+    qkv = to_device(inp["qkv_bits"], dtype, gpu)
+    dout = to_device(inp["dout_bits"], dtype, gpu)
+    kvl = torch.tensor([300, 211], dtype=torch.int32, device=gpu)
+    o, lse = attn.gqa_fwd(qkv, B, S, Hq, Hkv, D, causal=True, kv_len=kvl)
+    o_ref, lse_ref = oracle.fwd(inp["qkv"], B, S, Hq, Hkv, D, causal=True, kv_len=[300, 211], f64=True)
+    d_ref = oracle.bwd(inp["qkv"], oracle.round_to(o_ref, dtype)[0], inp["dout"], lse_ref, B, S, Hq, Hkv, D,
+                       causal=True, kv_len=[300, 211], f64=True)
+    res, ds = {}, {}
+    for name, stages in (("split", (attn.BWD_DELTA, attn.BWD_DKDV, attn.BWD_DQ)),
+                         ("fused", (attn.BWD_DQ_DELTA, attn.BWD_DKDV))):
+        ws = torch.zeros(attn.bwd_workspace_bytes(B, S, Hq), dtype=torch.uint8, device=gpu)
+        dqkv = torch.empty_like(qkv)
+        for st in stages:
+            attn.gqa_bwd(qkv, o, dout, lse, B, S, Hq, Hkv, D, causal=True, kv_len=kvl, dqkv=dqkv,
+                         workspace=ws, stage=st)
+        torch.cuda.synchronize()
+        res[name] = from_device(dqkv)
+        ds[name] = ws[:B * Hq * S * 4].view(torch.float32).cpu().numpy()
+        for nm, g, r in zip(("dQ", "dK", "dV"), split_dqkv(res[name], B, S, Hq, Hkv, D),
+                            split_dqkv(d_ref, B, S, Hq, Hkv, D)):
+            st = compare(nm, g, r, TOL_BWD)
+            log(f"    {name} {nm}: max_abs={st['max_abs']:.3e} bad={st['n_bad']}")
+            assert not st["n_bad"], st
+    np.testing.assert_allclose(ds["fused"], ds["split"], rtol=1e-5, atol=1e-6)
+    d_whole = attn.gqa_bwd(qkv, o, dout, lse, B, S, Hq, Hkv, D, causal=True, kv_len=kvl)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_device(d_whole), res["fused"])
 
 
 def test_deterministic(gpu):

@@ -4,8 +4,8 @@ The product is libtkm_attn.so (HIP kernels + the C ABI in include/tkm_attn.h);
 this package builds it (tokamak_amd.build) and binds it for Python callers
 (tokamak_amd.attn).
 """
-from .attn import (AttnError, BF16, BWD_DELTA, BWD_DKDV, BWD_DQ, F16, attention_flops,
+from .attn import (AttnError, BF16, BWD_DELTA, BWD_DKDV, BWD_DQ, BWD_DQ_DELTA, F16, attention_flops,
                    bwd_workspace_bytes, default_scale, gqa_bwd, gqa_fwd)
 
-__all__ = ["AttnError", "BF16", "BWD_DELTA", "BWD_DKDV", "BWD_DQ", "F16", "attention_flops",
+__all__ = ["AttnError", "BF16", "BWD_DELTA", "BWD_DKDV", "BWD_DQ", "BWD_DQ_DELTA", "F16", "attention_flops",
            "bwd_workspace_bytes", "default_scale", "gqa_bwd", "gqa_fwd"]

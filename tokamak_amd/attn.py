@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(PKG, "libtkm_attn.so")
 HEADER = os.path.join(ROOT, "include", "tkm_attn.h")
 
 F16, BF16 = 0, 1
-BWD_DELTA, BWD_DKDV, BWD_DQ = 0, 1, 2
+BWD_DELTA, BWD_DKDV, BWD_DQ, BWD_DQ_DELTA = 0, 1, 2, 3
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -174,4 +174,4 @@ def attention_flops(B, S, Hq, D, causal, kv_len=None, mode="fwd") -> float:
 
 __all__ = ["gqa_fwd", "gqa_bwd", "bwd_workspace_bytes", "attention_flops", "default_scale",
            "lib", "header_functions", "AttnError", "F16", "BF16", "BWD_DELTA", "BWD_DKDV",
-           "BWD_DQ"]
+           "BWD_DQ", "BWD_DQ_DELTA"]

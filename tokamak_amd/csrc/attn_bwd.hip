@@ -7,7 +7,9 @@
 //   P_ij = exp(s_ij - LSE_i),  dS_ij = P_ij (<dO_i, v_j> - D_i)
 //   dK_j = scale sum_i dS_ij q_i,  dV_j = sum_i P_ij dO_i   (fa_bwd_dkdv_kernel)
 //   dQ_i = scale sum_j dS_ij k_j                            (fa_bwd_dq_kernel)
-// in three launches.  dK/dV are accumulated in registers by the one workgroup that owns
+// in three launches, or two: fa_bwd_dq_kernel<WD = true> computes D for its own rows from
+// the O and dO rows it loads anyway, uses it and writes it for fa_bwd_dkdv_kernel, which
+// then runs second.  dK/dV are accumulated in registers by the one workgroup that owns
 // a key block (looping over every query block and every q-head of the kv group) and
 // written once, so the backward uses no atomics and is deterministic.  dQ is produced by
 // a separate pass that owns a query block and loops over key blocks.  All three write
@@ -263,12 +265,15 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
 // tiles go HBM -> LDS by buffer DMA, double-buffered, as in the forward.  Per tile and wave:
 //   S^T = K Q^T, dP^T = V dO^T  (lane = query row: LSE and D are per-lane scalars)
 //   dS^T = P^T (dP^T - D),  dQ^T += K^T dS^T  (K^T from transposed LDS reads)
-template <int D, int DT>
+// WD: D of the wave's rows is computed here (fp32 sum of O * dO over the lane pair that holds
+// the row) and written to delta instead of read from it.
+template <int D, int DT, bool WD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ dout,
-                      const float* __restrict__ lse, const float* __restrict__ delta,
-                      uint16_t* __restrict__ dqkv, const int32_t* __restrict__ kv_len, int B,
-                      int S, int Hq, int Hkv, float scale, float sl2, int causal, int n_qblk) {
+void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ o,
+                      const uint16_t* __restrict__ dout, const float* __restrict__ lse,
+                      float* __restrict__ delta, uint16_t* __restrict__ dqkv,
+                      const int32_t* __restrict__ kv_len, int B, int S, int Hq, int Hkv,
+                      float scale, float sl2, int causal, int n_qblk) {
     constexpr int BM = 128, BN = 64;
     constexpr int KS = D / 16, NKB = BN / 32, NDB = D / 32, PKS = BN / 16;
     constexpr int ROWB = D * 2, CPR = D / 8, TILEB = BN * ROWB;
@@ -297,6 +302,7 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
     const int q = q0 + l32;
     u32x4 qf[KS], of[KS];
     float nl2 = 0.f, Dl = 0.f;  // -LSE*log2(e) and D of this lane's query row
+    const size_t li = ((size_t)b * Hq + h) * S + q;
     if (q < S) {
         const uint16_t* qp = bqkv + (size_t)q * ld + (size_t)h * D + hi * 8;
         const uint16_t* op = dout + ((size_t)b * S + q) * ldo + (size_t)h * D + hi * 8;
@@ -305,12 +311,29 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
             qf[ks] = ld_global16(qp + ks * 16);
             of[ks] = ld_global16(op + ks * 16);
         }
-        const size_t li = ((size_t)b * Hq + h) * S + q;
         nl2 = -lse[li] * 1.4426950408889634f;
-        Dl = delta[li];
+        if constexpr (!WD) Dl = delta[li];
     } else {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) qf[ks] = of[ks] = u32x4{0u, 0u, 0u, 0u};
+    }
+    if constexpr (WD) {
+        // This lane holds head-dim elements ks*16 + hi*8 + 0..7 of dO; lane l ^ 32 the rest.
+        float acc = 0.f;
+        if (q < S) {
+            const uint16_t* orow = o + ((size_t)b * S + q) * ldo + (size_t)h * D + hi * 8;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const u32x4 x = ld_global16(orow + ks * 16);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    acc += to_f32<DT>((uint16_t)(x[w] & 0xffffu)) * to_f32<DT>((uint16_t)(of[ks][w] & 0xffffu));
+                    acc += to_f32<DT>((uint16_t)(x[w] >> 16)) * to_f32<DT>((uint16_t)(of[ks][w] >> 16));
+                }
+            }
+        }
+        Dl = acc + xor32(acc);
+        if (q < S && hi == 0) delta[li] = Dl;
     }
 
     int kv_end = kvl;
@@ -447,17 +470,21 @@ static int launch_dkdv_t(const BwdArgs& a) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-template <int D, int DT>
+template <int D, int DT, bool WD>
 static int launch_dq_t(const BwdArgs& a) {
     constexpr int BM = 128;
     const int n_qblk = (a.S + BM - 1) / BM;
     dim3 grid((unsigned)(a.B * a.Hq * n_qblk)), block(256);
-    hipLaunchKernelGGL((fa_bwd_dq_kernel<D, DT>), grid, block, 0, (hipStream_t)a.stream,
-                       (const uint16_t*)a.qkv, (const uint16_t*)a.dout, a.lse, (const float*)a.delta,
-                       (uint16_t*)a.dqkv, a.kv_len, a.B, a.S, a.Hq, a.Hkv, a.scale,
+    hipLaunchKernelGGL((fa_bwd_dq_kernel<D, DT, WD>), grid, block, 0, (hipStream_t)a.stream,
+                       (const uint16_t*)a.qkv, (const uint16_t*)a.o, (const uint16_t*)a.dout, a.lse,
+                       a.delta, (uint16_t*)a.dqkv, a.kv_len, a.B, a.S, a.Hq, a.Hkv, a.scale,
                        a.scale * 1.4426950408889634f, a.causal, n_qblk);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
+template <int D, int DT>
+static int launch_dq_read_t(const BwdArgs& a) { return launch_dq_t<D, DT, false>(a); }
+template <int D, int DT>
+static int launch_dq_write_t(const BwdArgs& a) { return launch_dq_t<D, DT, true>(a); }
 
 #define TKM_DISPATCH(FN, a)                                                                 \
     ((a).D == 128 ? ((a).dtype == DT_F16 ? FN<128, DT_F16>(a) : FN<128, DT_BF16>(a))        \
@@ -465,6 +492,7 @@ static int launch_dq_t(const BwdArgs& a) {
 
 int launch_bwd_delta(const BwdArgs& a) { return TKM_DISPATCH(launch_delta_t, a); }
 int launch_bwd_dkdv(const BwdArgs& a) { return TKM_DISPATCH(launch_dkdv_t, a); }
-int launch_bwd_dq(const BwdArgs& a) { return TKM_DISPATCH(launch_dq_t, a); }
+int launch_bwd_dq(const BwdArgs& a) { return TKM_DISPATCH(launch_dq_read_t, a); }
+int launch_bwd_dq_delta(const BwdArgs& a) { return TKM_DISPATCH(launch_dq_write_t, a); }
 
 }  // namespace tkm

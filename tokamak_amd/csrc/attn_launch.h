@@ -34,5 +34,6 @@ int launch_fwd(const FwdArgs& a);
 int launch_bwd_delta(const BwdArgs& a);
 int launch_bwd_dkdv(const BwdArgs& a);
 int launch_bwd_dq(const BwdArgs& a);
+int launch_bwd_dq_delta(const BwdArgs& a);  // dQ, and D written for launch_bwd_dkdv
 
 }  // namespace tkm

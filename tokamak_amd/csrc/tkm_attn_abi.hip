@@ -50,6 +50,7 @@ int run_bwd_stage(int stage, const tkm::BwdArgs& a) {
         case TKM_ATTN_BWD_DELTA: rc = tkm::launch_bwd_delta(a); break;
         case TKM_ATTN_BWD_DKDV: rc = tkm::launch_bwd_dkdv(a); break;
         case TKM_ATTN_BWD_DQ: rc = tkm::launch_bwd_dq(a); break;
+        case TKM_ATTN_BWD_DQ_DELTA: rc = tkm::launch_bwd_dq_delta(a); break;
         default: return fail(TKM_ATTN_EINVAL, "unknown backward stage %d", stage);
     }
     if (rc != 0) return fail(TKM_ATTN_ELAUNCH, "kernel launch failed in backward stage %d", stage);
@@ -111,7 +112,7 @@ TKM_ATTN_API int tkm_attn_bwd(const void* qkv, const void* o, const void* dout, 
     int rc = prepare_bwd(a, qkv, o, dout, lse, dqkv, kv_len, B, S, Hq, Hkv, D, scale, causal,
                          dtype, workspace, workspace_bytes, stream);
     if (rc) return rc;
-    for (int stage : {TKM_ATTN_BWD_DELTA, TKM_ATTN_BWD_DKDV, TKM_ATTN_BWD_DQ}) {
+    for (int stage : {TKM_ATTN_BWD_DQ_DELTA, TKM_ATTN_BWD_DKDV}) {
         rc = run_bwd_stage(stage, a);
         if (rc) return rc;
     }
@@ -123,7 +124,7 @@ TKM_ATTN_API int tkm_attn_bwd_stage(int stage, const void* qkv, const void* o, c
                                     int S, int Hq, int Hkv, int D, float scale, int causal,
                                     int dtype, void* workspace, size_t workspace_bytes,
                                     void* stream) {
-    if (stage < TKM_ATTN_BWD_DELTA || stage > TKM_ATTN_BWD_DQ)
+    if (stage < TKM_ATTN_BWD_DELTA || stage > TKM_ATTN_BWD_DQ_DELTA)
         return fail(TKM_ATTN_EINVAL, "unknown backward stage %d", stage);
     tkm::BwdArgs a;
     int rc = prepare_bwd(a, qkv, o, dout, lse, dqkv, kv_len, B, S, Hq, Hkv, D, scale, causal,
