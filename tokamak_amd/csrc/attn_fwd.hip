@@ -415,6 +415,8 @@ static int launch_fwd_t(const FwdArgs& a) {
 }
 
 int launch_fwd(const FwdArgs& a) {
+    const int rc = launch_fwd_asm(a);  // D = 128 fp16: hand-scheduled assembly kernel
+    if (rc != 1) return rc;
     if (a.D == 128) return a.dtype == DT_F16 ? launch_fwd_t<128, DT_F16>(a) : launch_fwd_t<128, DT_BF16>(a);
     return a.dtype == DT_F16 ? launch_fwd_t<64, DT_F16>(a) : launch_fwd_t<64, DT_BF16>(a);
 }

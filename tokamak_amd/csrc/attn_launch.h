@@ -31,6 +31,7 @@ struct BwdArgs {
 };
 
 int launch_fwd(const FwdArgs& a);
+int launch_fwd_asm(const FwdArgs& a);  // 1 = configuration not handled there
 int launch_bwd_delta(const BwdArgs& a);
 int launch_bwd_dkdv(const BwdArgs& a);
 int launch_bwd_dq(const BwdArgs& a);
