@@ -37,6 +37,7 @@ from __future__ import annotations
 
 import numpy as np
 
+from .common import Lanes, lane_basics, row_read_offsets, swz, tr_read_offsets
 from .gfx950 import (A, BRANCH, DMA, PERMLANE, Prog, S, V, VALU, ar, kernel_text, sr, vr)
 
 NAME = "tkm_fa_fwd_d128_f16"
@@ -110,66 +111,6 @@ A_Q = 128               # q[qb][ks] at 128 + (qb*8+ks)*4
 
 def sblk(J, kb, qb):
     return V_SET[J] + (kb * 2 + qb) * 16
-
-
-def swz(r):
-    return ((r & 3) << 2) | ((r >> 2) & 3)
-
-
-class Lanes:
-    """Emits integer VALU ops on per-lane values and evaluates them over 4 waves x 64 lanes
-    (numpy int64 arrays of 256 entries), so the prologue address arithmetic can be checked."""
-
-    def __init__(self, p: Prog, ldb: int):
-        self.p = p
-        self.val = {}
-        tid = np.arange(256, dtype=np.int64)
-        self.val[0] = tid  # v0 = workitem id
-        self.wave = tid >> 6
-        self.ldb = ldb
-
-    def _set(self, d, x):
-        self.val[d] = np.asarray(x, dtype=np.int64) & 0xFFFFFFFF
-
-    def op2(self, mnem, d, a, b, fn):
-        """d = fn(a, b); a, b are VGPR indices or ('k', const) / ('s', sgpr, value)."""
-        def txt(x):
-            if isinstance(x, int):
-                return vr(x)
-            if x[0] == "k":
-                return str(x[1])
-            return sr(x[1])
-
-        def v(x):
-            if isinstance(x, int):
-                return self.val[x]
-            if x[0] == "k":
-                return np.full(256, x[1], dtype=np.int64)
-            return x[2]  # per-wave scalar values (array of 256)
-
-        reads = []
-        for x in (a, b):
-            if isinstance(x, int):
-                reads += V(x)
-            elif x[0] == "s":
-                reads += S(x[1])
-        self.p.valu(f"{mnem} {vr(d)}, {txt(a)}, {txt(b)}", reads, V(d))
-        self._set(d, fn(v(a), v(b)))
-
-    def and_(self, d, a, b): self.op2("v_and_b32", d, a, b, lambda x, y: x & y)
-    def or_(self, d, a, b): self.op2("v_or_b32", d, a, b, lambda x, y: x | y)
-    def xor(self, d, a, b): self.op2("v_xor_b32", d, a, b, lambda x, y: x ^ y)
-    def add(self, d, a, b): self.op2("v_add_u32", d, a, b, lambda x, y: x + y)
-    def shr(self, d, sh, a): self.op2("v_lshrrev_b32", d, sh, a, lambda s_, x: x >> s_)
-    def shl(self, d, sh, a): self.op2("v_lshlrev_b32", d, sh, a, lambda s_, x: x << s_)
-    def mul(self, d, a, b): self.op2("v_mul_lo_u32", d, a, b, lambda x, y: x * y)
-
-    def k(self, c):
-        return ("k", c)
-
-    def s(self, sgpr, per_wave):
-        """An SGPR operand whose value is per_wave[wave]."""
-        return ("s", sgpr, np.asarray(per_wave, dtype=np.int64)[self.wave])
 
 
 def build(check_ldb: int = 12288) -> str:
@@ -255,9 +196,7 @@ def build(check_ldb: int = 12288) -> str:
 
     # ------------------------------------------------------------------ prologue: lane values
     LANE, L32, HI, DR, DP, TA, TB, TC = (V_PT + i for i in range(1, 9))
-    L.and_(LANE, L.k(63), 0)
-    L.and_(L32, L.k(31), 0)
-    L.shr(HI, L.k(5), LANE)
+    lane_basics(L, (LANE, L32, HI))
     L.shr(DR, L.k(4), LANE)
     L.and_(DP, L.k(15), LANE)
     ldb_per_wave = np.full(4, check_ldb)
@@ -274,45 +213,8 @@ def build(check_ldb: int = 12288) -> str:
         L.xor(TC, TC, DP)
         L.shl(TC, L.k(4), TC)
         L.add(V_DOFF + i, TB, TC)
-    # K operand offsets: l32*256 + ((2ks+hi) ^ swz(l32)) << 4
-    L.and_(TA, L.k(3), L32)
-    L.shl(TA, L.k(2), TA)
-    L.shr(TB, L.k(2), L32)
-    L.and_(TB, L.k(3), TB)
-    L.or_(TA, TA, TB)                               # swz(l32)
-    L.shl(TB, L.k(8), L32)                          # l32*256
-    for ks in range(8):
-        L.add(TC, HI, L.k(2 * ks))
-        L.xor(TC, TC, TA)
-        L.shl(TC, L.k(4), TC)
-        L.add(V_KOFF + ks, TC, TB)
-    # V^T offsets: trow = (lane&15)>>2, c1 = ((lane>>4)&1)*2 + ((lane&3)>>1), e = (lane&1)*8
-    #   row = tt*8 + hi*4 + trow; off = row*256 + (((4db + c1) ^ (4trow + 2tt + hi)) << 4) + e
-    TROW, C1, E, RB = V_PT + 9, V_PT + 10, V_PT + 11, V_PT + 12
-    L.and_(TROW, L.k(15), LANE)
-    L.shr(TROW, L.k(2), TROW)
-    L.shr(C1, L.k(4), LANE)
-    L.and_(C1, L.k(1), C1)
-    L.shl(C1, L.k(1), C1)
-    L.and_(TC, L.k(3), LANE)
-    L.shr(TC, L.k(1), TC)
-    L.or_(C1, C1, TC)
-    L.and_(E, L.k(1), LANE)
-    L.shl(E, L.k(3), E)
-    L.shl(TA, L.k(2), HI)
-    L.add(RB, TA, TROW)                             # hi*4 + trow
-    L.shl(TB, L.k(2), TROW)
-    L.add(TB, TB, HI)                               # 4trow + hi
-    for tt in range(2):
-        for db in range(4):
-            L.add(TC, C1, L.k(4 * db))
-            L.add(TA, TB, L.k(2 * tt))
-            L.xor(TC, TC, TA)
-            L.shl(TC, L.k(4), TC)
-            L.add(TC, TC, E)
-            L.add(TA, RB, L.k(8 * tt))
-            L.shl(TA, L.k(8), TA)
-            L.add(V_VOFF + tt * 4 + db, TC, TA)
+    row_read_offsets(L, V_KOFF, (LANE, L32, HI), (TA, TB, TC))
+    tr_read_offsets(L, V_VOFF, (LANE, L32, HI), (TA, TB, TC, V_PT + 9, V_PT + 10, V_PT + 11, V_PT + 12))
     _check_lanes(L, check_ldb)
     return _rest(p, L, (LANE, L32, HI))
 
@@ -321,28 +223,12 @@ def _check_lanes(L: Lanes, ldb: int):
     tid = np.arange(256)
     lane = tid & 63
     wave = tid >> 6
-    l32 = lane & 31
-    hi = lane >> 5
     CPR, RPI, NI = 16, 4, 4
     dma_r, dma_p = lane // CPR, lane % CPR
     for i in range(4):
         row = (wave * NI + i) * RPI + dma_r
         ref = row * ldb + ((dma_p ^ np.vectorize(swz)(row)) << 4)
         assert np.array_equal(L.val[V_DOFF + i], ref & 0xFFFFFFFF), f"dma offset {i}"
-    fk = np.vectorize(swz)(l32)
-    for ks in range(8):
-        ref = l32 * ROWB + (((ks * 2 + hi) ^ fk) << 4)
-        assert np.array_equal(L.val[V_KOFF + ks], ref), f"koff {ks}"
-    trow = (lane & 15) >> 2
-    tcol = ((lane >> 4) & 1) * 16 + (lane & 3) * 4
-    for tt in range(2):
-        row = tt * 8 + hi * 4 + trow
-        for db in range(4):
-            d = db * 32 + tcol
-            ref = row * ROWB + (((d >> 3) ^ np.vectorize(swz)(row)) << 4) + (d & 7) * 2
-            assert np.array_equal(L.val[V_VOFF + tt * 4 + db], ref), f"voff {tt} {db}"
-
-
 
 
 class Body:
