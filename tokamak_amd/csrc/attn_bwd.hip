@@ -491,7 +491,10 @@ static int launch_dq_write_t(const BwdArgs& a) { return launch_dq_t<D, DT, true>
                   : ((a).dtype == DT_F16 ? FN<64, DT_F16>(a) : FN<64, DT_BF16>(a)))
 
 int launch_bwd_delta(const BwdArgs& a) { return TKM_DISPATCH(launch_delta_t, a); }
-int launch_bwd_dkdv(const BwdArgs& a) { return TKM_DISPATCH(launch_dkdv_t, a); }
+int launch_bwd_dkdv(const BwdArgs& a) {
+    const int r = launch_bwd_dkdv_asm(a);
+    return r != 1 ? r : TKM_DISPATCH(launch_dkdv_t, a);
+}
 int launch_bwd_dq(const BwdArgs& a) { return TKM_DISPATCH(launch_dq_read_t, a); }
 int launch_bwd_dq_delta(const BwdArgs& a) { return TKM_DISPATCH(launch_dq_write_t, a); }
 
