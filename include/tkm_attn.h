@@ -61,7 +61,8 @@ enum {
  *   DELTA, then DKDV and DQ (independent of each other: they may run on two streams);
  *   DQ_DELTA, then DKDV (one stream, one pass over O and dO fewer; what tkm_attn_bwd runs).
  * DELTA writes D = <O, dO> per row into the workspace; DQ_DELTA computes D inside the dQ
- * pass and writes it there; DKDV and DQ read it. */
+ * pass and writes it there; DKDV and DQ read it.  Both also write the row pairs
+ * (-LSE*log2(e), -D) that DKDV reads. */
 enum { TKM_ATTN_BWD_DELTA = 0, TKM_ATTN_BWD_DKDV = 1, TKM_ATTN_BWD_DQ = 2, TKM_ATTN_BWD_DQ_DELTA = 3 };
 
 /* Forward: O and (if lse != NULL) LSE.
@@ -70,7 +71,8 @@ TKM_ATTN_API int tkm_attn_fwd(const void *qkv, void *o, float *lse, const int32_
                               int B, int S, int Hq, int Hkv, int D, float scale, int causal,
                               int dtype, void *stream);
 
-/* Bytes of device workspace tkm_attn_bwd needs (the per-row D = <O, dO> vector).
+/* Bytes of device workspace tkm_attn_bwd needs: the per-row D = <O, dO> vector, and the same
+ * rows' (-LSE*log2(e), -D) pairs, padded to 32 rows per (batch, head), for the dK/dV pass.
  * Replaces the per-node save buffer sizing of init_node_resources, src/tkm_gpu.cu:1000-1001. */
 TKM_ATTN_API size_t tkm_attn_bwd_workspace_bytes(int B, int S, int Hq);
 

@@ -31,7 +31,13 @@ the code correct for the hardware without changing the order:
   (A wait state is one issued instruction; ``s_nop N`` counts N+1.)
 * before every branch, outstanding LDS reads and VMEM loads into registers are waited for
   and the MFMA/transcendental hazards are settled, so a jump target needs no state from
-  the jump source.
+  the jump source.  Two exceptions, both the caller's promise about every path into a
+  target: ``branch(..., keep_lgkm=True)`` leaves LDS reads in flight, and every target then
+  starts with ``assume_lgkm`` naming exactly those reads (oldest first); ``skip_xdl``
+  names MFMA destinations left unpadded because every target only accumulates into them
+  with MFMAs (no wait states needed) or pads for them itself.
+* v_mov_b32_dpp and v_permlane* are PERMLANE-class: they read a VGPR a VALU wrote no
+  earlier than 2 wait states before.
 
 Nothing here writes through the scalar data cache: the builder has no scalar store.
 """
@@ -40,7 +46,7 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 
 XDL, VALU, TRANS, SALU, DS_READ, DS_WRITE, VMEM_LOAD, VMEM_STORE, DMA, SMEM, NOP, WAIT, BRANCH, \
-    LABEL, BARRIER, PERMLANE, READLANE = range(17)
+    LABEL, BARRIER, PERMLANE, READLANE, ASSUME = range(18)
 
 # hazard wait states (see module docstring)
 W_XDL_RAW = 12
@@ -90,11 +96,18 @@ class Ins:
     ab: list = field(default_factory=list)
     c: list = field(default_factory=list)
     dst: list = field(default_factory=list)
+    # BRANCH: leave LDS reads in flight / MFMA destinations not to pad; ASSUME: reads in flight
+    keep_lgkm: bool = False
+    skip_xdl: object = None
+    pending: list = field(default_factory=list)
 
 
 class Prog:
-    def __init__(self):
+    def __init__(self, coalesce_lgkm: bool = False):
+        """coalesce_lgkm: an LDS wait in front of an MFMA also covers the reads the next MFMA
+        needs that are already in flight (one wait per two MFMAs instead of one each)."""
         self.ins: list[Ins] = []
+        self.coalesce_lgkm = coalesce_lgkm
 
     # ---- raw emission -------------------------------------------------------------------
     def emit(self, text, kind, reads=(), writes=(), **kw):
@@ -165,8 +178,16 @@ class Prog:
     def barrier(self):
         self.emit("s_barrier", BARRIER)
 
-    def branch(self, text, reads=()):
-        self.emit(text, BRANCH, reads)
+    def branch(self, text, reads=(), keep_lgkm=False, skip_xdl=None):
+        self.emit(text, BRANCH, reads, keep_lgkm=keep_lgkm, skip_xdl=skip_xdl)
+
+    def assume_lgkm(self, pending):
+        """At a branch target: the LDS reads in flight on every path into it (register lists,
+        oldest first)."""
+        self.emit("", ASSUME, pending=[set(d) for d in pending])
+
+    def permlane(self, text, reads=(), writes=()):
+        self.emit(text, PERMLANE, reads, writes)
 
     def nop(self, n):
         while n > 0:
@@ -201,18 +222,22 @@ class Prog:
                 put(f"\ts_nop {k - 1}", k)
                 need -= k
 
-        def settle_all():
+        def settle_all(keep_lgkm=False, skip_xdl=None):
             # wait for every register-writing memory op, pad every pending hazard
-            if lgkm:
+            if lgkm and not keep_lgkm:
                 put("\ts_waitcnt lgkmcnt(0)")
                 lgkm.clear()
             if any(d for d in vm):
                 put("\ts_waitcnt vmcnt(0)")
                 vm.clear()
             need = 0
-            for t in last_xdl_w.values():
+            for r, t in last_xdl_w.items():
+                if skip_xdl is not None and r in skip_xdl:
+                    continue
                 need = max(need, t[0] + W_XDL_RAW - ws)
-            for t in last_xdl_rc.values():
+            for r, t in last_xdl_rc.items():
+                if skip_xdl is not None and r in skip_xdl:
+                    continue
                 need = max(need, t + W_XDL_WAR_C - ws)
             for t in last_trans_w.values():
                 need = max(need, t + W_TRANS - ws)
@@ -220,14 +245,17 @@ class Prog:
                 need = max(need, t + W_VALU_SGPR - ws)
             pad(need)
 
-        for ins in self.ins:
+        for pos, ins in enumerate(self.ins):
             k = ins.kind
             if k == LABEL:
                 out.append(ins.text if not ins.text.startswith(";") else "\t" + ins.text)
                 continue
             if k == BRANCH:
-                settle_all()
+                settle_all(ins.keep_lgkm, ins.skip_xdl)
                 put("\t" + ins.text)
+                continue
+            if k == ASSUME:
+                lgkm[:] = [set(d) for d in ins.pending]
                 continue
             regs_r = set(ins.reads)
             regs_w = set(ins.writes)
@@ -238,6 +266,16 @@ class Prog:
                 for i, d in enumerate(lgkm):
                     if d & touched:
                         idx = i
+                if idx >= 0 and k == XDL and self.coalesce_lgkm:
+                    for nxt in self.ins[pos + 1:]:
+                        if nxt.kind in (BRANCH, LABEL, ASSUME, BARRIER):
+                            break
+                        if nxt.kind == XDL:
+                            nt = set(nxt.reads) | set(nxt.writes)
+                            for i, d in enumerate(lgkm):
+                                if d & nt:
+                                    idx = max(idx, i)
+                            break
                 if idx >= 0:
                     put(f"\ts_waitcnt lgkmcnt({len(lgkm) - 1 - idx})")
                     del lgkm[:idx + 1]

@@ -25,13 +25,27 @@ namespace tkm {
 template <int D, int DT>
 __global__ __launch_bounds__(256) void fa_bwd_delta_kernel(const uint16_t* __restrict__ o,
                                                            const uint16_t* __restrict__ dout,
-                                                           float* __restrict__ delta, int B, int S,
-                                                           int Hq) {
+                                                           const float* __restrict__ lse,
+                                                           float* __restrict__ delta,
+                                                           float* __restrict__ quads, int B,
+                                                           int S, int Hq) {
     constexpr int DC = D / 8;
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
     const size_t total = (size_t)B * S * Hq * DC;
+    const int SP = (S + 31) & ~31;
+    if (idx >= total) {  // threads past the rows zero the padding rows S..SP-1 of every head
+        const size_t p = idx - total, npad = (size_t)B * Hq * (SP - S);
+        if (p < npad) {
+            const size_t bh = p / (SP - S);
+            const int i = S + (int)(p % (SP - S));
+            float* qd = quads + bh * SP * 2 + (i >> 1) * 4 + (i & 1);
+            qd[0] = 0.f;
+            qd[2] = 0.f;
+        }
+        return;
+    }
     float acc = 0.f;
-    if (idx < total) {
+    {
         const u32x4 x = ld_global16(o + idx * 8), y = ld_global16(dout + idx * 8);
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -41,12 +55,16 @@ __global__ __launch_bounds__(256) void fa_bwd_delta_kernel(const uint16_t* __res
     }
 #pragma unroll
     for (int off = DC / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (idx < total && (idx % DC) == 0) {
+    if ((idx % DC) == 0) {
         const size_t rh = idx / DC;  // (b*S + i)*Hq + h
         const int h = (int)(rh % Hq);
         const size_t row = rh / Hq;
         const int i = (int)(row % S), b = (int)(row / S);
-        delta[((size_t)b * Hq + h) * S + i] = acc;
+        const size_t li = ((size_t)b * Hq + h) * S + i;
+        delta[li] = acc;
+        float* qd = quads + ((size_t)b * Hq + h) * SP * 2 + (i >> 1) * 4 + (i & 1);
+        qd[0] = -lse[li] * 1.4426950408889634f;
+        qd[2] = -acc;
     }
 }
 
@@ -271,7 +289,8 @@ template <int D, int DT, bool WD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ o,
                       const uint16_t* __restrict__ dout, const float* __restrict__ lse,
-                      float* __restrict__ delta, uint16_t* __restrict__ dqkv,
+                      float* __restrict__ delta, float* __restrict__ quads,
+                      uint16_t* __restrict__ dqkv,
                       const int32_t* __restrict__ kv_len, int B, int S, int Hq, int Hkv,
                       float scale, float sl2, int causal, int n_qblk) {
     constexpr int BM = 128, BN = 64;
@@ -334,6 +353,12 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
         }
         Dl = acc + xor32(acc);
         if (q < S && hi == 0) delta[li] = Dl;
+        const int SP = (S + 31) & ~31;
+        if (q < SP && hi == 0) {  // rows S..SP-1: zeros (nl2 = Dl = 0 there)
+            float* qd = quads + ((size_t)b * Hq + h) * SP * 2 + (q >> 1) * 4 + (q & 1);
+            qd[0] = nl2;
+            qd[2] = -Dl;
+        }
     }
 
     int kv_end = kvl;
@@ -451,10 +476,12 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
 // ---------------------------------------------------------------- launchers
 template <int D, int DT>
 static int launch_delta_t(const BwdArgs& a) {
-    const size_t total = (size_t)a.B * a.S * a.Hq * (D / 8);
+    const size_t total = (size_t)a.B * a.S * a.Hq * (D / 8) +
+                         (size_t)a.B * a.Hq * (((a.S + 31) & ~31) - a.S);  // + padding rows
     dim3 grid((unsigned)((total + 255) / 256)), block(256);
     hipLaunchKernelGGL((fa_bwd_delta_kernel<D, DT>), grid, block, 0, (hipStream_t)a.stream,
-                       (const uint16_t*)a.o, (const uint16_t*)a.dout, a.delta, a.B, a.S, a.Hq);
+                       (const uint16_t*)a.o, (const uint16_t*)a.dout, a.lse, a.delta, a.ld,
+                       a.B, a.S, a.Hq);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -477,7 +504,7 @@ static int launch_dq_t(const BwdArgs& a) {
     dim3 grid((unsigned)(a.B * a.Hq * n_qblk)), block(256);
     hipLaunchKernelGGL((fa_bwd_dq_kernel<D, DT, WD>), grid, block, 0, (hipStream_t)a.stream,
                        (const uint16_t*)a.qkv, (const uint16_t*)a.o, (const uint16_t*)a.dout, a.lse,
-                       a.delta, (uint16_t*)a.dqkv, a.kv_len, a.B, a.S, a.Hq, a.Hkv, a.scale,
+                       a.delta, a.ld, (uint16_t*)a.dqkv, a.kv_len, a.B, a.S, a.Hq, a.Hkv, a.scale,
                        a.scale * 1.4426950408889634f, a.causal, n_qblk);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -23,7 +23,9 @@ struct BwdArgs {
     const float* lse;
     void* dqkv;
     const int32_t* kv_len;
-    float* delta;  // workspace: B*Hq*S floats
+    float* delta;  // workspace: D per row, B*Hq*S floats
+    float* ld;     // workspace: per (b, h) and row pair m, m+1 (rows padded to 32):
+                   // -LSE*log2(e) of m, m+1, then -D of m, m+1
     int B, S, Hq, Hkv, D;
     float scale;
     int causal, dtype;

@@ -24,6 +24,13 @@ int fail(int status, const char* fmt, ...) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// Backward workspace: D per row (B*Hq*S floats), then at this 256-byte aligned offset the
+// per-row pairs (-LSE*log2(e), -D), B*Hq rows each padded to a multiple of 32.
+size_t tkm_ws_pairs_offset(int B, int S, int Hq) {
+    const size_t n = (size_t)B * Hq * S * sizeof(float);
+    return (n + 255) & ~(size_t)255;
+}
+
 // Shape checks shared by forward and backward (reference rules: tkm_core.c:392-404).
 int check_shape(int B, int S, int Hq, int Hkv, int D, int causal, int dtype) {
     if (B < 1 || S < 1 || Hq < 1 || Hkv < 1)
@@ -75,6 +82,7 @@ int prepare_bwd(tkm::BwdArgs& a, const void* qkv, const void* o, const void* dou
     if (!aligned(workspace, 16)) return fail(TKM_ATTN_EALIGN, "workspace must be 16-byte aligned");
     if (!(scale > 0.f) || scale == INFINITY) return fail(TKM_ATTN_EINVAL, "scale must be positive and finite");
     a = tkm::BwdArgs{qkv, o, dout, lse, dqkv, kv_len, (float*)workspace,
+                     (float*)((char*)workspace + tkm_ws_pairs_offset(B, S, Hq)),
                      B, S, Hq, Hkv, D, scale, causal, dtype, stream};
     return TKM_ATTN_OK;
 }
@@ -100,8 +108,7 @@ TKM_ATTN_API int tkm_attn_fwd(const void* qkv, void* o, float* lse, const int32_
 
 TKM_ATTN_API size_t tkm_attn_bwd_workspace_bytes(int B, int S, int Hq) {
     if (B < 1 || S < 1 || Hq < 1) return 0;
-    const size_t n = (size_t)B * Hq * S * sizeof(float);
-    return (n + 255) & ~(size_t)255;
+    return tkm_ws_pairs_offset(B, S, Hq) + (size_t)B * Hq * (((size_t)S + 31) & ~(size_t)31) * 8;
 }
 
 TKM_ATTN_API int tkm_attn_bwd(const void* qkv, const void* o, const void* dout, const float* lse,
