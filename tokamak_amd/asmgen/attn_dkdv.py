@@ -49,7 +49,10 @@ TILE = 32 * ROWB                    # 8 KB: one 32-row tile of Q or dO
 BUFB = 2 * TILE                     # Q then dO
 LDS_LD = NBUF * BUFB                # row quads: per buffer 4 waves x 256 B
 LDB = 1024
-LDS_BYTES = LDS_LD + NBUF * LDB
+LDS_EPI = LDS_LD + NBUF * LDB       # per wave: 32 key rows of 272 B staging dK, dV for the store
+EPI_ROW = 272                       # 256 B + 16 B pad: rows 16 B apart in the banks
+EPI_WAVE = 32 * EPI_ROW
+LDS_BYTES = LDS_EPI + 4 * EPI_WAVE
 LK = 4                              # slots between a row read and its MFMA
 LV = 4                              # slots between a transposed read pair and its MFMA
 NRB = 6                             # row-read registers in rotation (x4)
@@ -57,25 +60,29 @@ NTB = 6                             # transposed-read registers in rotation (x4)
 EW_SPLIT = False                    # elementwise pairs 4..7 in the dV/dK half (measured slower)
 
 ARGS = [(0, 8, "ptr"), (8, 8, "ptr"), (16, 8, "ptr"), (24, 8, "ptr"), (32, 8, "ptr")] + \
-       [(40 + 4 * i, 4, "val") for i in range(14)]
-KERNARG_BYTES = 96
+       [(40 + 4 * i, 4, "val") for i in range(16)]
+KERNARG_BYTES = 104
 
 # ---- SGPRs
-S_H, S_B, S_Z = 2, 3, 4                 # kv head, batch, key block
+S_WG = 2                               # workgroup index (one-dimensional grid)
+S_KA, S_KD = 3, 4                      # round of the current item / of the DMA stream's item
 S_QKV, S_DOUT, S_PAIRS, S_DQKV, S_KVLEN = 8, 10, 12, 14, 16
 S_SEQ, S_HQ, S_HKV, S_SL2, S_CAUSAL, S_LDB = 18, 19, 20, 21, 22, 23
-S_LDO, S_G, S_SCALE, S_NKBLK, S_SP = 24, 25, 26, 27, 28
+S_LDO, S_G, S_SCALE, S_NKBLK, S_SP, S_NWG, S_NI, S_BH = 24, 25, 26, 27, 28, 29, 30, 31
 S_TQ, S_TO, S_TL = 5, 6, 7             # offsets of the requested tile (Q, dO, row quads)
-S_LDB32, S_LDO32 = 29, 30              # 32 rows of qkv / dO in bytes
+S_LDB32, S_LDO32 = 88, 89              # 32 rows of qkv / dO in bytes
+S_MAGBH, S_MAGHKV = 90, 91             # ceil(2^32 / (B*Hkv)), ceil(2^32 / Hkv) (0 for 1)
+S_BA, S_KVHA, S_ITERSD, S_QTBD = 92, 93, 94, 95   # current item's batch, kv head; DMA item's tiles
 S_WAVE, S_KVL, S_KB0, S_KW0, S_QTB, S_QTE, S_ITERS, S_IT = 32, 33, 34, 35, 36, 37, 38, 39
-S_BQKV, S_BDO, S_BLD = 40, 42, 44      # 64-bit bases (batch, first q-head of the group)
+S_BQKV, S_BDO, S_BLD = 40, 42, 44      # 64-bit bases of the DMA stream's item
 S_CODE, S_KWACT = 46, 47               # variant of the current body; wave has a key < kv_len
-S_RQ, S_RO, S_RL = 48, 52, 56          # DMA descriptors (batch + group base, fixed)
+S_RQ, S_RO, S_RL = 48, 52, 56          # DMA descriptors of the DMA stream's item
 S_QT0, S_QT1, S_QT3, S_H3 = 60, 61, 62, 63
 S_LDSW, S_LDSL, S_KWMASK = 64, 65, 66  # DMA offsets; 1 if a key of the wave is >= kv_len
+S_ITD = 67                             # tiles of the DMA stream's item already requested
 S_KWEFF, S_KWDIAG = 68, 69             # causal ? kw0 : 0;  causal ? kw0 : -1
 S_TMP = 70                             # s70..s87
-NEXT_FREE_SGPR = 88
+NEXT_FREE_SGPR = 96
 
 # ---- VGPRs
 V_SD = (0, 32)          # set J: S at +0..15, dP at +16..31
@@ -325,11 +332,12 @@ class Body:
         s(f"s_cmp_ge_u32 {sr(qt)}, {sr(S_QTE)}", S(qt) + S(S_QTE), [("scc", 0)])
         s(f"s_cselect_b32 {sr(qt)}, {sr(S_QTB)}, {sr(qt)}", S(S_QTB) + S(qt) + [("scc", 0)], S(qt))
 
-    def advance_h(self, h, qt):
+    def advance_h(self, h, qt, qtb=S_QTBD):
+        """(h, qt) := (h, qt + 1), or (h + 1, qtb) past the last query tile."""
         s = self.s
         s(f"s_add_u32 {sr(qt)}, {sr(qt)}, 1", S(qt), S(qt))
         s(f"s_cmp_ge_u32 {sr(qt)}, {sr(S_QTE)}", S(qt) + S(S_QTE), [("scc", 0)])
-        s(f"s_cselect_b32 {sr(qt)}, {sr(S_QTB)}, {sr(qt)}", S(S_QTB) + S(qt) + [("scc", 0)], S(qt))
+        s(f"s_cselect_b32 {sr(qt)}, {sr(qtb)}, {sr(qt)}", S(qtb) + S(qt) + [("scc", 0)], S(qt))
         s(f"s_addc_u32 {sr(h)}, {sr(h)}, 0", S(h) + [("scc", 0)], S(h))
 
     def code(self):
@@ -350,11 +358,287 @@ class Body:
         s(f"s_cselect_b32 {sr(S_CODE)}, 8, {sr(S_CODE)}", S(S_CODE) + [("scc", 0)], S(S_CODE))
 
     def advance_and_code(self):
-        self.s(f"s_mov_b32 {sr(S_QT0)}, {sr(S_QT1)}", S(S_QT1), S(S_QT0))
+        """Next body's tiles: this item's next query tile, the DMA stream's next tile (bit 16 of
+        the code when that starts a new item); the next body's variant."""
+        s = self.s
+        s(f"s_mov_b32 {sr(S_QT0)}, {sr(S_QT1)}", S(S_QT1), S(S_QT0))
         self.advance_qt(S_QT1)
         self.advance_h(S_H3, S_QT3)
-        self.s(f"s_add_u32 {sr(S_IT)}, {sr(S_IT)}, 1", S(S_IT), S(S_IT))
+        s(f"s_add_u32 {sr(S_ITD)}, {sr(S_ITD)}, 1", S(S_ITD), S(S_ITD))
+        s(f"s_add_u32 {sr(S_IT)}, {sr(S_IT)}, 1", S(S_IT), S(S_IT))
         self.code()
+        T = S_TMP + 17
+        s(f"s_cmp_ge_u32 {sr(S_ITD)}, {sr(S_ITERSD)}", S(S_ITD) + S(S_ITERSD), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(T)}, 16, 0", [("scc", 0)], S(T))
+        s(f"s_or_b32 {sr(S_CODE)}, {sr(S_CODE)}, {sr(T)}", S(S_CODE) + S(T), S(S_CODE))
+
+    # ---------------------------------------------------------------- items
+    # A workgroup walks items i = z*(B*Hkv) + b*Hkv + kvh (z = key block, heaviest first for
+    # causal) in rounds of NWG: round k takes item k*NWG + wg, or k*NWG + NWG-1-wg for odd k,
+    # so the long and short items of consecutive rounds pair up.  An item has
+    # g*(QTE - QTB) query tiles, or one tile that no wave uses when its keys all lie past
+    # kv_len.  Two roles follow the item sequence: the current item (tile it: its keys, masks,
+    # accumulators) and the DMA stream (tile it+3), which runs ahead across item boundaries.
+    def item_index(self, k_sgpr, dst):
+        s, T = self.s, S_TMP + 12
+        s(f"s_mul_i32 {sr(dst)}, {sr(k_sgpr)}, {sr(S_NWG)}", S(k_sgpr) + S(S_NWG), S(dst))
+        s(f"s_sub_u32 {sr(T)}, {sr(S_NWG)}, 1", S(S_NWG), S(T))
+        s(f"s_sub_u32 {sr(T)}, {sr(T)}, {sr(S_WG)}", S(T) + S(S_WG), S(T))
+        s(f"s_bitcmp1_b32 {sr(k_sgpr)}, 0", S(k_sgpr), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(T)}, {sr(T)}, {sr(S_WG)}", S(T) + S(S_WG) + [("scc", 0)], S(T))
+        s(f"s_add_u32 {sr(dst)}, {sr(dst)}, {sr(T)}", S(dst) + S(T), S(dst))
+
+    def decode(self, i, z, b, kvh):
+        """z = i / (B*Hkv), b = (i % (B*Hkv)) / Hkv, kvh = i % Hkv (multiply-high by the host's
+        reciprocals, checked exact on the host for every index that occurs)."""
+        s, R = self.s, S_TMP + 13
+        s(f"s_mul_hi_u32 {sr(z)}, {sr(i)}, {sr(S_MAGBH)}", S(i) + S(S_MAGBH), S(z))
+        s(f"s_cmp_eq_u32 {sr(S_BH)}, 1", S(S_BH), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(z)}, {sr(i)}, {sr(z)}", S(i) + S(z) + [("scc", 0)], S(z))
+        s(f"s_mul_i32 {sr(R)}, {sr(z)}, {sr(S_BH)}", S(z) + S(S_BH), S(R))
+        s(f"s_sub_u32 {sr(R)}, {sr(i)}, {sr(R)}", S(i) + S(R), S(R))
+        s(f"s_mul_hi_u32 {sr(b)}, {sr(R)}, {sr(S_MAGHKV)}", S(R) + S(S_MAGHKV), S(b))
+        s(f"s_cmp_eq_u32 {sr(S_HKV)}, 1", S(S_HKV), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(b)}, {sr(R)}, {sr(b)}", S(R) + S(b) + [("scc", 0)], S(b))
+        s(f"s_mul_i32 {sr(kvh)}, {sr(b)}, {sr(S_HKV)}", S(b) + S(S_HKV), S(kvh))
+        s(f"s_sub_u32 {sr(kvh)}, {sr(R)}, {sr(kvh)}", S(R) + S(kvh), S(kvh))
+
+    def kvl_of(self, b, dst, label):
+        """dst = clamp(kv_len[b], 0, S), or S without kv_len.  No LDS read may be in flight."""
+        p, s, T = self.p, self.s, S_TMP + 12
+        s(f"s_mov_b32 {sr(dst)}, {sr(S_SEQ)}", S(S_SEQ), S(dst))
+        s(f"s_cmp_eq_u64 {sr(S_KVLEN, 2)}, 0", S(S_KVLEN, 2), [("scc", 0)])
+        p.branch(f"s_cbranch_scc1 {label}", [("scc", 0)], skip_xdl=ACC)
+        s(f"s_lshl_b32 {sr(T)}, {sr(b)}, 2", S(b), S(T))
+        p.smem(f"s_load_dword {sr(dst)}, {sr(S_KVLEN, 2)}, {sr(T)}", S(dst), S(S_KVLEN, 2) + S(T))
+        p.waitcnt(lgkm=0)
+        s(f"s_max_i32 {sr(dst)}, {sr(dst)}, 0", S(dst), S(dst))
+        s(f"s_min_i32 {sr(dst)}, {sr(dst)}, {sr(S_SEQ)}", S(dst) + S(S_SEQ), S(dst))
+        p.label(label)
+
+    def tiles_of(self, kb0, kvl, qtb, iters):
+        """qtb = causal ? kb0/32 : 0; iters = kb0 >= kvl ? 1 : g*(QTE - qtb)."""
+        s = self.s
+        s(f"s_lshr_b32 {sr(qtb)}, {sr(kb0)}, 5", S(kb0), S(qtb))
+        s(f"s_cmp_eq_u32 {sr(S_CAUSAL)}, 0", S(S_CAUSAL), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(qtb)}, 0, {sr(qtb)}", S(qtb) + [("scc", 0)], S(qtb))
+        s(f"s_sub_u32 {sr(iters)}, {sr(S_QTE)}, {sr(qtb)}", S(S_QTE) + S(qtb), S(iters))
+        s(f"s_mul_i32 {sr(iters)}, {sr(iters)}, {sr(S_G)}", S(iters) + S(S_G), S(iters))
+        s(f"s_cmp_ge_u32 {sr(kb0)}, {sr(kvl)}", S(kb0) + S(kvl), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(iters)}, 1, {sr(iters)}", S(iters) + [("scc", 0)], S(iters))
+
+    def decode_d(self, sfx):
+        """DMA stream: item of round S_KD -> bases, descriptors, QTBD, ITERSD; tile (0, QTBD).
+        Past the last item the stream keeps re-reading its item (in bounds, never used)."""
+        p, s = self.p, self.s
+        I, Z, B, KVH, KVL, KB0 = (S_TMP + k for k in range(6))
+        T0, T1, T2 = S_TMP + 6, S_TMP + 7, S_TMP + 8
+        self.item_index(S_KD, I)
+        s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
+        p.branch(f"s_cbranch_scc0 .Ldd_{sfx}", [("scc", 0)], skip_xdl=ACC)
+        s(f"s_mov_b32 {sr(S_ITERSD)}, 0x7fffffff", [], S(S_ITERSD))
+        p.branch(f"s_branch .Lde_{sfx}", skip_xdl=ACC)
+        p.label(f".Ldd_{sfx}")
+        self.decode(I, Z, B, KVH)
+        self.kvl_of(B, KVL, f".Ldk_{sfx}")
+        s(f"s_lshl_b32 {sr(KB0)}, {sr(Z)}, 7", S(Z), S(KB0))
+        self.tiles_of(KB0, KVL, S_QTBD, S_ITERSD)
+        s(f"s_mov_b32 {sr(S_ITD)}, 0", [], S(S_ITD))
+        s(f"s_mov_b32 {sr(S_H3)}, 0", [], S(S_H3))
+        s(f"s_mov_b32 {sr(S_QT3)}, {sr(S_QTBD)}", S(S_QTBD), S(S_QT3))
+        # bases: qkv + b*S*ldb + kvh*g*256; dout + b*S*ldo + kvh*g*256; pairs + (b*Hq + kvh*g)*SP*8
+        s(f"s_mul_i32 {sr(T0)}, {sr(B)}, {sr(S_SEQ)}", S(B) + S(S_SEQ), S(T0))
+        s(f"s_mul_i32 {sr(T1)}, {sr(KVH)}, {sr(S_G)}", S(KVH) + S(S_G), S(T1))
+        s(f"s_lshl_b32 {sr(T2)}, {sr(T1)}, 8", S(T1), S(T2))
+        for base, src, stride in ((S_BQKV, S_QKV, S_LDB), (S_BDO, S_DOUT, S_LDO)):
+            self.add64(base, src, T0, stride, T2)
+        s(f"s_mul_i32 {sr(T0)}, {sr(B)}, {sr(S_HQ)}", S(B) + S(S_HQ), S(T0))
+        s(f"s_add_u32 {sr(T0)}, {sr(T0)}, {sr(T1)}", S(T0) + S(T1), S(T0))
+        s(f"s_mul_i32 {sr(T0)}, {sr(T0)}, {sr(S_SP)}", S(T0) + S(S_SP), S(T0))
+        s(f"s_mov_b32 {sr(T1)}, 8", [], S(T1))
+        self.add64(S_BLD, S_PAIRS, T0, T1, None)
+        for dst, base in ((S_RQ, S_BQKV), (S_RO, S_BDO), (S_RL, S_BLD)):
+            s(f"s_mov_b32 {sr(dst)}, {sr(base)}", S(base), S(dst))
+            s(f"s_and_b32 {sr(dst + 1)}, {sr(base + 1)}, 0xffff", S(base + 1), S(dst + 1))
+        p.label(f".Lde_{sfx}")
+
+    def add64(self, dst, src, rows, stride, extra):
+        """s[dst:dst+1] = s[src:src+1] + rows*stride (+ extra)."""
+        s, lo, hi = self.s, S_TMP + 14, S_TMP + 15
+        s(f"s_mul_i32 {sr(lo)}, {sr(rows)}, {sr(stride)}", S(rows) + S(stride), S(lo))
+        s(f"s_mul_hi_u32 {sr(hi)}, {sr(rows)}, {sr(stride)}", S(rows) + S(stride), S(hi))
+        if extra is not None:
+            s(f"s_add_u32 {sr(lo)}, {sr(lo)}, {sr(extra)}", S(lo) + S(extra), S(lo) + [("scc", 0)])
+            s(f"s_addc_u32 {sr(hi)}, {sr(hi)}, 0", S(hi) + [("scc", 0)], S(hi))
+        s(f"s_add_u32 {sr(dst)}, {sr(src)}, {sr(lo)}", S(src) + S(lo), S(dst) + [("scc", 0)])
+        s(f"s_addc_u32 {sr(dst + 1)}, {sr(src + 1)}, {sr(hi)}", S(src + 1) + S(hi) + [("scc", 0)], S(dst + 1))
+
+    def d_advance(self, sfx):
+        """DMA stream to its next tile (outside the loop bodies)."""
+        p, s = self.p, self.s
+        self.advance_h(S_H3, S_QT3)
+        s(f"s_add_u32 {sr(S_ITD)}, {sr(S_ITD)}, 1", S(S_ITD), S(S_ITD))
+        s(f"s_cmp_lt_u32 {sr(S_ITD)}, {sr(S_ITERSD)}", S(S_ITD) + S(S_ITERSD), [("scc", 0)])
+        p.branch(f"s_cbranch_scc1 .Lda_{sfx}", [("scc", 0)], skip_xdl=ACC)
+        s(f"s_add_u32 {sr(S_KD)}, {sr(S_KD)}, 1", S(S_KD), S(S_KD))
+        self.decode_d(sfx)
+        p.label(f".Lda_{sfx}")
+
+    def decode_a(self, i, sfx):
+        """Current item i: its keys, masks and tiles; tile it = its first tile."""
+        s = self.s
+        Z = S_TMP
+        self.decode(i, Z, S_BA, S_KVHA)
+        self.kvl_of(S_BA, S_KVL, f".Lak_{sfx}")
+        s(f"s_lshl_b32 {sr(S_KB0)}, {sr(Z)}, 7", S(Z), S(S_KB0))
+        T0 = S_TMP + 1
+        s(f"s_lshl_b32 {sr(T0)}, {sr(S_WAVE)}, 5", S(S_WAVE), S(T0))
+        s(f"s_add_u32 {sr(S_KW0)}, {sr(S_KB0)}, {sr(T0)}", S(S_KB0) + S(T0), S(S_KW0))
+        s(f"s_cmp_lt_u32 {sr(S_KW0)}, {sr(S_KVL)}", S(S_KW0) + S(S_KVL), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(S_KWACT)}, 1, 0", [("scc", 0)], S(S_KWACT))
+        s(f"s_add_u32 {sr(T0)}, {sr(S_KW0)}, 32", S(S_KW0), S(T0))
+        s(f"s_cmp_gt_u32 {sr(T0)}, {sr(S_KVL)}", S(T0) + S(S_KVL), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(S_KWMASK)}, 1, 0", [("scc", 0)], S(S_KWMASK))
+        s(f"s_cmp_eq_u32 {sr(S_CAUSAL)}, 0", S(S_CAUSAL), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(S_KWEFF)}, 0, {sr(S_KW0)}", S(S_KW0) + [("scc", 0)], S(S_KWEFF))
+        s(f"s_cselect_b32 {sr(S_KWDIAG)}, -1, {sr(S_KW0)}", S(S_KW0) + [("scc", 0)], S(S_KWDIAG))
+        self.tiles_of(S_KB0, S_KVL, S_QTB, S_ITERS)
+        s(f"s_mov_b32 {sr(S_IT)}, 0", [], S(S_IT))
+        s(f"s_mov_b32 {sr(S_QT0)}, {sr(S_QTB)}", S(S_QTB), S(S_QT0))
+        s(f"s_mov_b32 {sr(S_QT1)}, {sr(S_QTB)}", S(S_QTB), S(S_QT1))
+        self.advance_qt(S_QT1)
+
+    def kv_load(self):
+        """K (into VGPRs 0..31, to be scaled) and V (into its AGPRs) of the current item's
+        wave keys: lane (l32, hi) loads key kw0 + l32, bytes hi*16 + 32ks .. +15."""
+        p, s = self.p, self.s
+        RK, RV = S_TMP + 6, S_TMP + 10   # 4-aligned
+        ROWS, COL, T0 = S_TMP, S_TMP + 1, S_TMP + 2
+        s(f"s_sub_u32 {sr(ROWS)}, {sr(S_KVL)}, {sr(S_KW0)}", S(S_KVL) + S(S_KW0), S(ROWS))
+        s(f"s_max_i32 {sr(ROWS)}, {sr(ROWS)}, 0", S(ROWS), S(ROWS))
+        s(f"s_min_i32 {sr(ROWS)}, {sr(ROWS)}, 32", S(ROWS), S(ROWS))
+        s(f"s_mul_i32 {sr(T0)}, {sr(S_BA)}, {sr(S_SEQ)}", S(S_BA) + S(S_SEQ), S(T0))
+        s(f"s_add_u32 {sr(T0)}, {sr(T0)}, {sr(S_KW0)}", S(T0) + S(S_KW0), S(T0))      # first key row
+        s(f"s_add_u32 {sr(COL)}, {sr(S_HQ)}, {sr(S_KVHA)}", S(S_HQ) + S(S_KVHA), S(COL))
+        s(f"s_lshl_b32 {sr(COL)}, {sr(COL)}, 8", S(COL), S(COL))
+        for rs, more in ((RK, False), (RV, True)):
+            if more:
+                s(f"s_lshl_b32 {sr(S_TMP + 3)}, {sr(S_HKV)}, 8", S(S_HKV), S(S_TMP + 3))
+                s(f"s_add_u32 {sr(COL)}, {sr(COL)}, {sr(S_TMP + 3)}", S(COL) + S(S_TMP + 3), S(COL))
+            self.add64(rs, S_QKV, T0, S_LDB, COL)
+            s(f"s_and_b32 {sr(rs + 1)}, {sr(rs + 1)}, 0xffff", S(rs + 1), S(rs + 1))
+            s(f"s_mul_i32 {sr(rs + 2)}, {sr(ROWS)}, {sr(S_LDB)}", S(ROWS) + S(S_LDB), S(rs + 2))
+            s(f"s_mov_b32 {sr(rs + 3)}, 0x20000", [], S(rs + 3))
+        KO = V_T
+        p.valu(f"v_mul_lo_u32 {vr(KO)}, {vr(V_L32)}, {sr(S_LDB)}", V(V_L32) + S(S_LDB), V(KO))
+        p.valu(f"v_lshl_add_u32 {vr(KO)}, {vr(V_HI4)}, 2, {vr(KO)}", V(V_HI4) + V(KO), V(KO))
+        for ks in range(8):
+            p.vmem_load(f"buffer_load_dwordx4 {vr(ks * 4, 4)}, {vr(KO)}, {sr(RK, 4)}, 0 offen offset:{ks * 32}",
+                        V(ks * 4, 4), V(KO) + S(RK, 4))
+        for ks in range(8):
+            p.vmem_load(f"buffer_load_dwordx4 {ar(A_V + ks * 4, 4)}, {vr(KO)}, {sr(RV, 4)}, 0 offen offset:{ks * 32}",
+                        A(A_V + ks * 4, 4), V(KO) + S(RV, 4))
+
+    def zero_acc(self):
+        p = self.p
+        for i in range(4):
+            p.valu(f"v_mov_b32_e32 {vr(V_TB + i)}, 0", [], V(V_TB + i))
+        for i in range(8):   # dV, dK := 0 with eight MFMAs of zero operands
+            p.mfma(MFMA, A_DV + 16 * i, V_TB, V_TB, None, dst_acc=True)
+
+    def scale_k(self):
+        p = self.p
+        t0, t1 = V_T + 1, V_T + 2
+        for i in range(32):   # K * scale*log2e, rounded to fp16
+            p.valu(f"v_fma_mix_f32 {vr(t0)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t0))
+            p.valu(f"v_fma_mix_f32 {vr(t1)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t1))
+            p.valu(f"v_cvt_pk_f16_f32 {vr(i)}, {vr(t0)}, {vr(t1)}", V(t0, 2), V(i))
+            p.valu(f"v_accvgpr_write_b32 {ar(A_K + i)}, {vr(i)}", V(i), A(A_K + i))
+
+    def epilogue(self):
+        """dK^T * scale and dV^T of the current item into dqkv.  A lane holds key kw0 + l32,
+        d = db*32 + g4*8 + hi*4 + 0..3; the values go to fp16, through the wave's LDS staging
+        rows (row = key, 16-byte chunk db*4 + g4), and back out 16 bytes per lane so that every
+        store instruction writes four whole 256-byte rows.  Keys past S are dropped by the
+        descriptors."""
+        p, s = self.p, self.s
+        RK, RV = S_TMP + 6, S_TMP + 10   # 4-aligned
+        T0, COL, T2, EPW = S_TMP, S_TMP + 1, S_TMP + 2, S_TMP + 3
+        s(f"s_mul_i32 {sr(T0)}, {sr(S_BA)}, {sr(S_SEQ)}", S(S_BA) + S(S_SEQ), S(T0))
+        s(f"s_add_u32 {sr(COL)}, {sr(S_HQ)}, {sr(S_KVHA)}", S(S_HQ) + S(S_KVHA), S(COL))
+        s(f"s_lshl_b32 {sr(COL)}, {sr(COL)}, 8", S(COL), S(COL))
+        for rs, more in ((RK, False), (RV, True)):
+            if more:
+                s(f"s_lshl_b32 {sr(T2)}, {sr(S_HKV)}, 8", S(S_HKV), S(T2))
+                s(f"s_add_u32 {sr(COL)}, {sr(COL)}, {sr(T2)}", S(COL) + S(T2), S(COL))
+            self.add64(rs, S_DQKV, T0, S_LDB, COL)
+            s(f"s_and_b32 {sr(rs + 1)}, {sr(rs + 1)}, 0xffff", S(rs + 1), S(rs + 1))
+            s(f"s_mul_i32 {sr(rs + 2)}, {sr(S_SEQ)}, {sr(S_LDB)}", S(S_SEQ) + S(S_LDB), S(rs + 2))
+            s(f"s_mov_b32 {sr(rs + 3)}, 0x20000", [], S(rs + 3))
+        s(f"s_mul_i32 {sr(EPW)}, {sr(S_WAVE)}, {EPI_WAVE}", S(S_WAVE), S(EPW))
+        s(f"s_add_u32 {sr(EPW)}, {sr(EPW)}, {LDS_EPI}", S(EPW), S(EPW))
+        s(f"s_lshl_b32 {sr(T2)}, {sr(S_LDB)}, 2", S(S_LDB), S(T2))              # 4 rows
+        BW, BR, TA, TB = 16, 17, 18, 19
+        OO = 40
+        # write address: EPW + l32*272 + hi*8;  read address: EPW + (lane>>4)*272 + (lane&15)*16
+        p.valu(f"v_mul_u32_u24_e32 {vr(BW)}, {EPI_ROW}, {vr(V_L32)}", V(V_L32), V(BW))
+        p.valu(f"v_add_u32_e32 {vr(BW)}, {sr(EPW)}, {vr(BW)}", S(EPW) + V(BW), V(BW))
+        p.valu(f"v_lshl_add_u32 {vr(BW)}, {vr(V_HI4)}, 1, {vr(BW)}", V(V_HI4) + V(BW), V(BW))
+        p.valu(f"v_lshrrev_b32_e32 {vr(TA)}, 4, {vr(V_L32)}", V(V_L32), V(TA))
+        p.valu(f"v_lshrrev_b32_e32 {vr(TB)}, 1, {vr(V_HI4)}", V(V_HI4), V(TB))
+        p.valu(f"v_add_u32_e32 {vr(TA)}, {vr(TA)}, {vr(TB)}", V(TA) + V(TB), V(TA))        # lane >> 4
+        p.valu(f"v_and_b32_e32 {vr(TB)}, 15, {vr(V_L32)}", V(V_L32), V(TB))                 # lane & 15
+        p.valu(f"v_mul_u32_u24_e32 {vr(BR)}, {EPI_ROW}, {vr(TA)}", V(TA), V(BR))
+        p.valu(f"v_lshl_add_u32 {vr(BR)}, {vr(TB)}, 4, {vr(BR)}", V(TB) + V(BR), V(BR))
+        p.valu(f"v_add_u32_e32 {vr(BR)}, {sr(EPW)}, {vr(BR)}", S(EPW) + V(BR), V(BR))
+        # global offsets of rows kw0 + 4i + (lane >> 4), chunk lane & 15
+        p.valu(f"v_add_u32_e32 {vr(TA)}, {sr(S_KW0)}, {vr(TA)}", S(S_KW0) + V(TA), V(TA))
+        p.valu(f"v_mul_lo_u32 {vr(TA)}, {vr(TA)}, {sr(S_LDB)}", V(TA) + S(S_LDB), V(TA))
+        p.valu(f"v_lshl_add_u32 {vr(OO)}, {vr(TB)}, 4, {vr(TA)}", V(TB) + V(TA), V(OO))
+        for i in range(1, 8):
+            p.valu(f"v_add_u32_e32 {vr(OO + i)}, {sr(T2)}, {vr(OO + i - 1)}", S(T2) + V(OO + i - 1), V(OO + i))
+        W = 0
+        for acc, rs, scale in ((A_DK, RK, True), (A_DV, RV, False)):
+            for db in range(4):
+                for g4 in range(4):
+                    a0 = acc + db * 16 + g4 * 4
+                    for j in range(4):
+                        p.valu(f"v_accvgpr_read_b32 {vr(W + j)}, {ar(a0 + j)}", A(a0 + j), V(W + j))
+                    if scale:
+                        for j in range(4):
+                            p.valu(f"v_mul_f32_e32 {vr(W + j)}, {sr(S_SCALE)}, {vr(W + j)}", V(W + j) + S(S_SCALE), V(W + j))
+                    p.valu(f"v_cvt_pk_f16_f32 {vr(W + 4)}, {vr(W)}, {vr(W + 1)}", V(W, 2), V(W + 4))
+                    p.valu(f"v_cvt_pk_f16_f32 {vr(W + 5)}, {vr(W + 2)}, {vr(W + 3)}", V(W + 2, 2), V(W + 5))
+                    p.ds_write(f"ds_write_b64 {vr(BW)}, {vr(W + 4, 2)} offset:{(db * 4 + g4) * 16}", V(BW) + V(W + 4, 2))
+                    W = 8 if W == 0 else 0
+            for i in range(8):   # LDS operations of a wave complete in order: reads see the rows
+                R = 20 + 4 * (i % 4)
+                p.ds_read(f"ds_read_b128 {vr(R, 4)}, {vr(BR)} offset:{i * 4 * EPI_ROW}", V(R, 4), V(BR))
+                p.vmem_store(f"buffer_store_dwordx4 {vr(R, 4)}, {vr(OO + i)}, {sr(rs, 4)}, 0 offen",
+                             V(R, 4) + V(OO + i) + S(rs, 4))
+
+    def start_item(self, u, sfx):
+        """The current item's tile it (in buffer u, score set u % 2) after its K, V are loaded:
+        start values, S/dP of tile it when active, the body's variant, start values and first
+        row reads of tile it+1."""
+        p, s = self.p, self.s
+        T0 = S_TMP
+        self.cinit(u)
+        self.active(S_QT0, T0)
+        s(f"s_cmp_eq_u32 {sr(T0)}, 0", S(T0), [("scc", 0)])
+        p.branch(f"s_cbranch_scc1 .Lss_{sfx}", [("scc", 0)], skip_xdl=ACC)
+        rissued = 0
+        for i in range(16):
+            while rissued < 16 and rissued - LK <= i:
+                self.row_read(rissued, u)
+                rissued += 1
+            self.sdp_mfma(i, u % 2)
+        p.label(f".Lss_{sfx}")
+        self.code()
+        self.cinit((u + 1) % 4)
+        for i in range(LK):
+            self.row_read(i, (u + 1) % 4)
+        p.branch(f"s_branch .Ldisp{u}", keep_lgkm=True, skip_xdl=ACC)
 
     # ---------------------------------------------------------------- iteration bodies
     def body(self, u, sdp, ew, masked):
@@ -444,71 +728,23 @@ class Body:
 def build(check_ldb: int = 12288, check_ldo: int = 4096) -> str:
     p = Prog(coalesce_lgkm=True)
     sal = p.salu
+    b = Body(p)
     # ---------------------------------------------------------------- scalars
     p.smem(f"s_load_dwordx16 {sr(8, 16)}, {sr(0, 2)}, 0x0", S(8, 16), S(0, 2))
     p.smem(f"s_load_dwordx8 {sr(24, 8)}, {sr(0, 2)}, 0x40", S(24, 8), S(0, 2))
+    p.smem(f"s_load_dwordx2 {sr(S_MAGBH, 2)}, {sr(0, 2)}, 0x60", S(S_MAGBH, 2), S(0, 2))
     L = Lanes(p, check_ldb)
     L.shr(V_PT + 0, L.k(6), 0)
     p.readlane(f"v_readfirstlane_b32 {sr(S_WAVE)}, {vr(V_PT + 0)}", V(V_PT + 0), S(S_WAVE))
     p.waitcnt(lgkm=0)
-    T0, T1, T2, T3, T4 = S_TMP, S_TMP + 1, S_TMP + 2, S_TMP + 3, S_TMP + 4
-    # kv_len
-    sal(f"s_mov_b32 {sr(S_KVL)}, {sr(S_SEQ)}", S(S_SEQ), S(S_KVL))
-    sal(f"s_cmp_eq_u64 {sr(S_KVLEN, 2)}, 0", S(S_KVLEN, 2), [("scc", 0)])
-    p.branch("s_cbranch_scc1 .Lkvl_done", [("scc", 0)])
-    sal(f"s_lshl_b32 {sr(T0)}, {sr(S_B)}, 2", S(S_B), S(T0))
-    p.smem(f"s_load_dword {sr(S_KVL)}, {sr(S_KVLEN, 2)}, {sr(T0)}", S(S_KVL), S(S_KVLEN, 2) + S(T0))
-    p.waitcnt(lgkm=0)
-    sal(f"s_max_i32 {sr(S_KVL)}, {sr(S_KVL)}, 0", S(S_KVL), S(S_KVL))
-    sal(f"s_min_i32 {sr(S_KVL)}, {sr(S_KVL)}, {sr(S_SEQ)}", S(S_KVL) + S(S_SEQ), S(S_KVL))
-    p.label(".Lkvl_done")
-    # key block, this wave's keys
-    sal(f"s_lshl_b32 {sr(S_KB0)}, {sr(S_Z)}, 7", S(S_Z), S(S_KB0))
-    sal(f"s_lshl_b32 {sr(T0)}, {sr(S_WAVE)}, 5", S(S_WAVE), S(T0))
-    sal(f"s_add_u32 {sr(S_KW0)}, {sr(S_KB0)}, {sr(T0)}", S(S_KB0) + S(T0), S(S_KW0))
-    sal(f"s_cmp_lt_u32 {sr(S_KW0)}, {sr(S_KVL)}", S(S_KW0) + S(S_KVL), [("scc", 0)])
-    sal(f"s_cselect_b32 {sr(S_KWACT)}, 1, 0", [("scc", 0)], S(S_KWACT))
-    sal(f"s_add_u32 {sr(T0)}, {sr(S_KW0)}, 32", S(S_KW0), S(T0))
-    sal(f"s_cmp_gt_u32 {sr(T0)}, {sr(S_KVL)}", S(T0) + S(S_KVL), [("scc", 0)])
-    sal(f"s_cselect_b32 {sr(S_KWMASK)}, 1, 0", [("scc", 0)], S(S_KWMASK))
-    sal(f"s_cmp_eq_u32 {sr(S_CAUSAL)}, 0", S(S_CAUSAL), [("scc", 0)])
-    sal(f"s_cselect_b32 {sr(S_KWEFF)}, 0, {sr(S_KW0)}", S(S_KW0) + [("scc", 0)], S(S_KWEFF))
-    sal(f"s_cselect_b32 {sr(S_KWDIAG)}, -1, {sr(S_KW0)}", S(S_KW0) + [("scc", 0)], S(S_KWDIAG))
-    # q-tiles: [qt_begin, qt_end) per head; iters = g * (qt_end - qt_begin)
+    T0, T3 = S_TMP, S_TMP + 3
     sal(f"s_add_u32 {sr(T0)}, {sr(S_SEQ)}, 31", S(S_SEQ), S(T0))
     sal(f"s_lshr_b32 {sr(S_QTE)}, {sr(T0)}, 5", S(T0), S(S_QTE))
-    sal(f"s_lshr_b32 {sr(T0)}, {sr(S_KB0)}, 5", S(S_KB0), S(T0))
-    sal(f"s_cmp_eq_u32 {sr(S_CAUSAL)}, 0", S(S_CAUSAL), [("scc", 0)])
-    sal(f"s_cselect_b32 {sr(S_QTB)}, 0, {sr(T0)}", S(T0) + [("scc", 0)], S(S_QTB))
-    sal(f"s_sub_u32 {sr(T0)}, {sr(S_QTE)}, {sr(S_QTB)}", S(S_QTE) + S(S_QTB), S(T0))
-    sal(f"s_mul_i32 {sr(S_ITERS)}, {sr(T0)}, {sr(S_G)}", S(T0) + S(S_G), S(S_ITERS))
-    # a workgroup whose keys all lie at or past kv_len only writes zero gradients
-    sal(f"s_cmp_ge_u32 {sr(S_KB0)}, {sr(S_KVL)}", S(S_KB0) + S(S_KVL), [("scc", 0)])
-    sal(f"s_cselect_b32 {sr(S_ITERS)}, 0, {sr(S_ITERS)}", S(S_ITERS) + [("scc", 0)], S(S_ITERS))
-    # batch bases: qkv + b*S*ldb + kvh*g*256 (Q columns of the group's first q-head);
-    # dout + b*S*ldo + kvh*g*256; pairs + (b*Hq + kvh*g)*SP*8
-    sal(f"s_mul_i32 {sr(T0)}, {sr(S_B)}, {sr(S_SEQ)}", S(S_B) + S(S_SEQ), S(T0))
-    sal(f"s_mul_i32 {sr(T1)}, {sr(S_H)}, {sr(S_G)}", S(S_H) + S(S_G), S(T1))           # first q-head
-    sal(f"s_lshl_b32 {sr(T2)}, {sr(T1)}, 8", S(T1), S(T2))
-    for base, src, stride in ((S_BQKV, S_QKV, S_LDB), (S_BDO, S_DOUT, S_LDO)):
-        sal(f"s_mul_i32 {sr(T3)}, {sr(T0)}, {sr(stride)}", S(T0) + S(stride), S(T3))
-        sal(f"s_mul_hi_u32 {sr(T4)}, {sr(T0)}, {sr(stride)}", S(T0) + S(stride), S(T4))
-        sal(f"s_add_u32 {sr(T3)}, {sr(T3)}, {sr(T2)}", S(T3) + S(T2), S(T3) + [("scc", 0)])
-        sal(f"s_addc_u32 {sr(T4)}, {sr(T4)}, 0", S(T4) + [("scc", 0)], S(T4))
-        sal(f"s_add_u32 {sr(base)}, {sr(src)}, {sr(T3)}", S(src) + S(T3), S(base) + [("scc", 0)])
-        sal(f"s_addc_u32 {sr(base + 1)}, {sr(src + 1)}, {sr(T4)}", S(src + 1) + S(T4) + [("scc", 0)], S(base + 1))
-    sal(f"s_mul_i32 {sr(T3)}, {sr(S_B)}, {sr(S_HQ)}", S(S_B) + S(S_HQ), S(T3))
-    sal(f"s_add_u32 {sr(T3)}, {sr(T3)}, {sr(T1)}", S(T3) + S(T1), S(T3))
-    sal(f"s_mul_i32 {sr(T3)}, {sr(T3)}, {sr(S_SP)}", S(T3) + S(S_SP), S(T3))
-    sal(f"s_mul_hi_u32 {sr(T4)}, {sr(T3)}, 8", S(T3), S(T4))
-    sal(f"s_lshl_b32 {sr(T3)}, {sr(T3)}, 3", S(T3), S(T3))
-    sal(f"s_add_u32 {sr(S_BLD)}, {sr(S_PAIRS)}, {sr(T3)}", S(S_PAIRS) + S(T3), S(S_BLD) + [("scc", 0)])
-    sal(f"s_addc_u32 {sr(S_BLD + 1)}, {sr(S_PAIRS + 1)}, {sr(T4)}", S(S_PAIRS + 1) + S(T4) + [("scc", 0)], S(S_BLD + 1))
-    # DMA placement: Q/dO rows wave*8.. of a tile; the wave's own row-pair slot
-    sal(f"s_lshl_b32 {sr(S_LDSW)}, {sr(S_WAVE)}, 11", S(S_WAVE), S(S_LDSW))
-    sal(f"s_lshl_b32 {sr(S_LDSL)}, {sr(S_WAVE)}, 8", S(S_WAVE), S(S_LDSL))
+    sal(f"s_lshl_b32 {sr(S_LDB32)}, {sr(S_LDB)}, 5", S(S_LDB), S(S_LDB32))
+    sal(f"s_lshl_b32 {sr(S_LDO32)}, {sr(S_LDO)}, 5", S(S_LDO), S(S_LDO32))
+    sal(f"s_lshl_b32 {sr(S_LDSW)}, {sr(S_WAVE)}, 11", S(S_WAVE), S(S_LDSW))       # Q/dO rows wave*8..
+    sal(f"s_lshl_b32 {sr(S_LDSL)}, {sr(S_WAVE)}, 8", S(S_WAVE), S(S_LDSL))        # the wave's quad slot
     sal(f"s_add_u32 {sr(S_LDSL)}, {sr(S_LDSL)}, {LDS_LD}", S(S_LDSL), S(S_LDSL))
-
     # ---------------------------------------------------------------- DMA lane offsets
     LANE, L32, HI = V_PT + 1, V_PT + 2, V_PT + 3
     DR, DP, TA, TB, TC = V_PT + 4, V_PT + 5, V_PT + 6, V_PT + 7, V_PT + 8
@@ -536,57 +772,28 @@ def build(check_ldb: int = 12288, check_ldo: int = 4096) -> str:
     L.shl(V_LOFF, L.k(2), LANE)
     p.valu(f"v_mov_b32_e32 {vr(V_L32)}, {vr(L32)}", V(L32), V(V_L32))
     p.valu(f"v_lshlrev_b32_e32 {vr(V_HI4)}, 2, {vr(HI)}", V(HI), V(V_HI4))
-    # ---------------------------------------------------------------- fixed DMA descriptors
-    sal(f"s_lshl_b32 {sr(S_LDB32)}, {sr(S_LDB)}, 5", S(S_LDB), S(S_LDB32))
-    sal(f"s_lshl_b32 {sr(S_LDO32)}, {sr(S_LDO)}, 5", S(S_LDO), S(S_LDO32))
-    for dst, base, nrec in ((S_RQ, S_BQKV, None), (S_RO, S_BDO, None), (S_RL, S_BLD, None)):
-        sal(f"s_mov_b32 {sr(dst)}, {sr(base)}", S(base), S(dst))
-        sal(f"s_and_b32 {sr(dst + 1)}, {sr(base + 1)}, 0xffff", S(base + 1), S(dst + 1))
-        sal(f"s_mov_b32 {sr(dst + 3)}, 0x20000", [], S(dst + 3))
+    # ---------------------------------------------------------------- DMA descriptor sizes
+    # (the same for every item: a batch's Q / dO rows, a kv group's row quads)
     sal(f"s_mul_i32 {sr(S_RQ + 2)}, {sr(S_SEQ)}, {sr(S_LDB)}", S(S_SEQ) + S(S_LDB), S(S_RQ + 2))
     sal(f"s_mul_i32 {sr(S_RO + 2)}, {sr(S_SEQ)}, {sr(S_LDO)}", S(S_SEQ) + S(S_LDO), S(S_RO + 2))
     sal(f"s_mul_i32 {sr(S_RL + 2)}, {sr(S_G)}, {sr(S_SP)}", S(S_G) + S(S_SP), S(S_RL + 2))
     sal(f"s_lshl_b32 {sr(S_RL + 2)}, {sr(S_RL + 2)}, 3", S(S_RL + 2), S(S_RL + 2))
-    b = Body(p)
-    # ---------------------------------------------------------------- tiles 0, 1 in flight
-    sal(f"s_mov_b32 {sr(S_IT)}, 0", [], S(S_IT))
-    sal(f"s_mov_b32 {sr(S_H3)}, 0", [], S(S_H3))
-    sal(f"s_mov_b32 {sr(S_QT3)}, {sr(S_QTB)}", S(S_QTB), S(S_QT3))
+    for dst in (S_RQ, S_RO, S_RL):
+        sal(f"s_mov_b32 {sr(dst + 3)}, 0x20000", [], S(dst + 3))
+    # ---------------------------------------------------------------- first items, tiles 0, 1
+    sal(f"s_mov_b32 {sr(S_KA)}, 0", [], S(S_KA))
+    sal(f"s_mov_b32 {sr(S_KD)}, 0", [], S(S_KD))
+    b.decode_d("p0")
     for t in range(2):
         b.tile_offsets(S_H3, S_QT3)
         b.dma_all(t)
-        b.advance_h(S_H3, S_QT3)
-    # ---------------------------------------------------------------- K, V of the wave's keys
-    # lane (l32, hi): key kw0 + l32, head-dim elements ks*16 + hi*8 .. +7; K into VGPRs (to
-    # be scaled), V straight into its AGPRs
-    RK, RV = S_TMP + 10, S_TMP + 14
-    T1, T2 = S_TMP + 1, S_TMP + 2
-    sal(f"s_sub_u32 {sr(T1)}, {sr(S_KVL)}, {sr(S_KW0)}", S(S_KVL) + S(S_KW0), S(T1))
-    sal(f"s_max_i32 {sr(T1)}, {sr(T1)}, 0", S(T1), S(T1))
-    sal(f"s_min_i32 {sr(T1)}, {sr(T1)}, 32", S(T1), S(T1))
-    # S_BQKV points at the group's first q-head columns (kvh*g*256): K columns are at
-    # (Hq + kvh - kvh*g)*256 from it (a positive offset), V columns Hkv*256 further
-    sal(f"s_mul_i32 {sr(T2)}, {sr(S_H)}, {sr(S_G)}", S(S_H) + S(S_G), S(T2))
-    sal(f"s_sub_u32 {sr(T2)}, {sr(S_H)}, {sr(T2)}", S(S_H) + S(T2), S(T2))
-    sal(f"s_add_u32 {sr(T2)}, {sr(T2)}, {sr(S_HQ)}", S(T2) + S(S_HQ), S(T2))
-    sal(f"s_lshl_b32 {sr(T2)}, {sr(T2)}, 8", S(T2), S(T2))
-    b.rsrc(RK, S_BQKV, S_KW0, S_LDB, T1, T2)
-    sal(f"s_lshl_b32 {sr(T3)}, {sr(S_HKV)}, 8", S(S_HKV), S(T3))
-    sal(f"s_add_u32 {sr(T2)}, {sr(T2)}, {sr(T3)}", S(T2) + S(T3), S(T2))
-    b.rsrc(RV, S_BQKV, S_KW0, S_LDB, T1, T2)
-    KO = V_T   # row offset l32*ldb + hi*16
-    p.valu(f"v_mul_lo_u32 {vr(KO)}, {vr(V_L32)}, {sr(S_LDB)}", V(V_L32) + S(S_LDB), V(KO))
-    p.valu(f"v_lshl_add_u32 {vr(KO)}, {vr(V_HI4)}, 2, {vr(KO)}", V(V_HI4) + V(KO), V(KO))
-    for ks in range(8):
-        p.vmem_load(f"buffer_load_dwordx4 {vr(ks * 4, 4)}, {vr(KO)}, {sr(RK, 4)}, 0 offen offset:{ks * 32}",
-                    V(ks * 4, 4), V(KO) + S(RK, 4))
-    for ks in range(8):
-        p.vmem_load(f"buffer_load_dwordx4 {ar(A_V + ks * 4, 4)}, {vr(KO)}, {sr(RV, 4)}, 0 offen offset:{ks * 32}",
-                    A(A_V + ks * 4, 4), V(KO) + S(RV, 4))
-    # ---------------------------------------------------------------- tile 2 in flight
+        b.d_advance(f"p{t + 1}")
+    b.item_index(S_KA, S_TMP + 16)
+    b.decode_a(S_TMP + 16, "p")
+    b.kv_load()
     b.tile_offsets(S_H3, S_QT3)
     b.dma_all(2)
-    b.advance_h(S_H3, S_QT3)
+    b.d_advance("p3")
     # ---------------------------------------------------------------- LDS read offsets
     # row quads: lane (k = lane & 7, hi) reads quad (k//2)*4 + (k & 1) + 2hi of its wave's slot
     L.and_(TA, L.k(6), LANE)
@@ -600,18 +807,21 @@ def build(check_ldb: int = 12288, check_ldo: int = 4096) -> str:
     row_read_offsets(L, V_KOFF, (LANE, L32, HI), (TA, TB, TC))
     tr_read_offsets(L, V_VOFF, (LANE, L32, HI), (TA, TB, TC, V_PT + 9, V_PT + 10, V_PT + 11, V_PT + 12))
     _check_lanes(L, check_ldb, check_ldo)
-    # ---------------------------------------------------------------- accumulators, K scale
-    for i in range(4):
-        p.valu(f"v_mov_b32_e32 {vr(V_TB + i)}, 0", [], V(V_TB + i))
-    for i in range(8):   # dV, dK := 0 with eight MFMAs of zero operands
-        p.mfma(MFMA, A_DV + 16 * i, V_TB, V_TB, None, dst_acc=True)
-    t0, t1 = V_T + 1, V_T + 2
-    for i in range(32):   # K * scale*log2e, rounded to fp16
-        p.valu(f"v_fma_mix_f32 {vr(t0)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t0))
-        p.valu(f"v_fma_mix_f32 {vr(t1)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t1))
-        p.valu(f"v_cvt_pk_f16_f32 {vr(i)}, {vr(t0)}, {vr(t1)}", V(t0, 2), V(i))
-        p.valu(f"v_accvgpr_write_b32 {ar(A_K + i)}, {vr(i)}", V(i), A(A_K + i))
-    return _rest(p, b)
+    b.zero_acc()
+    b.scale_k()
+    p.waitcnt(vm=0)
+    p.barrier()
+    b.start_item(0, "p")
+    # ---------------------------------------------------------------- bodies, boundaries
+    for u in range(4):
+        _dispatch(b, u)
+    for u in range(4):
+        _boundary(b, u)
+    p.label(".Lexit")
+    p.waitcnt(vm=0, lgkm=0)   # DMA requests past the last item still write LDS
+    p.emit("s_endpgm", BRANCH)
+    return kernel_text(NAME, p.finalize(), lds_bytes=LDS_BYTES, kernarg_bytes=KERNARG_BYTES,
+                       next_free_sgpr=NEXT_FREE_SGPR, args=ARGS, wg_ids=(1, 0, 0))
 
 
 def _check_lanes(L: Lanes, ldb, ldo):
@@ -633,89 +843,53 @@ def _check_lanes(L: Lanes, ldb, ldo):
     assert np.array_equal(L.val[V_LDR], LDS_LD + wave * 256 + (rows // 2) * 16), "quad read offsets"
 
 
-def _rest(p: Prog, b: Body) -> str:
-    s = b.s
-    T0, T1, T2, T3 = S_TMP, S_TMP + 1, S_TMP + 2, S_TMP + 3
-    # ---------------------------------------------------------------- tile 0
-    p.waitcnt(vm=5)   # everything but tile 2
-    p.barrier()
-    s(f"s_mov_b32 {sr(S_QT0)}, {sr(S_QTB)}", S(S_QTB), S(S_QT0))
-    s(f"s_mov_b32 {sr(S_QT1)}, {sr(S_QTB)}", S(S_QTB), S(S_QT1))
-    b.cinit(0)
-    # S/dP(0) if tile 0 is active for this wave
-    b.active(S_QT0, T0)
-    s(f"s_cmp_eq_u32 {sr(T0)}, 0", S(T0), [("scc", 0)])
-    p.branch("s_cbranch_scc1 .Lpro_skip", [("scc", 0)])
-    rissued = 0
-    for i in range(16):
-        while rissued < 16 and rissued - LK <= i:
-            b.row_read(rissued, 0)
-            rissued += 1
-        b.sdp_mfma(i, 0)
-    p.label(".Lpro_skip")
-    b.advance_qt(S_QT1)
-    b.code()
-    b.cinit(1)
-    for i in range(LK):
-        b.row_read(i, 1)
-    p.branch("s_branch .Ldisp0", keep_lgkm=True)
-    # ---------------------------------------------------------------- tile loop
-    for u in range(4):
-        _dispatch(b, u)
-    p.label(".Lloop_done")
-    p.nop(16)         # MFMA results of the last body before any accumulator read
-    p.waitcnt(vm=0, lgkm=0)   # the last (empty) tile requests still write LDS
-    # ---------------------------------------------------------------- epilogue
-    # dK^T * scale, dV^T: lane holds key kw0 + l32, d = db*32 + g4*8 + hi*4 + 0..3
-    s(f"s_mov_b32 {sr(T1)}, {sr(S_SEQ)}", S(S_SEQ), S(T1))
-    s(f"s_add_u32 {sr(T2)}, {sr(S_HQ)}, {sr(S_H)}", S(S_HQ) + S(S_H), S(T2))
-    s(f"s_lshl_b32 {sr(T2)}, {sr(T2)}, 8", S(T2), S(T2))
-    # base: dqkv + b*S*ldb + column; rows [0, S)
-    s(f"s_mul_i32 {sr(T0)}, {sr(S_B)}, {sr(S_SEQ)}", S(S_B) + S(S_SEQ), S(T0))
-    b.rsrc(S_RQ, S_DQKV, T0, S_LDB, T1, T2)
-    s(f"s_lshl_b32 {sr(T3)}, {sr(S_HKV)}, 8", S(S_HKV), S(T3))
-    s(f"s_add_u32 {sr(T2)}, {sr(T2)}, {sr(T3)}", S(T2) + S(T3), S(T2))
-    b.rsrc(S_RO, S_DQKV, T0, S_LDB, T1, T2)
-    OO = V_T
-    p.valu(f"v_add_u32_e32 {vr(OO)}, {sr(S_KW0)}, {vr(V_L32)}", S(S_KW0) + V(V_L32), V(OO))
-    p.valu(f"v_mul_lo_u32 {vr(OO)}, {vr(OO)}, {sr(S_LDB)}", V(OO) + S(S_LDB), V(OO))
-    p.valu(f"v_lshl_add_u32 {vr(OO)}, {vr(V_HI4)}, 1, {vr(OO)}", V(V_HI4) + V(OO), V(OO))
-    W = 0
-    for acc, rs, scale in ((A_DK, S_RQ, True), (A_DV, S_RO, False)):
-        for db in range(4):
-            for g4 in range(4):
-                a0 = acc + db * 16 + g4 * 4
-                for j in range(4):
-                    p.valu(f"v_accvgpr_read_b32 {vr(W + j)}, {ar(a0 + j)}", A(a0 + j), V(W + j))
-                if scale:
-                    for j in range(4):
-                        p.valu(f"v_mul_f32_e32 {vr(W + j)}, {sr(S_SCALE)}, {vr(W + j)}", V(W + j) + S(S_SCALE), V(W + j))
-                p.valu(f"v_cvt_pk_f16_f32 {vr(W + 4)}, {vr(W)}, {vr(W + 1)}", V(W, 2), V(W + 4))
-                p.valu(f"v_cvt_pk_f16_f32 {vr(W + 5)}, {vr(W + 2)}, {vr(W + 3)}", V(W + 2, 2), V(W + 5))
-                p.vmem_store(f"buffer_store_dwordx2 {vr(W + 4, 2)}, {vr(OO)}, {sr(rs, 4)}, 0 offen offset:{db * 64 + g4 * 16}",
-                             V(W + 4, 2) + V(OO) + S(rs, 4))
-                W = 8 if W == 0 else 0
-    p.emit("s_endpgm", BRANCH)
-    return kernel_text(NAME, p.finalize(), lds_bytes=LDS_BYTES, kernarg_bytes=KERNARG_BYTES,
-                       next_free_sgpr=NEXT_FREE_SGPR, args=ARGS)
-
-
 def _dispatch(b: Body, u: int):
-    """Dispatcher and the six body variants of iteration residue u."""
+    """Dispatcher and the six body variants of residue u: first a DMA stream that moved on to
+    its next item (code bit 16), then the end of the current item (code 8), then the variant."""
     p, s = b.p, b.s
     pend = b.prefetch_regs()
     p.label(f".Ldisp{u}")
     p.assume_lgkm(pend)
+    s(f"s_bitcmp1_b32 {sr(S_CODE)}, 4", S(S_CODE), [("scc", 0)])
+    p.branch(f"s_cbranch_scc0 .Lnod{u}", [("scc", 0)], keep_lgkm=True, skip_xdl=ACC)
+    p.waitcnt(lgkm=0)
+    s(f"s_add_u32 {sr(S_KD)}, {sr(S_KD)}, 1", S(S_KD), S(S_KD))
+    b.decode_d(f"d{u}")
+    s(f"s_andn2_b32 {sr(S_CODE)}, {sr(S_CODE)}, 16", S(S_CODE), S(S_CODE))
+    p.label(f".Lnod{u}")
+    p.assume_lgkm(pend)
+    s(f"s_bitcmp1_b32 {sr(S_CODE)}, 3", S(S_CODE), [("scc", 0)])
+    p.branch(f"s_cbranch_scc1 .Lbnd{u}", [("scc", 0)], keep_lgkm=True, skip_xdl=ACC)
     for lab, _, _, _ in VARIANTS[:-1]:
         for c in CODES[lab]:
             s(f"s_cmp_eq_u32 {sr(S_CODE)}, {c}", S(S_CODE), [("scc", 0)])
             p.branch(f"s_cbranch_scc1 .L{lab}{u}", [("scc", 0)], keep_lgkm=True, skip_xdl=ACC)
-    s(f"s_cmp_ge_u32 {sr(S_CODE)}, 8", S(S_CODE), [("scc", 0)])
-    p.branch("s_cbranch_scc1 .Lloop_done", [("scc", 0)], keep_lgkm=True, skip_xdl=ACC)
     for lab, sdp, ew, masked in VARIANTS[::-1]:     # idle falls through from the dispatcher
         p.label(f".L{lab}{u}")
         p.assume_lgkm(pend)
         b.body(u, sdp=sdp, ew=ew, masked=masked)
+
+
+def _boundary(b: Body, u: int):
+    """End of the current item before body residue u: store its dK, dV; take the next item
+    (or stop), load its K, V and start it on tile it (buffer u), whose data the DMA stream
+    has already delivered."""
+    p, s = b.p, b.s
+    I = S_TMP + 16
+    p.label(f".Lbnd{u}")
+    p.nop(16)                 # MFMA results of the last body before the accumulator reads
+    p.waitcnt(lgkm=0)
+    b.epilogue()
+    s(f"s_add_u32 {sr(S_KA)}, {sr(S_KA)}, 1", S(S_KA), S(S_KA))
+    b.item_index(S_KA, I)
+    s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
+    p.branch("s_cbranch_scc1 .Lexit", [("scc", 0)], skip_xdl=ACC)
+    b.decode_a(I, f"b{u}")
+    b.kv_load()
+    b.zero_acc()
+    b.scale_k()
+    p.waitcnt(vm=0)
+    b.start_item(u, f"b{u}")
 
 
 def main(path: str) -> None:

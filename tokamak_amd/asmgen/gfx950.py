@@ -481,7 +481,7 @@ def metadata(name, *, args, lds_bytes, kernarg_bytes, sgpr_count, wg_size=256):
     return "\n".join(lines) + "\n"
 
 
-def kernel_text(name, body_lines, *, lds_bytes, kernarg_bytes, next_free_sgpr, args):
+def kernel_text(name, body_lines, *, lds_bytes, kernarg_bytes, next_free_sgpr, args, wg_ids=(1, 1, 1)):
     head = [
         '\t.amdgcn_target "amdgcn-amd-amdhsa--gfx950"',
         "\t.text",
@@ -493,6 +493,6 @@ def kernel_text(name, body_lines, *, lds_bytes, kernarg_bytes, next_free_sgpr, a
     tail = [f".Lfunc_end_{name}:", f"\t.size {name}, .Lfunc_end_{name}-{name}"]
     return ("\n".join(head + body_lines + tail) + "\n"
             + kernel_descriptor(name, lds_bytes=lds_bytes, kernarg_bytes=kernarg_bytes,
-                                next_free_sgpr=next_free_sgpr)
+                                next_free_sgpr=next_free_sgpr, wg_ids=wg_ids)
             + metadata(name, args=args, lds_bytes=lds_bytes, kernarg_bytes=kernarg_bytes,
                        sgpr_count=next_free_sgpr + 6))
