@@ -47,7 +47,10 @@ TILE = 64 * ROWB        # one 64-key tile
 LDS_K = (0, TILE)       # K buffers
 LDS_V = (2 * TILE, 3 * TILE)
 LDS_FLAG = 4 * TILE
-LDS_BYTES = 4 * TILE + 4
+LDS_EPI = 4 * TILE + 16     # per wave: 32 rows of 272 B staging O for the store
+EPI_ROW = 272               # 256 B + 16 B pad: rows 16 B apart in the banks
+EPI_WAVE = 32 * EPI_ROW
+LDS_BYTES = LDS_EPI + 4 * EPI_WAVE
 LK = 4                  # slots between a K read and its first MFMA
 LV = 4
 NKB = 4                 # K operand registers in rotation (need 2*NKB > LK + 2)
@@ -696,16 +699,38 @@ def _rest(p: Prog, L, lanes) -> str:
     s(f"s_cselect_b32 {sr(S_RL + 2)}, 0, {sr(S_RL + 2)}", S(S_RL + 2) + [("scc", 0)], S(S_RL + 2))
     s(f"s_mov_b32 {sr(S_RL + 3)}, 0x20000", [], S(S_RL + 3))
     s(f"s_lshl_b32 {sr(T0)}, {sr(S_H)}, 8", S(S_H), S(T0))
-    Q, OO, LO, L_, INV, LG = 0, 1, 2, 3, 4, 5   # registers in the free score region
+    Q, LO, L_, INV, LG = 0, 2, 3, 4, 5           # registers in the free score region
     W = 8                                        # 4 values + 2 packed words
+    # O leaves through the wave's LDS staging rows (row = query, 16-byte chunk db*4 + g4) so
+    # that each store instruction writes four whole 256-byte rows; write address
+    # EPW + l32*272 + hi*8, read address EPW + (lane>>4)*272 + (lane&15)*16
+    BW, BR, TA, TB, RBUF, OOS = 24, 25, 26, 27, 28, 44
+    EPW, ROW4 = S_TMP + 4, S_TMP + 5
+    s(f"s_mul_i32 {sr(EPW)}, {sr(S_WAVE)}, {EPI_WAVE}", S(S_WAVE), S(EPW))
+    s(f"s_add_u32 {sr(EPW)}, {sr(EPW)}, {LDS_EPI}", S(EPW), S(EPW))
+    s(f"s_lshl_b32 {sr(ROW4)}, {sr(S_LDO)}, 2", S(S_LDO), S(ROW4))
+    p.valu(f"v_mul_u32_u24_e32 {vr(BW)}, {EPI_ROW}, {vr(V_L32)}", V(V_L32), V(BW))
+    p.valu(f"v_add_u32_e32 {vr(BW)}, {sr(EPW)}, {vr(BW)}", S(EPW) + V(BW), V(BW))
+    p.valu(f"v_lshl_add_u32 {vr(BW)}, {vr(V_HI4)}, 1, {vr(BW)}", V(V_HI4) + V(BW), V(BW))
+    p.valu(f"v_lshrrev_b32_e32 {vr(TA)}, 4, {vr(V_L32)}", V(V_L32), V(TA))
+    p.valu(f"v_lshrrev_b32_e32 {vr(TB)}, 1, {vr(V_HI4)}", V(V_HI4), V(TB))
+    p.valu(f"v_add_u32_e32 {vr(TA)}, {vr(TA)}, {vr(TB)}", V(TA) + V(TB), V(TA))        # lane >> 4
+    p.valu(f"v_and_b32_e32 {vr(TB)}, 15, {vr(V_L32)}", V(V_L32), V(TB))                 # lane & 15
+    p.valu(f"v_mul_u32_u24_e32 {vr(BR)}, {EPI_ROW}, {vr(TA)}", V(TA), V(BR))
+    p.valu(f"v_lshl_add_u32 {vr(BR)}, {vr(TB)}, 4, {vr(BR)}", V(TB) + V(BR), V(BR))
+    p.valu(f"v_add_u32_e32 {vr(BR)}, {sr(EPW)}, {vr(BR)}", S(EPW) + V(BR), V(BR))
+    # global offset of row q0 + (lane >> 4), chunk lane & 15 of this head; +4 rows per read
+    p.valu(f"v_add_u32_e32 {vr(TA)}, {sr(S_Q0)}, {vr(TA)}", S(S_Q0) + V(TA), V(TA))
+    p.valu(f"v_mul_lo_u32 {vr(TA)}, {vr(TA)}, {sr(S_LDO)}", V(TA) + S(S_LDO), V(TA))
+    p.valu(f"v_lshl_add_u32 {vr(OOS)}, {vr(TB)}, 4, {vr(TA)}", V(TB) + V(TA), V(OOS))
+    p.valu(f"v_add_u32_e32 {vr(OOS)}, {sr(T0)}, {vr(OOS)}", S(T0) + V(OOS), V(OOS))
+    for i in range(1, 16):
+        p.valu(f"v_add_u32_e32 {vr(OOS + i)}, {sr(ROW4)}, {vr(OOS + i - 1)}", S(ROW4) + V(OOS + i - 1), V(OOS + i))
     for qb in range(2):
-        # q, O and LSE offsets
+        # q and LSE offsets
         p.valu(f"v_add_u32_e32 {vr(Q)}, {sr(S_Q0)}, {vr(V_L32)}", S(S_Q0) + V(V_L32), V(Q))
         if qb:
             p.valu(f"v_add_u32_e32 {vr(Q)}, 32, {vr(Q)}", V(Q), V(Q))
-        p.valu(f"v_mul_lo_u32 {vr(OO)}, {vr(Q)}, {sr(S_LDO)}", V(Q) + S(S_LDO), V(OO))
-        p.valu(f"v_add_u32_e32 {vr(OO)}, {sr(T0)}, {vr(OO)}", S(T0) + V(OO), V(OO))
-        p.valu(f"v_lshl_add_u32 {vr(OO)}, {vr(V_HI4)}, 1, {vr(OO)}", V(V_HI4) + V(OO), V(OO))
         p.valu(f"v_lshlrev_b32_e32 {vr(LO)}, 2, {vr(Q)}", V(Q), V(LO))
         p.valu(f"v_cmp_eq_u32_e32 vcc, 0, {vr(V_HI4)}", V(V_HI4), [("vcc", 0)])
         p.valu(f"v_mov_b32_e32 {vr(V_T)}, 0x7ffffff0", [], V(V_T))
@@ -732,9 +757,13 @@ def _rest(p: Prog, L, lanes) -> str:
                     p.valu(f"v_mul_f32_e32 {vr(W + j)}, {vr(W + j)}, {vr(INV)}", V(W + j) + V(INV), V(W + j))
                 p.valu(f"v_cvt_pk_f16_f32 {vr(W + 4)}, {vr(W)}, {vr(W + 1)}", V(W, 2), V(W + 4))
                 p.valu(f"v_cvt_pk_f16_f32 {vr(W + 5)}, {vr(W + 2)}, {vr(W + 3)}", V(W + 2, 2), V(W + 5))
-                p.vmem_store(f"buffer_store_dwordx2 {vr(W + 4, 2)}, {vr(OO)}, {sr(S_RQ, 4)}, 0 offen offset:{db * 64 + g4 * 16}",
-                             V(W + 4, 2) + V(OO) + S(S_RQ, 4))
-                W = 8 if W == 16 else 16   # alternate register sets between stores
+                p.ds_write(f"ds_write_b64 {vr(BW)}, {vr(W + 4, 2)} offset:{(db * 4 + g4) * 16}", V(BW) + V(W + 4, 2))
+                W = 8 if W == 16 else 16   # alternate register sets
+        for i in range(8):   # LDS operations of a wave complete in order: reads see the rows
+            R = RBUF + 4 * (i % 4)
+            p.ds_read(f"ds_read_b128 {vr(R, 4)}, {vr(BR)} offset:{i * 4 * EPI_ROW}", V(R, 4), V(BR))
+            p.vmem_store(f"buffer_store_dwordx4 {vr(R, 4)}, {vr(OOS + qb * 8 + i)}, {sr(S_RQ, 4)}, 0 offen",
+                         V(R, 4) + V(OOS + qb * 8 + i) + S(S_RQ, 4))
     p.emit("s_endpgm", BRANCH)
     body_lines = p.finalize()
     return kernel_text(NAME, body_lines, lds_bytes=LDS_BYTES, kernarg_bytes=KERNARG_BYTES,
