@@ -460,16 +460,27 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
         __syncthreads();
     }
 
-    if (q < S) {
-        uint16_t* qrow = dqkv + ((size_t)b * S + q) * ld + (size_t)h * D;
+    // dQ (times scale) leaves through LDS: a lane holds query q, d = db*32 + g4*8 + hi*4 + 0..3;
+    // the wave's rows go to LDS row-major (rows padded by 16 bytes against bank conflicts, the
+    // K/V tiles are free after the loop's last barrier) and come back 16 bytes per lane, so
+    // each store writes whole rows instead of 8 bytes in each of 32 rows.
+    constexpr int SROW = ROWB + 16, RPP = 64 / CPR;  // staging row bytes; rows per pass
+    char* stg = &smem[0][0][0] + wave * 32 * SROW;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-                u32x2 w = {pack2<DT>(dq[db][g4 * 4 + 0] * scale, dq[db][g4 * 4 + 1] * scale),
-                           pack2<DT>(dq[db][g4 * 4 + 2] * scale, dq[db][g4 * 4 + 3] * scale)};
-                *reinterpret_cast<u32x2*>(qrow + db * 32 + g4 * 8 + hi * 4) = w;
-            }
+        for (int g4 = 0; g4 < 4; ++g4) {
+            u32x2 w = {pack2<DT>(dq[db][g4 * 4 + 0] * scale, dq[db][g4 * 4 + 1] * scale),
+                       pack2<DT>(dq[db][g4 * 4 + 2] * scale, dq[db][g4 * 4 + 3] * scale)};
+            *reinterpret_cast<u32x2*>(stg + l32 * SROW + (db * 4 + g4) * 16 + hi * 8) = w;
+        }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 32 / RPP; ++i) {
+        const int row = i * RPP + lane / CPR, chunk = lane % CPR;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * SROW + chunk * 16);
+        if (q0 + row < S)
+            *reinterpret_cast<u32x4*>(dqkv + ((size_t)b * S + q0 + row) * ld + (size_t)h * D + chunk * 8) = v;
     }
 }
 
