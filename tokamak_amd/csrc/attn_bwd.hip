@@ -533,7 +533,13 @@ int launch_bwd_dkdv(const BwdArgs& a) {
     const int r = launch_bwd_dkdv_asm(a);
     return r != 1 ? r : TKM_DISPATCH(launch_dkdv_t, a);
 }
-int launch_bwd_dq(const BwdArgs& a) { return TKM_DISPATCH(launch_dq_read_t, a); }
-int launch_bwd_dq_delta(const BwdArgs& a) { return TKM_DISPATCH(launch_dq_write_t, a); }
+int launch_bwd_dq(const BwdArgs& a) {
+    const int r = launch_bwd_dq_asm(a, false);
+    return r != 1 ? r : TKM_DISPATCH(launch_dq_read_t, a);
+}
+int launch_bwd_dq_delta(const BwdArgs& a) {
+    const int r = launch_bwd_dq_asm(a, true);
+    return r != 1 ? r : TKM_DISPATCH(launch_dq_write_t, a);
+}
 
 }  // namespace tkm

@@ -37,6 +37,7 @@ int launch_fwd_asm(const FwdArgs& a);  // 1 = configuration not handled there
 int launch_bwd_delta(const BwdArgs& a);
 int launch_bwd_dkdv(const BwdArgs& a);
 int launch_bwd_dkdv_asm(const BwdArgs& a);  // 1 = configuration not handled there
+int launch_bwd_dq_asm(const BwdArgs& a, bool compute_d);  // 1 = not handled there
 int launch_bwd_dq(const BwdArgs& a);
 int launch_bwd_dq_delta(const BwdArgs& a);  // dQ, and D written for launch_bwd_dkdv
 
