@@ -1,0 +1,138 @@
+"""Scalar control flow of the generated persistent attention kernels, run on the CPU by
+tests/asm_scalar_sim.py over whole launches: every workgroup ends, all four waves meet at
+every barrier, each item is stored exactly once, descriptors stay inside their tensors, and
+every K/V tile a body or an item start reads was requested earlier with the expected rows."""
+import struct
+
+import pytest
+
+from tokamak_amd.asmgen import attn_fwd, gfx950
+
+from asm_scalar_sim import Fail, Sim
+
+QKV, OUT, LSE, KVLEN = 0x10000000, 0x40000000, 0x70000000, 0x7F000000
+
+
+def reciprocal(d, limit):
+    if d == 1:
+        return 0
+    m = ((1 << 32) + d - 1) // d
+    e = m * d - (1 << 32)
+    assert m <= 0xFFFFFFFF and (limit - 1) * e < (1 << 32)
+    return m
+
+
+_lines = {}
+
+
+def fwd_lines():
+    if "fwd" not in _lines:
+        captured = []
+        orig = gfx950.Prog.finalize
+
+        def finalize(self):
+            out = orig(self)
+            captured.append(out)
+            return out
+        gfx950.Prog.finalize = finalize
+        try:
+            attn_fwd.build()
+        finally:
+            gfx950.Prog.finalize = orig
+        _lines["fwd"] = captured[-1]
+    return _lines["fwd"]
+
+
+def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, overflow=()):
+    n_qblk = (S + 255) // 256
+    bhq, G = B * Hq, Hq // Hkv
+    n_items = n_qblk * bhq
+    n_wg = min(n_wg, n_items)
+    ldb, ldo = (Hq + 2 * Hkv) * 256, Hq * 256
+    kv = None if kv_len is None else [int(x) for x in kv_len]
+    args = struct.pack("<QQQQIIIfIIIIIIIIIIII", QKV, OUT, LSE, KVLEN if kv else 0, S, Hq, Hkv,
+                       0.127, int(causal), n_qblk, ldb, ldo, G, n_wg, n_items, bhq,
+                       reciprocal(bhq, n_items), reciprocal(Hq, bhq), reciprocal(G, Hq), 0)
+    assert len(args) == attn_fwd.KERNARG_BYTES
+    mem = {"qkv": (QKV, B * S * ldb, ldb, 256), "out": (OUT, B * S * ldo, ldo, ldo),
+           "lse": (LSE, B * Hq * S * 4, 4, 4), "kv_len": (KVLEN, 4 * B, 4, 4)}
+
+    def kvl(b):
+        return S if kv is None else max(0, min(kv[b], S))
+
+    def kvend(b, qblk):
+        return min(kvl(b), 256 * qblk + 256) if causal else kvl(b)
+
+    def tile(b, kvh, qblk, t, v):
+        col = (Hq + (Hkv if v else 0) + kvh) * 256
+        rows = max(0, min(64, kvend(b, qblk) - 64 * t))
+        return QKV + (b * S + 64 * t) * ldb + col, rows * ldb
+
+    def item_of(w):
+        s = w.s
+        b, h, kvh, q0 = s[attn_fwd.S_BA], s[attn_fwd.S_HA], s[attn_fwd.S_KVHA], s[attn_fwd.S_Q0]
+        return b, h, kvh, q0, q0 >> 8
+
+    def expect(w, words):
+        b, h, kvh, q0, qblk = item_of(w)
+        s = w.s
+        if words[0] == "start":
+            assert kvh == h // G
+            nt = max(1, -(-kvend(b, qblk) // 64))
+            act = 0 if kvl(b) == 0 else (min(nt, q0 // 64 + 1) if causal else nt)
+            maskb = min(kvl(b) // 64, q0 // 64 if causal else nt)
+            got = (s[attn_fwd.S_NT], s[attn_fwd.S_ACTEND], s[attn_fwd.S_MASKB], s[attn_fwd.S_IT])
+            if got != (nt, act, maskb, 0):
+                raise Fail(f"item (b {b}, h {h}, q0 {q0}): NT/ACTEND/MASKB/IT {got}, expected {(nt, act, maskb, 0)}")
+            u = int(words[1])
+            return [(attn_fwd.LDS_K[u], *tile(b, kvh, qblk, 0, False))] if act else []
+        if words[0] == "body":
+            variant, u, t = words[1], int(words[2]), s[attn_fwd.S_IT]
+            code = s[attn_fwd.S_CODE] & ~16
+            if dict(attn_fwd.VARIANTS).get(variant) not in (code, code & ~1 if variant == "idle" else code):
+                raise Fail(f"body {variant} entered with code {code}")
+            if variant == "full":
+                return [(attn_fwd.LDS_K[u ^ 1], *tile(b, kvh, qblk, t + 1, False)),
+                        (attn_fwd.LDS_V[u], *tile(b, kvh, qblk, t, True))]
+            if variant in ("last", "lastm"):
+                return [(attn_fwd.LDS_V[u], *tile(b, kvh, qblk, t, True))]
+        return []
+
+    stored = {}
+
+    def on_event(w, words):
+        if words[0] == "epilogue":
+            b, h, _, q0, _ = item_of(w)
+            key = (b, h, q0)
+            stored[key] = stored.get(key, 0) + 1
+
+    sim = Sim(fwd_lines(), args, mem, kv, n_wg, expect, on_event, overflow=overflow)
+    sim.run()
+    want = {(b, h, 256 * z + 64 * wv) for b in range(B) for h in range(Hq) for z in range(n_qblk) for wv in range(4)}
+    assert set(stored) == want and all(c == 1 for c in stored.values()), \
+        (len(stored), len(want), [k for k, c in stored.items() if c != 1][:4])
+    # O and LSE stores of each wave target its item's rows
+    assert {m for _, _, m, _, _ in sim.stores} <= {"out", "lse", None}
+    return sim
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", [
+    (1, 512, 2, 1, True, None, 3),
+    (2, 700, 4, 2, True, None, 5),
+    (2, 700, 4, 2, False, None, 4),
+    (2, 1000, 2, 2, False, [1000, 333], 3),
+    (3, 600, 2, 1, True, [0, 65, 600], 2),
+    (1, 64, 1, 1, True, None, 1),
+    (1, 1, 1, 1, False, None, 1),
+    (2, 2048, 4, 4, True, None, 7),
+    (1, 300, 3, 1, True, [129], 256),
+])
+def test_fwd_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg):
+    run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg)
+
+
+def test_fwd_scalar_flow_redo():
+    """An overflow vote in some items: the item is repeated with the stream rewound, every
+    tile still arrives as expected and each item is stored once."""
+    run_fwd(2, 700, 4, 2, True, None, 3, overflow={(0, 0), (1, 2), (2, 5)})
+    run_fwd(1, 512, 2, 1, False, [300], 2, overflow={(0, 1), (1, 0)})

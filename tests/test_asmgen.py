@@ -11,11 +11,8 @@ import pytest
 from tokamak_amd import build as tb
 from tokamak_amd.asmgen import attn_dkdv, attn_dq, attn_fwd, gfx950
 
-# (generator, workgroup-id SGPRs, registers defined on entry or on every path to their reads).
-# The forward's exact second pass reads the start values -m (V_CINIT) that the code after the
-# main loop writes before jumping back to the loop head: later in program order, not unset.
-KERNELS = [(attn_fwd, (1, 1, 1), {("s", 8 + i) for i in range(18)} |
-            {("v", attn_fwd.V_CINIT + i) for i in range(32)}),
+# (generator, workgroup-id SGPRs, registers defined on entry: the kernel arguments)
+KERNELS = [(attn_fwd, (1, 0, 0), {("s", 8 + i) for i in range(24)}),
            (attn_dkdv, (1, 0, 0), {("s", 8 + i) for i in range(24)} | {("s", 90), ("s", 91)}),
            (attn_dq, (1, 0, 0), {("s", 8 + i) for i in range(34)})]
 

@@ -100,6 +100,8 @@ class Ins:
     keep_lgkm: bool = False
     skip_xdl: object = None
     pending: list = field(default_factory=list)
+    # VMEM_LOAD: not tracked by the automatic waits (the kernel waits for it explicitly)
+    untracked: bool = False
 
 
 class Prog:
@@ -155,8 +157,10 @@ class Prog:
     def ds_write(self, text, addr_data):
         self.emit(text, DS_WRITE, addr_data, [])
 
-    def vmem_load(self, text, dst, reads):
-        self.emit(text, VMEM_LOAD, reads, dst)
+    def vmem_load(self, text, dst, reads, untracked=False):
+        """untracked: no automatic wait for the destination (nor at branches); the kernel
+        itself waits (vmcnt) before anything touches it."""
+        self.emit(text, VMEM_LOAD, reads, dst, untracked=untracked)
 
     def vmem_store(self, text, reads):
         self.emit(text, VMEM_STORE, reads, [])
@@ -395,7 +399,7 @@ class Prog:
                     last_xdl_w.pop(r, None)
                     last_valu_w.pop(r, None)
                     last_trans_w.pop(r, None)
-                vm.append(set(regs_w))
+                vm.append(set() if ins.untracked else set(regs_w))
             elif k == SMEM:
                 for r in regs_w:
                     last_valu_sw.pop(r, None)
