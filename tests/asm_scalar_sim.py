@@ -122,11 +122,13 @@ class Sim:
     lane row touches) of the tensors the descriptors may cover; kv_len: list or None (its pointer in the arguments is nonzero then);
     n_wg: grid; overflow: set of (wg, item round) whose overflow vote says yes; expect: a
     callable (wave, event words) -> list of checks [(lds_base, base, nrec)] of LDS tiles
-    the wave reads at that event, or None; on_event(wave, words) for bookkeeping."""
+    the wave reads at that event, or None; on_event(wave, words) for bookkeeping; wave_vgpr:
+    the VGPR holding v0 >> 6 when the prologue reads the wave index from it."""
 
     def __init__(self, lines, kernarg, mem, kv_len, n_wg, expect, on_event=None, overflow=(),
-                 tile_bytes=16384, max_steps=2_000_000):
+                 tile_bytes=16384, max_steps=2_000_000, wave_vgpr=64):
         self.ins, self.labels = parse(lines)
+        self.wave_vgpr = wave_vgpr
         self.kernarg = kernarg
         self.mem = mem
         self.kv_len = kv_len
@@ -137,6 +139,7 @@ class Sim:
         self.tile_bytes = tile_bytes
         self.max_steps = max_steps
         self.stores = []
+        self.clock = 0
 
     # ---------------------------------------------------------------- memory checks
     def _desc(self, w, o):
@@ -238,8 +241,8 @@ class Sim:
             return
         if op == "v_readfirstlane_b32":
             src = a[1]
-            if src == ("v", 64, 1):
-                w.put(a[0], w.wave)       # wave index (v64 = v0 >> 6 in the prologue)
+            if src == ("v", self.wave_vgpr, 1):
+                w.put(a[0], w.wave)       # wave index (v0 >> 6 in the prologue)
             else:
                 key = (w.wg, w.s.get(32))
                 w.put(a[0], 1 if key in self.overflow else 0)
@@ -278,7 +281,11 @@ class Sim:
             base, nrec, _ = self._desc(w, a[2])
             self.stores.append((w.wg, w.wave, self._inside(base, nrec, text), base, nrec))
             return
-        if op.startswith("ds_") or op.startswith("s_memtime") or op.startswith("s_memrealtime"):
+        if op in ("s_memtime", "s_memrealtime"):
+            self.clock += 1000
+            w.put(a[0], self.clock, True)
+            return
+        if op.startswith("ds_"):
             return
         b64 = op.endswith("_b64") or op.endswith("_u64")
         if op in ("s_mov_b32", "s_mov_b64"):
@@ -293,6 +300,10 @@ class Sim:
             w.put(a[0], x - y)
         elif op == "s_sub_i32":
             w.put(a[0], _s32(g(a[1])) - _s32(g(a[2])))
+        elif op in ("s_lshl1_add_u32", "s_lshl2_add_u32"):
+            r = (g(a[1]) << (1 if op == "s_lshl1_add_u32" else 2)) + g(a[2])
+            w.scc = int(r > M32)
+            w.put(a[0], r)
         elif op == "s_mul_i32":
             w.put(a[0], g(a[1]) * g(a[2]))
         elif op == "s_mul_hi_u32":

@@ -136,3 +136,117 @@ def test_fwd_scalar_flow_redo():
     tile still arrives as expected and each item is stored once."""
     run_fwd(2, 700, 4, 2, True, None, 3, overflow={(0, 0), (1, 2), (2, 5)})
     run_fwd(1, 512, 2, 1, False, [300], 2, overflow={(0, 1), (1, 0)})
+
+
+# ---------------------------------------------------------------- backward kernels
+from tokamak_amd.asmgen import attn_dkdv, attn_dq  # noqa: E402
+
+O_, DOUT, QUADS, DELTA, DQKV = 0x20000000, 0x30000000, 0x50000000, 0x60000000, 0x80000000
+
+
+def _gen_lines(gen):
+    key = gen.NAME
+    if key not in _lines:
+        captured = []
+        orig = gfx950.Prog.finalize
+
+        def finalize(self):
+            out = orig(self)
+            captured.append(out)
+            return out
+        gfx950.Prog.finalize = finalize
+        try:
+            gen.build()
+        finally:
+            gfx950.Prog.finalize = orig
+        _lines[key] = captured[-1]
+    return _lines[key]
+
+
+def _bwd_mem(B, S, Hq, Hkv, kv):
+    ldb, ldo = (Hq + 2 * Hkv) * 256, Hq * 256
+    sp = (S + 31) // 32 * 32
+    return {"qkv": (QKV, B * S * ldb, ldb, 256), "dqkv": (DQKV, B * S * ldb, ldb, 256),
+            "o": (O_, B * S * ldo, ldo, 256), "dout": (DOUT, B * S * ldo, ldo, 256),
+            "lse": (LSE, B * Hq * S * 4, 4, 4), "delta": (DELTA, B * Hq * S * 4, 4, 4),
+            "quads": (QUADS, B * Hq * sp * 8, 16, 16), "kv_len": (KVLEN, 4 * B, 4, 4)}
+
+
+def run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg):
+    n_kblk, bh = (S + 127) // 128, B * Hkv
+    n_items = n_kblk * bh
+    n_wg = min(n_wg, n_items)
+    ldb, ldo = (Hq + 2 * Hkv) * 256, Hq * 256
+    kv = None if kv_len is None else [int(x) for x in kv_len]
+    args = struct.pack("<QQQQQIIIfIIIIfIIIIIII", QKV, DOUT, QUADS, DQKV, KVLEN if kv else 0, S, Hq, Hkv,
+                       0.127, int(causal), ldb, ldo, Hq // Hkv, 0.088, n_kblk, (S + 31) // 32 * 32, n_wg,
+                       n_items, bh, reciprocal(bh, n_items), reciprocal(Hkv, bh))
+    assert len(args) == attn_dkdv.KERNARG_BYTES
+    stored = {}
+
+    def on_event(w, words):
+        if words[0] == "epilogue":
+            key = (w.s[attn_dkdv.S_BA], w.s[attn_dkdv.S_KVHA], w.s[attn_dkdv.S_KW0])
+            stored[key] = stored.get(key, 0) + 1
+
+    sim = Sim(_gen_lines(attn_dkdv), args, _bwd_mem(B, S, Hq, Hkv, kv), kv, n_wg, None, on_event,
+              wave_vgpr=attn_dkdv.V_PT)
+    sim.run()
+    want = {(b, h, 128 * z + 32 * w) for b in range(B) for h in range(Hkv) for z in range(n_kblk) for w in range(4)}
+    assert set(stored) == want and all(c == 1 for c in stored.values()), \
+        (len(stored), len(want), [k for k, c in stored.items() if c != 1][:4])
+    return sim
+
+
+def run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d):
+    n_qblk, bhq, G = (S + 255) // 256, B * Hq, Hq // Hkv
+    n_items = n_qblk * bhq
+    n_wg = min(n_wg, n_items)
+    ldb, ldo = (Hq + 2 * Hkv) * 256, Hq * 256
+    kv = None if kv_len is None else [int(x) for x in kv_len]
+    args = struct.pack("<QQQQQQQQIIIfIIIIfIIIIIIIII", QKV, O_, DOUT, LSE, DELTA, QUADS, DQKV,
+                       KVLEN if kv else 0, S, Hq, Hkv, 0.127, int(causal), ldb, ldo, G, 0.088, n_qblk,
+                       (S + 31) // 32 * 32, n_wg, n_items, bhq, reciprocal(bhq, n_items),
+                       reciprocal(Hq, bhq), reciprocal(G, Hq), int(compute_d))
+    assert len(args) == attn_dq.KERNARG_BYTES
+    stored = {}
+
+    def on_event(w, words):
+        if words[0] == "epilogue":
+            key = (w.s[attn_dq.S_BA], w.s[attn_dq.S_HA], w.s[attn_dq.S_Q0])
+            stored[key] = stored.get(key, 0) + 1
+
+    sim = Sim(_gen_lines(attn_dq), args, _bwd_mem(B, S, Hq, Hkv, kv), kv, n_wg, None, on_event,
+              wave_vgpr=attn_dq.V_PT)
+    sim.run()
+    want = {(b, h, 256 * z + 64 * w) for b in range(B) for h in range(Hq) for z in range(n_qblk) for w in range(4)}
+    assert set(stored) == want and all(c == 1 for c in stored.values()), \
+        (len(stored), len(want), [k for k, c in stored.items() if c != 1][:4])
+    return sim
+
+
+BWD_CASES = [(1, 512, 2, 1, True, None, 3), (2, 700, 4, 2, True, None, 5), (2, 700, 4, 2, False, None, 4),
+             (2, 1000, 2, 2, False, [1000, 333], 3), (3, 600, 2, 1, True, [0, 65, 600], 2),
+             (1, 64, 1, 1, True, None, 1), (1, 1, 1, 1, False, None, 1), (1, 300, 3, 1, True, [129], 256)]
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", BWD_CASES)
+def test_dkdv_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg):
+    """Every workgroup ends, waves meet at every barrier, DMA and stores stay in their tensors,
+    and each (key block, batch, kv head) item's dK and dV rows are stored."""
+    sim = run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg)
+    assert {m for _, _, m, _, _ in sim.stores} <= {"dqkv", None}
+    ldb = (Hq + 2 * Hkv) * 256
+    heads = {(base - DQKV) % ldb // 256 for _, _, m, base, _ in sim.stores if m}
+    assert heads == set(range(Hq, Hq + 2 * Hkv))
+
+
+@pytest.mark.parametrize("compute_d", [True, False])
+@pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", BWD_CASES)
+def test_dq_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d):
+    sim = run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d)
+    stored = {m for _, _, m, _, _ in sim.stores}
+    assert stored <= ({"dqkv", "delta", "quads", None} if compute_d else {"dqkv", None})
+    ldb = (Hq + 2 * Hkv) * 256
+    heads = {(base - DQKV) % ldb // 256 for _, _, m, base, _ in sim.stores if m == "dqkv"}
+    assert heads == set(range(Hq))

@@ -85,3 +85,41 @@ def test_split_scalar_keeps_scc_pairs():
             flat.append([i.text.split()[0] for i in c])
     for c in flat:   # an SCC reader never starts a chunk
         assert c[0] not in ("s_cselect_b32", "s_addc_u32")
+
+
+def _dead_loads(prog):
+    """Loads (LDS reads, buffer loads) whose destination another load overwrites before any
+    instruction reads it, within a basic block: the first load's data is lost."""
+    pending = {}
+    bad = []
+    for ins in prog.ins:
+        if ins.kind in (gfx950.LABEL, gfx950.BRANCH):
+            pending.clear()
+            continue
+        for r in ins.reads:
+            pending.pop(r, None)
+        if ins.kind in (gfx950.DS_READ, gfx950.VMEM_LOAD):
+            for r in ins.writes:
+                if r in pending:
+                    bad.append((pending[r], ins.text))
+            for r in ins.writes:
+                pending[r] = ins.text
+        else:
+            for r in ins.writes:
+                pending.pop(r, None)
+    return bad
+
+
+@pytest.mark.parametrize("gen,wg_ids,kernargs", KERNELS, ids=lambda x: getattr(x, "NAME", ""))
+def test_no_dead_loads(gen, wg_ids, kernargs):
+    prog, _ = _program(gen)
+    bad = _dead_loads(prog)
+    assert not bad, bad[:4]
+
+
+def test_dead_load_check_catches_register_reuse(monkeypatch):
+    """Six row reads in flight into four rotating registers (the lookahead above the number
+    of read registers): the check must flag it."""
+    monkeypatch.setattr(attn_dq, "LK", 6)
+    prog, _ = _program(attn_dq)
+    assert _dead_loads(prog)

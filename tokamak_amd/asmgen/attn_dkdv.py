@@ -57,6 +57,7 @@ LK = 4                              # slots between a row read and its MFMA
 LV = 4                              # slots between a transposed read pair and its MFMA
 NRB = 6                             # row-read registers in rotation (x4)
 NTB = 6                             # transposed-read registers in rotation (x4)
+assert LK <= NRB                    # the first LK row reads of a tile are in flight across bodies
 EW_SPLIT = False                    # elementwise pairs 4..7 in the dV/dK half (measured slower)
 
 ARGS = [(0, 8, "ptr"), (8, 8, "ptr"), (16, 8, "ptr"), (24, 8, "ptr"), (32, 8, "ptr")] + \
@@ -106,6 +107,7 @@ assert V_PT + 13 <= 256
 
 # ---- AGPRs
 A_DV, A_DK, A_K, A_V = 0, 64, 128, 160
+A_NK, A_NV = 192, 224     # the next item's K and V rows as loaded (before the K scaling)
 ACC = set(A(A_DV, 128))
 
 # variants of a body: (label, S/dP of the next tile, elementwise + dV/dK of this tile, masked)
@@ -539,6 +541,58 @@ class Body:
             p.vmem_load(f"buffer_load_dwordx4 {ar(A_V + ks * 4, 4)}, {vr(KO)}, {sr(RV, 4)}, 0 offen offset:{ks * 32}",
                         A(A_V + ks * 4, 4), V(KO) + S(RV, 4))
 
+    def kv_prefetch(self, i, sfx):
+        """Loads of item i's K and V rows of this wave's keys (z*128 + 32*wave + l32; rows past
+        kv_len read as zero) into the spare AGPRs, untracked: they are issued before the
+        current item's epilogue, whose time covers their latency; kv_take waits for them.
+        Touches no state of the current item."""
+        p, s = self.p, self.s
+        Z, B, KVH, KVL, KW0, ROWS = (S_TMP + k for k in range(6))
+        RK, RV, T0 = S_TMP + 6, S_TMP + 10, S_TMP + 17
+        assert i not in (Z, B, KVH, KVL, KW0, ROWS, T0) and i not in range(RK, RV + 4)
+        self.decode(i, Z, B, KVH)
+        self.kvl_of(B, KVL, f".Lpk_{sfx}")
+        s(f"s_lshl_b32 {sr(KW0)}, {sr(Z)}, 7", S(Z), S(KW0))
+        s(f"s_lshl_b32 {sr(T0)}, {sr(S_WAVE)}, 5", S(S_WAVE), S(T0))
+        s(f"s_add_u32 {sr(KW0)}, {sr(KW0)}, {sr(T0)}", S(KW0) + S(T0), S(KW0))
+        s(f"s_sub_u32 {sr(ROWS)}, {sr(KVL)}, {sr(KW0)}", S(KVL) + S(KW0), S(ROWS))
+        s(f"s_max_i32 {sr(ROWS)}, {sr(ROWS)}, 0", S(ROWS), S(ROWS))
+        s(f"s_min_i32 {sr(ROWS)}, {sr(ROWS)}, 32", S(ROWS), S(ROWS))
+        s(f"s_mul_i32 {sr(T0)}, {sr(B)}, {sr(S_SEQ)}", S(B) + S(S_SEQ), S(T0))
+        s(f"s_add_u32 {sr(T0)}, {sr(T0)}, {sr(KW0)}", S(T0) + S(KW0), S(T0))      # first key row
+        COL = Z
+        s(f"s_add_u32 {sr(COL)}, {sr(S_HQ)}, {sr(KVH)}", S(S_HQ) + S(KVH), S(COL))
+        s(f"s_lshl_b32 {sr(COL)}, {sr(COL)}, 8", S(COL), S(COL))
+        for rs, more in ((RK, False), (RV, True)):
+            if more:
+                s(f"s_lshl_b32 {sr(B)}, {sr(S_HKV)}, 8", S(S_HKV), S(B))
+                s(f"s_add_u32 {sr(COL)}, {sr(COL)}, {sr(B)}", S(COL) + S(B), S(COL))
+            self.add64(rs, S_QKV, T0, S_LDB, COL)
+            s(f"s_and_b32 {sr(rs + 1)}, {sr(rs + 1)}, 0xffff", S(rs + 1), S(rs + 1))
+            s(f"s_mul_i32 {sr(rs + 2)}, {sr(ROWS)}, {sr(S_LDB)}", S(ROWS) + S(S_LDB), S(rs + 2))
+            s(f"s_mov_b32 {sr(rs + 3)}, 0x20000", [], S(rs + 3))
+        KO = V_T
+        p.valu(f"v_mul_lo_u32 {vr(KO)}, {vr(V_L32)}, {sr(S_LDB)}", V(V_L32) + S(S_LDB), V(KO))
+        p.valu(f"v_lshl_add_u32 {vr(KO)}, {vr(V_HI4)}, 2, {vr(KO)}", V(V_HI4) + V(KO), V(KO))
+        for base, rs in ((A_NK, RK), (A_NV, RV)):
+            for ks in range(8):
+                p.vmem_load(f"buffer_load_dwordx4 {ar(base + ks * 4, 4)}, {vr(KO)}, {sr(rs, 4)}, 0 offen offset:{ks * 32}",
+                            A(base + ks * 4, 4), V(KO) + S(rs, 4), untracked=True)
+
+    def kv_take(self):
+        """The prefetched K and V into place: V as loaded, K scaled by scale*log2e to fp16."""
+        p = self.p
+        p.waitcnt(vm=0)
+        for i in range(32):
+            p.valu(f"v_accvgpr_mov_b32 {ar(A_V + i)}, {ar(A_NV + i)}", A(A_NV + i), A(A_V + i))
+        t0, t1 = V_T + 1, V_T + 2
+        for i in range(32):   # K * scale*log2e, rounded to fp16
+            p.valu(f"v_accvgpr_read_b32 {vr(i)}, {ar(A_NK + i)}", A(A_NK + i), V(i))
+            p.valu(f"v_fma_mix_f32 {vr(t0)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t0))
+            p.valu(f"v_fma_mix_f32 {vr(t1)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t1))
+            p.valu(f"v_cvt_pk_f16_f32 {vr(i)}, {vr(t0)}, {vr(t1)}", V(t0, 2), V(i))
+            p.valu(f"v_accvgpr_write_b32 {ar(A_K + i)}, {vr(i)}", V(i), A(A_K + i))
+
     def zero_acc(self):
         p = self.p
         for i in range(4):
@@ -562,6 +616,7 @@ class Body:
         store instruction writes four whole 256-byte rows.  Keys past S are dropped by the
         descriptors."""
         p, s = self.p, self.s
+        p.comment("epilogue")
         RK, RV = S_TMP + 6, S_TMP + 10   # 4-aligned
         T0, COL, T2, EPW = S_TMP, S_TMP + 1, S_TMP + 2, S_TMP + 3
         s(f"s_mul_i32 {sr(T0)}, {sr(S_BA)}, {sr(S_SEQ)}", S(S_BA) + S(S_SEQ), S(T0))
@@ -871,24 +926,29 @@ def _dispatch(b: Body, u: int):
 
 
 def _boundary(b: Body, u: int):
-    """End of the current item before body residue u: store its dK, dV; take the next item
-    (or stop), load its K, V and start it on tile it (buffer u), whose data the DMA stream
-    has already delivered."""
+    """End of the current item before body residue u: request the next item's K, V rows (their
+    latency hides behind the epilogue), store the current dK, dV; then the next item (or stop):
+    K, V into place, start on tile it (buffer u), whose data the DMA stream has already
+    delivered."""
     p, s = b.p, b.s
     I = S_TMP + 16
     p.label(f".Lbnd{u}")
     p.nop(16)                 # MFMA results of the last body before the accumulator reads
     p.waitcnt(lgkm=0)
+    K1 = S_TMP
+    s(f"s_add_u32 {sr(K1)}, {sr(S_KA)}, 1", S(S_KA), S(K1))
+    b.item_index(K1, I)
+    s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
+    p.branch(f"s_cbranch_scc1 .Lnopf{u}", [("scc", 0)], skip_xdl=ACC)
+    b.kv_prefetch(I, f"b{u}")
+    p.label(f".Lnopf{u}")
     b.epilogue()
     s(f"s_add_u32 {sr(S_KA)}, {sr(S_KA)}, 1", S(S_KA), S(S_KA))
-    b.item_index(S_KA, I)
     s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
     p.branch("s_cbranch_scc1 .Lexit", [("scc", 0)], skip_xdl=ACC)
     b.decode_a(I, f"b{u}")
-    b.kv_load()
     b.zero_acc()
-    b.scale_k()
-    p.waitcnt(vm=0)
+    b.kv_take()
     b.start_item(u, f"b{u}")
 
 

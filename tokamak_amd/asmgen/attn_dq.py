@@ -47,10 +47,12 @@ LDS_EPI = NBUF * BUFB               # per wave: 32 rows of 272 B staging dQ for 
 EPI_ROW = 272
 EPI_WAVE = 32 * EPI_ROW
 LDS_BYTES = LDS_EPI + 4 * EPI_WAVE
-LK = 4                              # slots between a row read and its first MFMA
-LV = 4                              # slots between a transposed read pair and its first MFMA
+LK = 3                              # slots between a row read and its first MFMA
+LV = 3                              # slots between a transposed read pair and its first MFMA
+                                    # (4 and 4: ~110 cycles more per body, measured)
 NRB = 4                             # row-read registers in rotation (x4)
 NTB = 4                             # transposed-read registers in rotation (x4)
+assert LK <= NRB                    # the first LK row reads of a tile are in flight across bodies
 
 ARGS = [(8 * i, 8, "ptr") for i in range(8)] + [(64 + 4 * i, 4, "val") for i in range(18)]
 KERNARG_BYTES = 136
@@ -597,6 +599,7 @@ class Body:
         """dQ^T * scale of the current item: lane holds row q0 + 32qb + l32, d = db*32 + g4*8 +
         hi*4 + 0..3; through the wave's LDS staging rows, whole 256-byte rows per store."""
         p, s = self.p, self.s
+        p.comment("epilogue")
         RQ = S_TMP + 4
         T0, COL, NREC, EPW, ROW4 = S_TMP, S_TMP + 1, S_TMP + 2, S_TMP + 3, S_TMP + 8
         s(f"s_mul_i32 {sr(T0)}, {sr(S_BA)}, {sr(S_SEQ)}", S(S_BA) + S(S_SEQ), S(T0))

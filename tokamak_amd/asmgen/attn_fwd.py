@@ -56,10 +56,12 @@ LDS_EPI = 4 * TILE + 16     # per wave: 32 rows of 272 B staging O for the store
 EPI_ROW = 272               # 256 B + 16 B pad: rows 16 B apart in the banks
 EPI_WAVE = 32 * EPI_ROW
 LDS_BYTES = LDS_EPI + 4 * EPI_WAVE
-LK = 4                  # slots between a K read and its first MFMA
-LV = 4
+LK = 5                  # slots between a K read and its first MFMA (4 puts the K and V reads
+LV = 3                  # on the DMA slots' parity: ~120 cycles more per tile, measured)
 NKB = 4                 # K operand registers in rotation (need 2*NKB > LK + 2)
 NVB = 4
+assert 2 * NKB > LK + 2 and 2 * NVB > LV + 2   # a read reuses its register four reads later
+DMA0 = 2                # slot of the first DMA request (then one every four slots)
 MFMA = "v_mfma_f32_32x32x16_f16"
 
 # kernel arguments (byte offsets in the kernarg segment): qkv, out, lse, kv_len, then
@@ -107,6 +109,7 @@ V_T = V_P + 4               # temporaries of the item boundary, when P is free (
 # ---- AGPRs
 A_O = 0                 # o[db][qb] at (db*2+qb)*16
 A_Q = 128               # q[qb][ks] at 128 + (qb*8+ks)*4
+A_QN = 192              # the next item's Q as loaded (same order), before the prescale
 ACC = set(A(A_O, 128))
 
 # body variants by code: 4*act(t+1) + 2*act(t) + mask(t); 8 = the item's end
@@ -537,7 +540,7 @@ class Body:
         kbase, vbase = LDS_K[Jn], LDS_V[J]
         exp_at = {(7 * n) // 4: n for n in range(32)}
         pack_at = {(7 * n) // 4 + 1: n for n in range(32)}
-        dma_at = {2 + 4 * i: i for i in range(8)}
+        dma_at = {DMA0 + 4 * i: i for i in range(8)}
         kissued = 0
         while kissued * 2 - LK < 0:
             self.k_read(kissued, kbase)
@@ -596,37 +599,66 @@ class Body:
         p.branch(f"s_branch .Ldisp{Jn}", skip_xdl=ACC)
 
     # ---------------------------------------------------------------- item start / end
-    def load_q(self):
-        """Q of the wave's 64 rows: lane (l32, hi) loads row q0 + 32qb + l32, bytes hi*16 +
-        32ks .. +15; prescaled by sl2, rounded to fp16, into the Q AGPRs."""
+    def q_loads(self, b, h, q0, dst_acc):
+        """Issue the loads of Q rows q0 + 32qb + l32 of (batch b, head h) for this wave: lane
+        (l32, hi) loads bytes hi*16 + 32ks .. +15; into VGPRs 0..63 (tracked) or, dst_acc,
+        into the next-item AGPRs (untracked: the next loop body's vmcnt(0) covers them)."""
         p, s = self.p, self.s
-        T0, COL, NREC, LO, HI = S_TMP, S_TMP + 1, S_TMP + 2, S_TMP + 3, S_TMP + 4
-        s(f"s_mul_i32 {sr(T0)}, {sr(S_BA)}, {sr(S_SEQ)}", S(S_BA) + S(S_SEQ), S(T0))
-        s(f"s_lshl_b32 {sr(COL)}, {sr(S_HA)}, 8", S(S_HA), S(COL))
-        self.add64(S_RQ, S_QKV, T0, S_LDB, COL, LO, HI)
-        s(f"s_and_b32 {sr(S_RQ + 1)}, {sr(S_RQ + 1)}, 0xffff", S(S_RQ + 1), S(S_RQ + 1))
-        s(f"s_mul_i32 {sr(S_RQ + 2)}, {sr(S_SEQ)}, {sr(S_LDB)}", S(S_SEQ) + S(S_LDB), S(S_RQ + 2))
-        s(f"s_mov_b32 {sr(S_RQ + 3)}, 0x20000", [], S(S_RQ + 3))
+        RQ = S_TMP + 16
+        T0, COL, LO, HI = S_TMP + 8, S_TMP + 9, S_TMP + 10, S_TMP + 11
+        s(f"s_mul_i32 {sr(T0)}, {sr(b)}, {sr(S_SEQ)}", S(b) + S(S_SEQ), S(T0))
+        s(f"s_lshl_b32 {sr(COL)}, {sr(h)}, 8", S(h), S(COL))
+        self.add64(RQ, S_QKV, T0, S_LDB, COL, LO, HI)
+        s(f"s_and_b32 {sr(RQ + 1)}, {sr(RQ + 1)}, 0xffff", S(RQ + 1), S(RQ + 1))
+        s(f"s_mul_i32 {sr(RQ + 2)}, {sr(S_SEQ)}, {sr(S_LDB)}", S(S_SEQ) + S(S_LDB), S(RQ + 2))
+        s(f"s_mov_b32 {sr(RQ + 3)}, 0x20000", [], S(RQ + 3))
         QOFF = V_P  # two registers
         p.valu(f"v_lshlrev_b32_e32 {vr(V_T)}, 2, {vr(V_HI4)}", V(V_HI4), V(V_T))     # 16*hi
         for qb in range(2):
-            p.valu(f"v_add_u32_e32 {vr(QOFF + qb)}, {sr(S_Q0)}, {vr(V_L32)}", S(S_Q0) + V(V_L32), V(QOFF + qb))
+            p.valu(f"v_add_u32_e32 {vr(QOFF + qb)}, {sr(q0)}, {vr(V_L32)}", S(q0) + V(V_L32), V(QOFF + qb))
             if qb:
                 p.valu(f"v_add_u32_e32 {vr(QOFF + qb)}, 32, {vr(QOFF + qb)}", V(QOFF + qb), V(QOFF + qb))
             p.valu(f"v_mul_lo_u32 {vr(QOFF + qb)}, {vr(QOFF + qb)}, {sr(S_LDB)}", V(QOFF + qb) + S(S_LDB), V(QOFF + qb))
             p.valu(f"v_add_u32_e32 {vr(QOFF + qb)}, {vr(QOFF + qb)}, {vr(V_T)}", V(QOFF + qb) + V(V_T), V(QOFF + qb))
         for qb in range(2):
             for ks in range(8):
-                dst = (qb * 8 + ks) * 4
-                p.vmem_load(f"buffer_load_dwordx4 {vr(dst, 4)}, {vr(QOFF + qb)}, {sr(S_RQ, 4)}, 0 offen offset:{ks * 32}",
-                            V(dst, 4), V(QOFF + qb) + S(S_RQ, 4))
-        # prescale: word w of a Q fragment -> two f32 (x * sl2) -> fp16 pair -> AGPR
+                i = (qb * 8 + ks) * 4
+                dst, regs = (ar(A_QN + i, 4), A(A_QN + i, 4)) if dst_acc else (vr(i, 4), V(i, 4))
+                p.vmem_load(f"buffer_load_dwordx4 {dst}, {vr(QOFF + qb)}, {sr(RQ, 4)}, 0 offen offset:{ks * 32}",
+                            regs, V(QOFF + qb) + S(RQ, 4), untracked=dst_acc)
+
+    def q_prescale(self, from_acc):
+        """Q words (VGPRs 0..63, or the next-item AGPRs) -> two f32 (x * sl2) -> fp16 pair
+        -> the Q AGPRs."""
+        p = self.p
         for i in range(64):
+            if from_acc:
+                p.valu(f"v_accvgpr_read_b32 {vr(i)}, {ar(A_QN + i)}", A(A_QN + i), V(i))
             t0, t1 = V_CINIT, V_CINIT + 1
             p.valu(f"v_fma_mix_f32 {vr(t0)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t0))
             p.valu(f"v_fma_mix_f32 {vr(t1)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t1))
             p.valu(f"v_cvt_pk_f16_f32 {vr(i)}, {vr(t0)}, {vr(t1)}", V(t0, 2), V(i))
             p.valu(f"v_accvgpr_write_b32 {ar(A_Q + i)}, {vr(i)}", V(i), A(A_Q + i))
+
+    def prefetch_next_q(self, sfx):
+        """Loads of the next round's item's Q rows into the next-item AGPRs (none after the
+        last item)."""
+        p, s = self.p, self.s
+        K, I, Z, B, H, KVH, R, QB = (S_TMP + k for k in range(8))
+        s(f"s_add_u32 {sr(K)}, {sr(S_KA)}, 1", S(S_KA), S(K))
+        self.item_index(K, I, S_TMP + 12)
+        s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
+        p.branch(f"s_cbranch_scc1 .Lpq_{sfx}", [("scc", 0)], skip_xdl=ACC)
+        self.decode(I, Z, B, H, KVH, R)
+        s(f"s_sub_u32 {sr(QB)}, {sr(S_NQBLK)}, 1", S(S_NQBLK), S(QB))
+        s(f"s_sub_u32 {sr(QB)}, {sr(QB)}, {sr(Z)}", S(QB) + S(Z), S(QB))
+        s(f"s_cmp_eq_u32 {sr(S_CAUSAL)}, 0", S(S_CAUSAL), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(QB)}, {sr(Z)}, {sr(QB)}", S(Z) + S(QB) + [("scc", 0)], S(QB))
+        s(f"s_lshl_b32 {sr(QB)}, {sr(QB)}, 8", S(QB), S(QB))
+        s(f"s_lshl_b32 {sr(Z)}, {sr(S_WAVE)}, 6", S(S_WAVE), S(Z))
+        s(f"s_add_u32 {sr(QB)}, {sr(QB)}, {sr(Z)}", S(QB) + S(Z), S(QB))
+        self.q_loads(B, H, QB, True)
+        p.label(f".Lpq_{sfx}")
 
     def reset_acc(self):
         """O accumulators, row sums and overflow trackers to 0 (O by 8 MFMAs of zeros)."""
@@ -639,11 +671,12 @@ class Body:
             p.valu(f"v_mov_b32_e32 {vr(V_LSUM + qb)}, 0", [], V(V_LSUM + qb))
             p.valu(f"v_mov_b32_e32 {vr(V_LMAX + qb)}, 0", [], V(V_LMAX + qb))
 
-    def start_item(self, u, sfx, fixed_m):
+    def start_item(self, u, sfx, fixed_m, prefetch=True):
         """Tile 0 of the current item (stream parity u): S(0) into set u when the wave uses
         it, its mask, and m = its row max (first pass) or S(0) from the start values -m
         (fixed_m: the exact pass after an overflow); one barrier (the first body's requests
-        overwrite K buffer u); then the first body."""
+        overwrite K buffer u); the loads of the next item's Q (prefetch); then the first
+        body."""
         p, s = self.p, self.s
         p.comment(f"start {u}")
         s(f"s_cmp_eq_u32 {sr(S_ACTEND)}, 0", S(S_ACTEND), [("scc", 0)])
@@ -658,6 +691,8 @@ class Body:
         p.label(f".Lsn_{sfx}")
         p.waitcnt(lgkm=0)
         p.barrier()
+        if prefetch:
+            self.prefetch_next_q(sfx)
         self.code(S_TMP + 8, S_TMP + 9, S_TMP + 10)
         p.branch(f"s_branch .Ldisp{u}", skip_xdl=ACC)
 
@@ -823,7 +858,8 @@ def build(check_ldb: int = 12288) -> str:
     b.stream_start(0, "p")
     b.item_index(S_KA, S_TMP + 15, S_TMP + 12)
     b.decode_a(S_TMP + 15, "p")
-    b.load_q()
+    b.q_loads(S_BA, S_HA, S_Q0, False)
+    b.q_prescale(False)
     b.reset_acc()
     p.waitcnt(vm=0)
     p.barrier()
@@ -895,7 +931,7 @@ def _boundary(b: Body, u: int):
     p.branch("s_cbranch_scc1 .Lexit", [("scc", 0)], skip_xdl=ACC)
     b.decode_a(I, f"b{u}")
     s(f"s_mov_b32 {sr(S_PASS)}, 0", [], S(S_PASS))
-    b.load_q()
+    b.q_prescale(True)
     b.reset_acc()
     b.start_item(u, f"b{u}", False)
 
@@ -954,7 +990,7 @@ def _redo(b: Body, u: int):
     p.barrier()
     s(f"s_mov_b32 {sr(S_PASS)}, 1", [], S(S_PASS))
     s(f"s_mov_b32 {sr(S_IT)}, 0", [], S(S_IT))
-    b.start_item(u, f"r{u}", True)
+    b.start_item(u, f"r{u}", True, prefetch=False)
 
 
 def main(path: str) -> None:
