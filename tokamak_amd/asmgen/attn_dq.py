@@ -86,6 +86,7 @@ V_TK = V_HI4 + 1        # mask thresholds per qb (2)
 V_T = V_TK + 2          # temporaries (8)
 assert V_T + 8 <= 256
 V_PT = 100              # prologue lane scratch (score set 1, free until the first body)
+EPI_BASE = V_DS         # epilogue temporaries at an item boundary: clear of the prefetched rows
 
 # ---- AGPRs
 A_DQ, A_Q, A_O = 0, 128, 192
@@ -466,14 +467,18 @@ class Body:
         for i in range(8):
             p.mfma(MFMA, A_DQ + 16 * i, V_TB, V_TB, None, dst_acc=True)
 
-    def rows_load(self, sfx):
-        """Q, dO (and O) of the wave's 64 rows into VGPRs 0..63, 64..127 (128..191): lane
-        (l32, hi) loads row q0 + 32qb + l32, bytes hi*16 + 32ks .. +15; then -LSE*log2e, D."""
+    def rows_issue(self, b, h, q0, prefetch, sfx):
+        """Loads of Q, dO (and, computing D, O) of the wave's 64 rows of (batch b, head h)
+        from row q0 (SGPRs), and of their LSE: lane (l32, hi) loads row q0 + 32qb + l32, bytes
+        hi*16 + 32ks .. +15.  Q -> VGPRs 0..63; LSE -> V_T+5, +6.  Direct (item start): dO ->
+        VGPRs 64..127, O -> 128..191, tracked.  Prefetch (before the previous item's
+        epilogue, whose time covers their latency): dO -> its AGPRs, O -> VGPRs 64..127,
+        untracked (the caller waits with vmcnt(0))."""
         p, s = self.p, self.s
         RQ, RDO, RO_, RL = S_TMP + 20, S_TMP + 24, S_TMP + 28, S_TMP + 4
         T0, COL, NREC = S_TMP, S_TMP + 1, S_TMP + 2
-        s(f"s_mul_i32 {sr(T0)}, {sr(S_BA)}, {sr(S_SEQ)}", S(S_BA) + S(S_SEQ), S(T0))
-        s(f"s_lshl_b32 {sr(COL)}, {sr(S_HA)}, 8", S(S_HA), S(COL))
+        s(f"s_mul_i32 {sr(T0)}, {sr(b)}, {sr(S_SEQ)}", S(b) + S(S_SEQ), S(T0))
+        s(f"s_lshl_b32 {sr(COL)}, {sr(h)}, 8", S(h), S(COL))
         s(f"s_mul_i32 {sr(NREC)}, {sr(S_SEQ)}, {sr(S_LDB)}", S(S_SEQ) + S(S_LDB), S(NREC))
         self.rsrc(RQ, S_QKV, T0, S_LDB, COL, NREC)
         s(f"s_mul_i32 {sr(NREC)}, {sr(S_SEQ)}, {sr(S_LDO)}", S(S_SEQ) + S(S_LDO), S(NREC))
@@ -481,7 +486,7 @@ class Body:
         self.rsrc(RO_, S_O, T0, S_LDO, COL, NREC)
         QO, OO = V_T, V_T + 2
         for qb in range(2):
-            p.valu(f"v_add_u32_e32 {vr(V_T + 4)}, {sr(S_Q0)}, {vr(V_L32)}", S(S_Q0) + V(V_L32), V(V_T + 4))
+            p.valu(f"v_add_u32_e32 {vr(V_T + 4)}, {sr(q0)}, {vr(V_L32)}", S(q0) + V(V_L32), V(V_T + 4))
             if qb:
                 p.valu(f"v_add_u32_e32 {vr(V_T + 4)}, 32, {vr(V_T + 4)}", V(V_T + 4), V(V_T + 4))
             p.valu(f"v_mul_lo_u32 {vr(QO + qb)}, {vr(V_T + 4)}, {sr(S_LDB)}", V(V_T + 4) + S(S_LDB), V(QO + qb))
@@ -492,39 +497,58 @@ class Body:
             for ks in range(8):
                 r = (qb * 8 + ks) * 4
                 p.vmem_load(f"buffer_load_dwordx4 {vr(r, 4)}, {vr(QO + qb)}, {sr(RQ, 4)}, 0 offen offset:{ks * 32}",
-                            V(r, 4), V(QO + qb) + S(RQ, 4))
-                p.vmem_load(f"buffer_load_dwordx4 {vr(64 + r, 4)}, {vr(OO + qb)}, {sr(RDO, 4)}, 0 offen offset:{ks * 32}",
-                            V(64 + r, 4), V(OO + qb) + S(RDO, 4))
-        # LSE (row q, zero past S) -> -LSE*log2e start values; D computed or read
-        s(f"s_mul_i32 {sr(T0)}, {sr(S_BA)}, {sr(S_HQ)}", S(S_BA) + S(S_HQ), S(T0))
-        s(f"s_add_u32 {sr(T0)}, {sr(T0)}, {sr(S_HA)}", S(T0) + S(S_HA), S(T0))
+                            V(r, 4), V(QO + qb) + S(RQ, 4), untracked=prefetch)
+                dst, regs = (ar(A_O + r, 4), A(A_O + r, 4)) if prefetch else (vr(64 + r, 4), V(64 + r, 4))
+                p.vmem_load(f"buffer_load_dwordx4 {dst}, {vr(OO + qb)}, {sr(RDO, 4)}, 0 offen offset:{ks * 32}",
+                            regs, V(OO + qb) + S(RDO, 4), untracked=prefetch)
+        # LSE (row q, zero past S)
+        s(f"s_mul_i32 {sr(T0)}, {sr(b)}, {sr(S_HQ)}", S(b) + S(S_HQ), S(T0))
+        s(f"s_add_u32 {sr(T0)}, {sr(T0)}, {sr(h)}", S(T0) + S(h), S(T0))
         s(f"s_lshl_b32 {sr(NREC)}, {sr(S_SEQ)}, 2", S(S_SEQ), S(NREC))
         s(f"s_mov_b32 {sr(COL)}, 4", [], S(COL))
         s(f"s_mul_i32 {sr(S_TMP + 3)}, {sr(T0)}, {sr(S_SEQ)}", S(T0) + S(S_SEQ), S(S_TMP + 3))
         self.rsrc(RL, S_LSE, S_TMP + 3, COL, None, NREC)
         LO = V_T + 4
-        p.valu(f"v_add_u32_e32 {vr(LO)}, {sr(S_Q0)}, {vr(V_L32)}", S(S_Q0) + V(V_L32), V(LO))
+        p.valu(f"v_add_u32_e32 {vr(LO)}, {sr(q0)}, {vr(V_L32)}", S(q0) + V(V_L32), V(LO))
         p.valu(f"v_lshlrev_b32_e32 {vr(LO)}, 2, {vr(LO)}", V(LO), V(LO))
         for qb in range(2):
             p.vmem_load(f"buffer_load_dword {vr(V_T + 5 + qb)}, {vr(LO)}, {sr(RL, 4)}, 0 offen offset:{128 * qb}",
-                        V(V_T + 5 + qb), V(LO) + S(RL, 4))
+                        V(V_T + 5 + qb), V(LO) + S(RL, 4), untracked=prefetch)
         s(f"s_cmp_eq_u32 {sr(S_WD)}, 0", S(S_WD), [("scc", 0)])
-        p.branch(f"s_cbranch_scc1 .Lrd_{sfx}", [("scc", 0)], skip_xdl=ACC)
-        # D = <O, dO>: this lane holds d = ks*16 + hi*8 .. +7, lane ^ 32 the rest
+        p.branch(f"s_cbranch_scc1 .Lro_{sfx}", [("scc", 0)], skip_xdl=ACC)
+        ob = 64 if prefetch else 128
         for qb in range(2):
             for ks in range(8):
                 r = (qb * 8 + ks) * 4
-                p.vmem_load(f"buffer_load_dwordx4 {vr(128 + r, 4)}, {vr(OO + qb)}, {sr(RO_, 4)}, 0 offen offset:{ks * 32}",
-                            V(128 + r, 4), V(OO + qb) + S(RO_, 4))
+                p.vmem_load(f"buffer_load_dwordx4 {vr(ob + r, 4)}, {vr(OO + qb)}, {sr(RO_, 4)}, 0 offen offset:{ks * 32}",
+                            V(ob + r, 4), V(OO + qb) + S(RO_, 4), untracked=prefetch)
+        p.label(f".Lro_{sfx}")
+
+    def rows_d(self, prefetched, sfx):
+        """D of the wave's rows (the current item's S_BA, S_HA, S_Q0): computed as fp32 sums of
+        the exact fp16 products O*dO (plain VALU, no dot op) and written with the row quads,
+        or read from delta.  The row loads have arrived (tracked, or waited for)."""
+        p, s = self.p, self.s
+        T0 = S_TMP
+        s(f"s_mul_i32 {sr(T0)}, {sr(S_BA)}, {sr(S_HQ)}", S(S_BA) + S(S_HQ), S(T0))
+        s(f"s_add_u32 {sr(T0)}, {sr(T0)}, {sr(S_HA)}", S(T0) + S(S_HA), S(T0))
+        s(f"s_cmp_eq_u32 {sr(S_WD)}, 0", S(S_WD), [("scc", 0)])
+        p.branch(f"s_cbranch_scc1 .Lrd_{sfx}", [("scc", 0)], skip_xdl=ACC)
+        ob, dt = (64, V_T + 7) if prefetched else (128, None)
         for qb in range(2):
             acc = V_ND + qb
             p.valu(f"v_mov_b32_e32 {vr(acc)}, 0", [], V(acc))
-            for ks in range(8):   # fp32 sums of the exact fp16 products, plain VALU (no dot op)
+            for ks in range(8):   # this lane holds d = ks*16 + hi*8 .. +7, lane ^ 32 the rest
                 for w in range(4):
                     r = (qb * 8 + ks) * 4 + w
+                    if prefetched:
+                        p.valu(f"v_accvgpr_read_b32 {vr(dt)}, {ar(A_O + r)}", A(A_O + r), V(dt))
+                        dv = dt
+                    else:
+                        dv = 64 + r
                     for half in ("op_sel_hi:[1,1,0]", "op_sel:[1,1,0] op_sel_hi:[1,1,0]"):
-                        p.valu(f"v_fma_mix_f32 {vr(acc)}, {vr(128 + r)}, {vr(64 + r)}, {vr(acc)} {half}",
-                               V(128 + r) + V(64 + r) + V(acc), V(acc))
+                        p.valu(f"v_fma_mix_f32 {vr(acc)}, {vr(ob + r)}, {vr(dv)}, {vr(acc)} {half}",
+                               V(ob + r) + V(dv) + V(acc), V(acc))
             t = V_T + 7
             p.valu(f"v_mov_b32_e32 {vr(t)}, {vr(acc)}", V(acc), V(t))
             p.emit(f"v_permlane32_swap_b32_e32 {vr(t)}, {vr(acc)}", PERMLANE, V(t) + V(acc), V(t) + V(acc))
@@ -532,13 +556,40 @@ class Body:
         self.write_d(T0)
         p.branch(f"s_branch .Lrdd_{sfx}", skip_xdl=ACC)
         p.label(f".Lrd_{sfx}")
+        COL, NREC, RL = S_TMP + 1, S_TMP + 2, S_TMP + 4
+        s(f"s_lshl_b32 {sr(NREC)}, {sr(S_SEQ)}, 2", S(S_SEQ), S(NREC))
+        s(f"s_mov_b32 {sr(COL)}, 4", [], S(COL))
         s(f"s_mul_i32 {sr(S_TMP + 3)}, {sr(T0)}, {sr(S_SEQ)}", S(T0) + S(S_SEQ), S(S_TMP + 3))
         self.rsrc(RL, S_DELTA, S_TMP + 3, COL, None, NREC)
+        LO = V_T + 4
+        p.valu(f"v_add_u32_e32 {vr(LO)}, {sr(S_Q0)}, {vr(V_L32)}", S(S_Q0) + V(V_L32), V(LO))
+        p.valu(f"v_lshlrev_b32_e32 {vr(LO)}, 2, {vr(LO)}", V(LO), V(LO))
         for qb in range(2):
             p.vmem_load(f"buffer_load_dword {vr(V_ND + qb)}, {vr(LO)}, {sr(RL, 4)}, 0 offen offset:{128 * qb}",
                         V(V_ND + qb), V(LO) + S(RL, 4))
         p.waitcnt(vm=0)
         p.label(f".Lrdd_{sfx}")
+
+    def rows_load(self, sfx):
+        """The current item's rows at its start: loads, then D."""
+        self.rows_issue(S_BA, S_HA, S_Q0, False, sfx)
+        self.rows_d(False, sfx)
+
+    def rows_prefetch(self, i, sfx):
+        """Loads of item i's rows (decoded into temporaries; the current item's state is not
+        touched), issued before the current item's epilogue."""
+        s = self.s
+        Z, B, H, KVH, Q0 = S_TMP + 8, S_TMP + 9, S_TMP + 10, S_TMP + 11, S_TMP + 12
+        assert i not in (Z, B, H, KVH, Q0, S_TMP + 13)
+        self.decode(i, Z, B, H, KVH)
+        s(f"s_sub_u32 {sr(Q0)}, {sr(S_NQBLK)}, 1", S(S_NQBLK), S(Q0))
+        s(f"s_sub_u32 {sr(Q0)}, {sr(Q0)}, {sr(Z)}", S(Q0) + S(Z), S(Q0))
+        s(f"s_cmp_eq_u32 {sr(S_CAUSAL)}, 0", S(S_CAUSAL), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(Q0)}, {sr(Z)}, {sr(Q0)}", S(Z) + S(Q0) + [("scc", 0)], S(Q0))
+        s(f"s_lshl_b32 {sr(Q0)}, {sr(Q0)}, 8", S(Q0), S(Q0))
+        s(f"s_lshl_b32 {sr(Z)}, {sr(S_WAVE)}, 6", S(S_WAVE), S(Z))
+        s(f"s_add_u32 {sr(Q0)}, {sr(Q0)}, {sr(Z)}", S(Q0) + S(Z), S(Q0))
+        self.rows_issue(B, H, Q0, True, sfx)
 
     def write_d(self, bh):
         """delta[row] = D and the row quads (-LSE*log2e, -D) of the wave's rows (hi == 0 lanes;
@@ -576,11 +627,12 @@ class Body:
             p.vmem_store(f"buffer_store_dword {vr(V_T + 7)}, {vr(QD)}, {sr(RQD, 4)}, 0 offen offset:8",
                          V(V_T + 7) + V(QD) + S(RQD, 4))
 
-    def finish_rows(self):
-        """dO -> AGPRs, Q * scale*log2e -> AGPRs, start values -LSE*log2e, -D."""
+    def finish_rows(self, do_in_acc=False):
+        """dO -> AGPRs (unless loaded there), Q * scale*log2e -> AGPRs, start values
+        -LSE*log2e, -D."""
         p = self.p
         p.waitcnt(vm=0)
-        for i in range(64):
+        for i in range(0 if do_in_acc else 64):
             p.valu(f"v_accvgpr_write_b32 {ar(A_O + i)}, {vr(64 + i)}", V(64 + i), A(A_O + i))
         t0, t1 = 128, 129
         for i in range(64):
@@ -595,9 +647,10 @@ class Body:
                 p.valu(f"v_mov_b32_e32 {vr(c + r)}, {vr(c)}", V(c), V(c + r))
             p.valu(f"v_sub_f32_e32 {vr(V_ND + qb)}, 0, {vr(V_ND + qb)}", V(V_ND + qb), V(V_ND + qb))
 
-    def epilogue(self):
+    def epilogue(self, base=8):
         """dQ^T * scale of the current item: lane holds row q0 + 32qb + l32, d = db*32 + g4*8 +
-        hi*4 + 0..3; through the wave's LDS staging rows, whole 256-byte rows per store."""
+        hi*4 + 0..3; through the wave's LDS staging rows, whole 256-byte rows per store.  Its
+        VGPR temporaries are base .. base+51."""
         p, s = self.p, self.s
         p.comment("epilogue")
         RQ = S_TMP + 4
@@ -609,7 +662,8 @@ class Body:
         s(f"s_mul_i32 {sr(EPW)}, {sr(S_WAVE)}, {EPI_WAVE}", S(S_WAVE), S(EPW))
         s(f"s_add_u32 {sr(EPW)}, {sr(EPW)}, {LDS_EPI}", S(EPW), S(EPW))
         s(f"s_lshl_b32 {sr(ROW4)}, {sr(S_LDB)}, 2", S(S_LDB), S(ROW4))
-        BW, BR, TA, TB, RBUF, OOS = 24, 25, 26, 27, 28, 44
+        BW, BR, TA, TB, RBUF, OOS = base + 16, base + 17, base + 18, base + 19, base + 20, base + 36
+        assert OOS + 16 <= 256 and (base + 52 <= V_RB or base >= V_T + 8)
         p.valu(f"v_mul_u32_u24_e32 {vr(BW)}, {EPI_ROW}, {vr(V_L32)}", V(V_L32), V(BW))
         p.valu(f"v_add_u32_e32 {vr(BW)}, {sr(EPW)}, {vr(BW)}", S(EPW) + V(BW), V(BW))
         p.valu(f"v_lshl_add_u32 {vr(BW)}, {vr(V_HI4)}, 1, {vr(BW)}", V(V_HI4) + V(BW), V(BW))
@@ -625,7 +679,7 @@ class Body:
         p.valu(f"v_lshl_add_u32 {vr(OOS)}, {vr(TB)}, 4, {vr(TA)}", V(TB) + V(TA), V(OOS))
         for i in range(1, 16):
             p.valu(f"v_add_u32_e32 {vr(OOS + i)}, {sr(ROW4)}, {vr(OOS + i - 1)}", S(ROW4) + V(OOS + i - 1), V(OOS + i))
-        W = 8
+        W0 = W = base
         for qb in range(2):
             for db in range(4):
                 for g4 in range(4):
@@ -637,7 +691,7 @@ class Body:
                     p.valu(f"v_cvt_pk_f16_f32 {vr(W + 4)}, {vr(W)}, {vr(W + 1)}", V(W, 2), V(W + 4))
                     p.valu(f"v_cvt_pk_f16_f32 {vr(W + 5)}, {vr(W + 2)}, {vr(W + 3)}", V(W + 2, 2), V(W + 5))
                     p.ds_write(f"ds_write_b64 {vr(BW)}, {vr(W + 4, 2)} offset:{(db * 4 + g4) * 16}", V(BW) + V(W + 4, 2))
-                    W = 8 if W == 16 else 16
+                    W = W0 if W == W0 + 8 else W0 + 8
             for i in range(8):   # LDS operations of a wave complete in order: reads see the rows
                 R = RBUF + 4 * (i % 4)
                 p.ds_read(f"ds_read_b128 {vr(R, 4)}, {vr(BR)} offset:{i * 4 * EPI_ROW}", V(R, 4), V(BR))
@@ -770,22 +824,30 @@ def _dispatch(b: Body, u: int):
 
 
 def _boundary(b: Body, u: int):
-    """End of the current item before body residue u: store its dQ; take the next item (or
-    stop), load its rows and start it on tile it (buffer u, already delivered)."""
+    """End of the current item before body residue u: request the next item's rows (their
+    latency hides behind the epilogue), store the current dQ; take the next item (or stop),
+    its D, and start it on tile it (buffer u, already delivered)."""
     p, s = b.p, b.s
     I = S_TMP + 17
     p.label(f".Lbnd{u}")
     p.nop(16)
     p.waitcnt(lgkm=0)
-    b.epilogue()
+    K1 = S_TMP + 16
+    s(f"s_add_u32 {sr(K1)}, {sr(S_KA)}, 1", S(S_KA), S(K1))
+    b.item_index(K1, I)
+    s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
+    p.branch(f"s_cbranch_scc1 .Lnopf{u}", [("scc", 0)], skip_xdl=ACC)
+    b.rows_prefetch(I, f"b{u}")
+    p.label(f".Lnopf{u}")
+    b.epilogue(EPI_BASE)
     s(f"s_add_u32 {sr(S_KA)}, {sr(S_KA)}, 1", S(S_KA), S(S_KA))
-    b.item_index(S_KA, I)
     s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
     p.branch("s_cbranch_scc1 .Lexit", [("scc", 0)], skip_xdl=ACC)
     b.decode_a(I, f"b{u}")
-    b.rows_load(f"b{u}")
+    p.waitcnt(vm=0)
+    b.rows_d(True, f"b{u}")
     b.zero_acc()
-    b.finish_rows()
+    b.finish_rows(do_in_acc=True)
     b.start_item(u, f"b{u}")
 
 

@@ -457,6 +457,26 @@ class Body:
                 issued += 1
             self.pv_mfma(j)
 
+    def stage_softmax_pv(self, J, vbase):
+        """Softmax of set J and O += V P from the V buffer at vbase, interleaved: PV k-step ks
+        (MFMAs 8ks .. 8ks+7) needs only P[*][ks] (softmax steps 8ks .. 8ks+7), so the softmax
+        of k-step ks+1 runs between the MFMAs of k-step ks."""
+        for n in range(8):
+            self.sm_exp(J, n)
+            self.sm_pack(J, n)
+        issued = 0
+        for j in range(32):
+            while issued < 16 and issued * 2 - LV <= j:
+                self.v_read(issued, vbase)
+                issued += 1
+            self.pv_mfma(j)
+            n = 8 + j            # softmax step of the next k-step, one per MFMA
+            if n < 32:
+                self.sm_exp(J, n)
+                self.sm_pack(J, n)
+            if j in (25, 27):
+                self.sm_finish((j - 25) // 2)
+
     def stage_mask(self, J, tsg):
         """Scores of set J, tile t (SGPR tsg), set to -inf where key > q (causal) or
         key >= kv_len.  Per lane and 32-row block: thr = min(causal ? q - k0 - 4hi : big,
@@ -588,8 +608,7 @@ class Body:
             self.dma_tile(S_RK, LDS_K[u])
             self.dma_tile(S_RV, LDS_V[Jn])
             if variant != "idle":
-                self.stage_softmax(u)
-                self.stage_pv(LDS_V[u])
+                self.stage_softmax_pv(u, LDS_V[u])
             for c in h:
                 p.ins.extend(c)
         p.waitcnt(vm=0)
