@@ -72,7 +72,7 @@ TKM_ATTN_API int tkm_attn_fwd(const void *qkv, void *o, float *lse, const int32_
                               int dtype, void *stream);
 
 /* Bytes of device workspace tkm_attn_bwd needs: the per-row D = <O, dO> vector, and the same
- * rows' (-LSE*log2(e), -D) pairs, padded to 32 rows per (batch, head), for the dK/dV pass.
+ * rows' -LSE*log2(e) and -D values in tiles of 32 rows per (batch, head), for the dK/dV pass.
  * Replaces the per-node save buffer sizing of init_node_resources, src/tkm_gpu.cu:1000-1001. */
 TKM_ATTN_API size_t tkm_attn_bwd_workspace_bytes(int B, int S, int Hq);
 

@@ -94,7 +94,7 @@ def test_bwd_rejects():
 def test_workspace_bytes():
     L = attn.lib()
     # D per row (B*Hq*S floats, rounded up to 256 bytes), then 8 bytes per row of the
-    # (-LSE*log2e, -D) quads with S padded to a multiple of 32
+    # row values (-LSE*log2e, -D) with S padded to a multiple of 32
     assert L.tkm_attn_bwd_workspace_bytes(4, 2048, 16) == 4 * 2048 * 16 * 4 + 4 * 16 * 2048 * 8
     assert L.tkm_attn_bwd_workspace_bytes(1, 3, 1) == 256 + 32 * 8
     assert L.tkm_attn_bwd_workspace_bytes(2, 100, 3) == 2560 + 2 * 3 * 128 * 8

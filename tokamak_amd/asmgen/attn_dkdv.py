@@ -8,8 +8,8 @@ writes copies of dQ/dO at 588-596 instead):
 over every query row i of every q-head of key j's kv group, key j visible from row i iff
 j < kv_len[b] and (!causal || j <= i); dK and dV are written (not accumulated) into dqkv.
 Instead of LSE and D it reads the workspace's row values -LSE*log2(e) and -D, stored per
-(batch, head) as quads (rows m, m+1: -LSE*log2e of both, then -D of both) with the rows padded
-to a multiple of 32 and the padding zero, which the pass that computes D writes.
+(batch, head) in tiles of 32 rows (the 32 values -LSE*log2e, then the 32 values -D; rows
+padded to a multiple of 32 with zeros), which the pass that computes D writes.
 
 Work decomposition: grid (Hkv, B, n_kblk), one workgroup = 4 waves = one (batch, kv head,
 block of 128 keys); one wave per SIMD.  A wave owns 32 keys: K (prescaled by
@@ -17,14 +17,14 @@ scale*log2(e)) and V of those keys sit in AGPRs as the B operands of S = Q K^T a
 dP = dO V^T, and the accumulators dV^T, dK^T (C[m = head dim][n = key]) in AGPRs.  The
 workgroup walks the query tiles (32 rows) of every q-head of the group (causal: from its own
 key block on); each tile's Q and dO rows go HBM -> LDS by buffer DMA into one of four buffers
-(tile t in buffer t % 4, requested three tiles ahead); each wave also copies the tile's row
-quads into its own slot.  The DMA descriptors are fixed for the kernel (whole batch, so rows
+(tile t in buffer t % 4, requested three tiles ahead); each wave also copies the tile's 256
+bytes of row values into its own slot.  The DMA descriptors are fixed for the kernel (whole batch, so rows
 past S read as zero); a tile's position enters as an offset added to the lane offsets.
 Per tile:
     S  = Q K'^T  + (-LSE*log2e)   8 MFMAs, C[m = query][n = key]: lane = key
-    dP = dO V^T  + (-D)           8 MFMAs (the offsets are the accumulators' start values,
-                                  broadcast from one LDS read per lane with 64-bit DPP
-                                  row_newbcast, two rows per move)
+    dP = dO V^T  + (-D)           8 MFMAs (the offsets are the accumulators' start values:
+                                  four consecutive rows per register group, read by each
+                                  half-wave as one 16-byte broadcast LDS read)
     P = exp2(S), dS = P * dP      masked to 0 where the key is hidden
     dV^T += dO^T P, dK^T += Q^T dS 16 MFMAs, P and dS packed to fp16 in place as B operands,
                                   dO^T and Q^T read transposed (ds_read_b64_tr_b16)
@@ -47,7 +47,7 @@ ROWB = 256
 NBUF = 4
 TILE = 32 * ROWB                    # 8 KB: one 32-row tile of Q or dO
 BUFB = 2 * TILE                     # Q then dO
-LDS_LD = NBUF * BUFB                # row quads: per buffer 4 waves x 256 B
+LDS_LD = NBUF * BUFB                # row values: per buffer 4 waves x 256 B
 LDB = 1024
 LDS_EPI = LDS_LD + NBUF * LDB       # per wave: 32 key rows of 272 B staging dK, dV for the store
 EPI_ROW = 272                       # 256 B + 16 B pad: rows 16 B apart in the banks
@@ -70,7 +70,7 @@ S_KA, S_KD = 3, 4                      # round of the current item / of the DMA 
 S_QKV, S_DOUT, S_PAIRS, S_DQKV, S_KVLEN = 8, 10, 12, 14, 16
 S_SEQ, S_HQ, S_HKV, S_SL2, S_CAUSAL, S_LDB = 18, 19, 20, 21, 22, 23
 S_LDO, S_G, S_SCALE, S_NKBLK, S_SP, S_NWG, S_NI, S_BH = 24, 25, 26, 27, 28, 29, 30, 31
-S_TQ, S_TO, S_TL = 5, 6, 7             # offsets of the requested tile (Q, dO, row quads)
+S_TQ, S_TO, S_TL = 5, 6, 7             # offsets of the requested tile (Q, dO, row values)
 S_LDB32, S_LDO32 = 88, 89              # 32 rows of qkv / dO in bytes
 S_MAGBH, S_MAGHKV = 90, 91             # ceil(2^32 / (B*Hkv)), ceil(2^32 / Hkv) (0 for 1)
 S_BA, S_KVHA, S_ITERSD, S_QTBD = 92, 93, 94, 95   # current item's batch, kv head; DMA item's tiles
@@ -95,9 +95,8 @@ V_KOFF = V_TB + 4 * NTB
 V_VOFF = V_KOFF + 8
 V_DOFF = V_VOFF + 8     # Q rows (2), dO rows (2)
 V_LOFF = V_DOFF + 4     # lane*4 (row-quad DMA)
-V_LDR = V_LOFF + 1      # row-quad read address (see the lane check)
-V_LDV = V_LDR + 1       # (4) the quad read
-V_DA = V_LDV + 4        # (5) DMA addresses of the requested tile
+V_LDR = V_LOFF + 1      # row-value read address: the wave's slot + 16*hi (see the lane check)
+V_DA = V_LDR + 1        # (5) DMA addresses of the requested tile
 V_L32 = V_DA + 5
 V_HI4 = V_L32 + 1
 V_TK = V_HI4 + 1        # mask threshold of the current tile
@@ -253,20 +252,18 @@ class Body:
             self.p.ds_read(f"ds_read_b64_tr_b16 {vr(dst + 2 * tt, 2)}, {vr(V_VOFF + tt * 4 + db)} offset:{off}",
                            V(dst + 2 * tt, 2), V(V_VOFF + tt * 4 + db))
 
-    def pair_read(self, jb):
-        self.p.ds_read(f"ds_read_b128 {vr(V_LDV, 4)}, {vr(V_LDR)} offset:{jb * LDB}", V(V_LDV, 4), V(V_LDR))
-
-    def pair_bcast(self, k):
-        """Start values of register rows 2k, 2k+1 (query rows mask_c(2k) + 4hi and the next):
-        lane k of each 16-lane row holds that row's quad, broadcast to its row."""
-        for base, src in ((V_CS, V_LDV), (V_CD, V_LDV + 2)):
-            self.p.permlane(f"v_mov_b64_dpp {vr(base + 2 * k, 2)}, {vr(src, 2)} row_newbcast:{k} row_mask:0xf bank_mask:0xf",
-                            V(src, 2), V(base + 2 * k, 2))
+    def cinit_read(self, jb, k):
+        """Start values of accumulator registers 4g .. 4g+3 (g = k % 4) of S (k < 4: -LSE*log2e)
+        or dP (k >= 4: -D): query rows 8g + 4hi .. +3 of the tile in buffer jb, the same for
+        every lane of a half-wave (one 16-byte broadcast read per half)."""
+        g, which = k % 4, k // 4
+        base = (V_CS if which == 0 else V_CD) + 4 * g
+        self.p.ds_read(f"ds_read_b128 {vr(base, 4)}, {vr(V_LDR)} offset:{jb * LDB + 128 * which + 32 * g}",
+                       V(base, 4), V(V_LDR))
 
     def cinit(self, jb):
-        self.pair_read(jb)
         for k in range(8):
-            self.pair_bcast(k)
+            self.cinit_read(jb, k)
 
     # ---------------------------------------------------------------- MFMAs
     def sdp_mfma(self, i, J):
@@ -751,8 +748,8 @@ class Body:
                 while tissued < 16 and 16 + tissued - LV <= s_:
                     self.tr_read(tissued, jb0)
                     tissued += 1
-            if s_ == 16:
-                self.pair_read(jb2)
+            if 16 <= s_ < 24:
+                self.cinit_read(jb2, s_ - 16)
             p.ins.extend(h2[s_ - 16])
             if s_ in dma_at:
                 which, i = self.DMA_ORDER[dma_at[s_]]
@@ -765,9 +762,6 @@ class Body:
                         self.ew_exp(J0, n)
                     else:
                         self.ew_rest(J0, n, masked)
-            b0 = 24 if EW_SPLIT else 20
-            if b0 <= s_ < b0 + 8:
-                self.pair_bcast(s_ - b0)
             if s_ in dma_at:
                 which, i = self.DMA_ORDER[dma_at[s_]]
                 self.dma_ld(which, i)
@@ -828,7 +822,7 @@ def build(check_ldb: int = 12288, check_ldo: int = 4096) -> str:
     p.valu(f"v_mov_b32_e32 {vr(V_L32)}, {vr(L32)}", V(L32), V(V_L32))
     p.valu(f"v_lshlrev_b32_e32 {vr(V_HI4)}, 2, {vr(HI)}", V(HI), V(V_HI4))
     # ---------------------------------------------------------------- DMA descriptor sizes
-    # (the same for every item: a batch's Q / dO rows, a kv group's row quads)
+    # (the same for every item: a batch's Q / dO rows, a kv group's row values)
     sal(f"s_mul_i32 {sr(S_RQ + 2)}, {sr(S_SEQ)}, {sr(S_LDB)}", S(S_SEQ) + S(S_LDB), S(S_RQ + 2))
     sal(f"s_mul_i32 {sr(S_RO + 2)}, {sr(S_SEQ)}, {sr(S_LDO)}", S(S_SEQ) + S(S_LDO), S(S_RO + 2))
     sal(f"s_mul_i32 {sr(S_RL + 2)}, {sr(S_G)}, {sr(S_SP)}", S(S_G) + S(S_SP), S(S_RL + 2))
@@ -850,14 +844,8 @@ def build(check_ldb: int = 12288, check_ldo: int = 4096) -> str:
     b.dma_all(2)
     b.d_advance("p3")
     # ---------------------------------------------------------------- LDS read offsets
-    # row quads: lane (k = lane & 7, hi) reads quad (k//2)*4 + (k & 1) + 2hi of its wave's slot
-    L.and_(TA, L.k(6), LANE)
-    L.shl(TA, L.k(1), TA)
-    L.and_(TB, L.k(1), LANE)
-    L.add(TA, TA, TB)
-    L.shl(TB, L.k(1), HI)
-    L.add(TA, TA, TB)
-    L.shl(TA, L.k(4), TA)
+    # row values: the half-wave hi reads rows 8g + 4hi .. +3 of its wave's slot (+32g, +128)
+    L.shl(TA, L.k(4), HI)
     L.add(V_LDR, TA, L.s(S_LDSL, LDS_LD + wave_vals * 256))
     row_read_offsets(L, V_KOFF, (LANE, L32, HI), (TA, TB, TC))
     tr_read_offsets(L, V_VOFF, (LANE, L32, HI), (TA, TB, TC, V_PT + 9, V_PT + 10, V_PT + 11, V_PT + 12))
@@ -889,13 +877,14 @@ def _check_lanes(L: Lanes, ldb, ldo):
         assert np.array_equal(L.val[V_DOFF + i], (row * ldb + chunk) & 0xFFFFFFFF), f"Q dma {i}"
         assert np.array_equal(L.val[V_DOFF + 2 + i], (row * ldo + chunk) & 0xFFFFFFFF), f"dO dma {i}"
     assert np.array_equal(L.val[V_LOFF], lane * 4)
-    # the quad a lane reads is the source of row_newbcast:k (k = lane & 15 < 8) for register
-    # rows 2k, 2k+1 of its 16-lane row R = lane >> 4: query rows mask_c(2k) + 4*(R >> 1), +1,
-    # stored as quad (row // 2) of the wave's 256-byte slot
-    k, hi = lane & 7, lane >> 5
-    rows = np.array([mask_c(2 * x) for x in k]) + 4 * hi
-    assert np.all(rows % 2 == 0)
-    assert np.array_equal(L.val[V_LDR], LDS_LD + wave * 256 + (rows // 2) * 16), "quad read offsets"
+    # accumulator register r of a lane holds query row mask_c(r) + 4hi; its start value sits at
+    # byte 4*(row) of the tile's 128-byte -LSE*log2e run (-D: +128) in the wave's slot, so the
+    # read of registers 4g .. 4g+3 at V_LDR + 32g covers rows mask_c(4g) + 4hi .. +3
+    hi = lane >> 5
+    for g in range(4):
+        rows = np.array([mask_c(4 * g + j) for j in range(4)])
+        assert np.array_equal(rows, rows[0] + np.arange(4)) and rows[0] == 8 * g
+    assert np.array_equal(L.val[V_LDR], LDS_LD + wave * 256 + 16 * hi), "row-value read offsets"
 
 
 def _dispatch(b: Body, u: int):

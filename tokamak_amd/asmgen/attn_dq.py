@@ -5,9 +5,9 @@ dQ part of the reference's k_gqa_flash_attn_tc_bwd (src/tkm_gpu.cu:440-598):
     P_ij = exp(s_ij - LSE_i),  dS_ij = P_ij (<dO_i, v_j> - D_i),  dQ_i = scale sum_j dS_ij k_j
 over the keys j visible from query row i (j < kv_len[b] and, causal, j <= i); dQ is written
 (not accumulated) into dqkv.  With compute_d set it also computes D_i = <O_i, dO_i> in fp32
-and writes it to delta and, with -LSE_i*log2(e), to the workspace's row quads (rows m, m+1:
--LSE*log2e of both, then -D of both; rows past S zero) that the dK/dV kernel reads; otherwise
-it reads D from delta.
+and writes it to delta and, with -LSE_i*log2(e), to the workspace's row values (per 32-row
+tile: the 32 values -LSE*log2e, then the 32 values -D; rows past S zero) that the dK/dV
+kernel reads; otherwise it reads D from delta.
 
 Work decomposition: persistent, one workgroup (4 waves, one per SIMD) per compute unit walks
 items (block of 256 query rows, batch, q-head), heaviest first for causal, in snake order
@@ -526,7 +526,7 @@ class Body:
 
     def rows_d(self, prefetched, sfx):
         """D of the wave's rows (the current item's S_BA, S_HA, S_Q0): computed as fp32 sums of
-        the exact fp16 products O*dO (plain VALU, no dot op) and written with the row quads,
+        the exact fp16 products O*dO (plain VALU, no dot op) and written with the row values,
         or read from delta.  The row loads have arrived (tracked, or waited for)."""
         p, s = self.p, self.s
         T0 = S_TMP
@@ -592,8 +592,8 @@ class Body:
         self.rows_issue(B, H, Q0, True, sfx)
 
     def write_d(self, bh):
-        """delta[row] = D and the row quads (-LSE*log2e, -D) of the wave's rows (hi == 0 lanes;
-        rows past S: only quads, with zeros, up to SP)."""
+        """delta[row] = D and the row values (-LSE*log2e, -D) of the wave's rows (hi == 0 lanes;
+        rows past S: only row values, zeros, up to SP)."""
         p, s = self.p, self.s
         RD, RQD = S_TMP + 8, S_TMP + 16
         NREC, C4, T = S_TMP + 2, S_TMP + 1, S_TMP + 3
@@ -607,14 +607,15 @@ class Body:
         p.waitcnt(vm=0)   # the LSE loads
         DO_, QD, LG = V_T + 3, V_T + 4, V_T + 0
         for qb in range(2):
-            # row q = q0 + 32qb + l32: delta offset 4q, quad offset (q>>1)*16 + (q&1)*4; hi lanes off
+            # row q = q0 + 32qb + l32: delta offset 4q; row-tile offset (q>>5)*256 + (q&31)*4
+            # (its -D 128 bytes further); hi lanes off
             p.valu(f"v_add_u32_e32 {vr(QD)}, {sr(S_Q0)}, {vr(V_L32)}", S(S_Q0) + V(V_L32), V(QD))
             if qb:
                 p.valu(f"v_add_u32_e32 {vr(QD)}, 32, {vr(QD)}", V(QD), V(QD))
             p.valu(f"v_lshlrev_b32_e32 {vr(DO_)}, 2, {vr(QD)}", V(QD), V(DO_))
-            p.valu(f"v_and_b32_e32 {vr(V_T + 7)}, 1, {vr(QD)}", V(QD), V(V_T + 7))
-            p.valu(f"v_lshrrev_b32_e32 {vr(QD)}, 1, {vr(QD)}", V(QD), V(QD))
-            p.valu(f"v_lshlrev_b32_e32 {vr(QD)}, 4, {vr(QD)}", V(QD), V(QD))
+            p.valu(f"v_and_b32_e32 {vr(V_T + 7)}, 31, {vr(QD)}", V(QD), V(V_T + 7))
+            p.valu(f"v_lshrrev_b32_e32 {vr(QD)}, 5, {vr(QD)}", V(QD), V(QD))
+            p.valu(f"v_lshlrev_b32_e32 {vr(QD)}, 8, {vr(QD)}", V(QD), V(QD))
             p.valu(f"v_lshl_add_u32 {vr(QD)}, {vr(V_T + 7)}, 2, {vr(QD)}", V(V_T + 7) + V(QD), V(QD))
             p.valu(f"v_cmp_eq_u32_e32 vcc, 0, {vr(V_HI4)}", V(V_HI4), [("vcc", 0)])
             p.valu(f"v_mov_b32_e32 {vr(V_T + 7)}, 0x7ffffff0", [], V(V_T + 7))
@@ -624,7 +625,7 @@ class Body:
             p.valu(f"v_mul_f32_e32 {vr(LG)}, 0xbfb8aa3b, {vr(V_T + 5 + qb)}", V(V_T + 5 + qb), V(LG))
             p.valu(f"v_sub_f32_e32 {vr(V_T + 7)}, 0, {vr(V_ND + qb)}", V(V_ND + qb), V(V_T + 7))
             p.vmem_store(f"buffer_store_dword {vr(LG)}, {vr(QD)}, {sr(RQD, 4)}, 0 offen", V(LG) + V(QD) + S(RQD, 4))
-            p.vmem_store(f"buffer_store_dword {vr(V_T + 7)}, {vr(QD)}, {sr(RQD, 4)}, 0 offen offset:8",
+            p.vmem_store(f"buffer_store_dword {vr(V_T + 7)}, {vr(QD)}, {sr(RQD, 4)}, 0 offen offset:128",
                          V(V_T + 7) + V(QD) + S(RQD, 4))
 
     def finish_rows(self, do_in_acc=False):

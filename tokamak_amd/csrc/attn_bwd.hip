@@ -22,6 +22,13 @@ namespace tkm {
 
 // ---------------------------------------------------------------- D = rowsum(O * dO)
 // One thread per 8 head-dim elements; D/8 consecutive lanes reduce one (row, head).
+// Row values of the workspace: per (batch, head) the rows are padded to SP (a multiple of 32)
+// and stored in tiles of 32 rows, 256 bytes each: -LSE*log2(e) of the tile's rows, then -D of
+// the same rows.  Index of row i's -LSE*log2(e) (its -D is 32 floats further).
+__device__ __forceinline__ size_t row_tile_index(size_t bh, int SP, int i) {
+    return bh * SP * 2 + (size_t)(i >> 5) * 64 + (i & 31);
+}
+
 template <int D, int DT>
 __global__ __launch_bounds__(256) void fa_bwd_delta_kernel(const uint16_t* __restrict__ o,
                                                            const uint16_t* __restrict__ dout,
@@ -38,9 +45,9 @@ __global__ __launch_bounds__(256) void fa_bwd_delta_kernel(const uint16_t* __res
         if (p < npad) {
             const size_t bh = p / (SP - S);
             const int i = S + (int)(p % (SP - S));
-            float* qd = quads + bh * SP * 2 + (i >> 1) * 4 + (i & 1);
+            float* qd = quads + row_tile_index(bh, SP, i);
             qd[0] = 0.f;
-            qd[2] = 0.f;
+            qd[32] = 0.f;
         }
         return;
     }
@@ -62,9 +69,9 @@ __global__ __launch_bounds__(256) void fa_bwd_delta_kernel(const uint16_t* __res
         const int i = (int)(row % S), b = (int)(row / S);
         const size_t li = ((size_t)b * Hq + h) * S + i;
         delta[li] = acc;
-        float* qd = quads + ((size_t)b * Hq + h) * SP * 2 + (i >> 1) * 4 + (i & 1);
+        float* qd = quads + row_tile_index((size_t)b * Hq + h, SP, i);
         qd[0] = -lse[li] * 1.4426950408889634f;
-        qd[2] = -acc;
+        qd[32] = -acc;
     }
 }
 
@@ -355,9 +362,9 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
         if (q < S && hi == 0) delta[li] = Dl;
         const int SP = (S + 31) & ~31;
         if (q < SP && hi == 0) {  // rows S..SP-1: zeros (nl2 = Dl = 0 there)
-            float* qd = quads + ((size_t)b * Hq + h) * SP * 2 + (q >> 1) * 4 + (q & 1);
+            float* qd = quads + row_tile_index((size_t)b * Hq + h, SP, q);
             qd[0] = nl2;
-            qd[2] = -Dl;
+            qd[32] = -Dl;
         }
     }
 
