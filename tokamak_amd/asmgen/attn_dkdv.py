@@ -666,7 +666,7 @@ class Body:
             for i in range(8):   # LDS operations of a wave complete in order: reads see the rows
                 R = 20 + 4 * (i % 4)
                 p.ds_read(f"ds_read_b128 {vr(R, 4)}, {vr(BR)} offset:{i * 4 * EPI_ROW}", V(R, 4), V(BR))
-                p.vmem_store(f"buffer_store_dwordx4 {vr(R, 4)}, {vr(OO + i)}, {sr(rs, 4)}, 0 offen",
+                p.vmem_store(f"buffer_store_dwordx4 {vr(R, 4)}, {vr(OO + i)}, {sr(rs, 4)}, 0 offen nt",
                              V(R, 4) + V(OO + i) + S(rs, 4))
 
     def start_item(self, u, sfx):

@@ -621,11 +621,11 @@ class Body:
             p.valu(f"v_mov_b32_e32 {vr(V_T + 7)}, 0x7ffffff0", [], V(V_T + 7))
             p.valu(f"v_cndmask_b32_e32 {vr(DO_)}, {vr(V_T + 7)}, {vr(DO_)}, vcc", V(V_T + 7) + V(DO_) + [("vcc", 0)], V(DO_))
             p.valu(f"v_cndmask_b32_e32 {vr(QD)}, {vr(V_T + 7)}, {vr(QD)}, vcc", V(V_T + 7) + V(QD) + [("vcc", 0)], V(QD))
-            p.vmem_store(f"buffer_store_dword {vr(V_ND + qb)}, {vr(DO_)}, {sr(RD, 4)}, 0 offen", V(V_ND + qb) + V(DO_) + S(RD, 4))
+            p.vmem_store(f"buffer_store_dword {vr(V_ND + qb)}, {vr(DO_)}, {sr(RD, 4)}, 0 offen nt", V(V_ND + qb) + V(DO_) + S(RD, 4))
             p.valu(f"v_mul_f32_e32 {vr(LG)}, 0xbfb8aa3b, {vr(V_T + 5 + qb)}", V(V_T + 5 + qb), V(LG))
             p.valu(f"v_sub_f32_e32 {vr(V_T + 7)}, 0, {vr(V_ND + qb)}", V(V_ND + qb), V(V_T + 7))
-            p.vmem_store(f"buffer_store_dword {vr(LG)}, {vr(QD)}, {sr(RQD, 4)}, 0 offen", V(LG) + V(QD) + S(RQD, 4))
-            p.vmem_store(f"buffer_store_dword {vr(V_T + 7)}, {vr(QD)}, {sr(RQD, 4)}, 0 offen offset:128",
+            p.vmem_store(f"buffer_store_dword {vr(LG)}, {vr(QD)}, {sr(RQD, 4)}, 0 offen nt", V(LG) + V(QD) + S(RQD, 4))
+            p.vmem_store(f"buffer_store_dword {vr(V_T + 7)}, {vr(QD)}, {sr(RQD, 4)}, 0 offen offset:128 nt",
                          V(V_T + 7) + V(QD) + S(RQD, 4))
 
     def finish_rows(self, do_in_acc=False):
@@ -696,7 +696,7 @@ class Body:
             for i in range(8):   # LDS operations of a wave complete in order: reads see the rows
                 R = RBUF + 4 * (i % 4)
                 p.ds_read(f"ds_read_b128 {vr(R, 4)}, {vr(BR)} offset:{i * 4 * EPI_ROW}", V(R, 4), V(BR))
-                p.vmem_store(f"buffer_store_dwordx4 {vr(R, 4)}, {vr(OOS + qb * 8 + i)}, {sr(RQ, 4)}, 0 offen",
+                p.vmem_store(f"buffer_store_dwordx4 {vr(R, 4)}, {vr(OOS + qb * 8 + i)}, {sr(RQ, 4)}, 0 offen nt",
                              V(R, 4) + V(OOS + qb * 8 + i) + S(RQ, 4))
 
     def start_item(self, u, sfx):

@@ -787,7 +787,7 @@ class Body:
             p.valu(f"v_sub_f32_e32 {vr(LG)}, {vr(LG)}, {vr(V_CINIT + qb * 16)}", V(LG) + V(V_CINIT + qb * 16), V(LG))
             p.valu(f"v_mul_f32_e32 {vr(LG)}, 0x3f317218, {vr(LG)}", V(LG), V(LG))
             p.valu(f"v_cndmask_b32_e32 {vr(LG)}, {vr(V_NINF)}, {vr(LG)}, vcc", V(V_NINF) + V(LG) + [("vcc", 0)], V(LG))
-            p.vmem_store(f"buffer_store_dword {vr(LG)}, {vr(LO)}, {sr(S_RL, 4)}, 0 offen", V(LG) + V(LO) + S(S_RL, 4))
+            p.vmem_store(f"buffer_store_dword {vr(LG)}, {vr(LO)}, {sr(S_RL, 4)}, 0 offen nt", V(LG) + V(LO) + S(S_RL, 4))
             for db in range(4):
                 for g4 in range(4):
                     o = A_O + (db * 2 + qb) * 16 + g4 * 4
@@ -802,7 +802,7 @@ class Body:
             for i in range(8):   # LDS operations of a wave complete in order: reads see the rows
                 R = RBUF + 4 * (i % 4)
                 p.ds_read(f"ds_read_b128 {vr(R, 4)}, {vr(BR)} offset:{i * 4 * EPI_ROW}", V(R, 4), V(BR))
-                p.vmem_store(f"buffer_store_dwordx4 {vr(R, 4)}, {vr(OOS + qb * 8 + i)}, {sr(S_RQ, 4)}, 0 offen",
+                p.vmem_store(f"buffer_store_dwordx4 {vr(R, 4)}, {vr(OOS + qb * 8 + i)}, {sr(S_RQ, 4)}, 0 offen nt",
                              V(R, 4) + V(OOS + qb * 8 + i) + S(S_RQ, 4))
 
     def overflow_vote(self, sfx):
