@@ -226,6 +226,7 @@ def run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d):
 
 
 BWD_CASES = [(1, 512, 2, 1, True, None, 3), (2, 700, 4, 2, True, None, 5), (2, 700, 4, 2, False, None, 4),
+             (2, 1024, 8, 8, True, None, 16),
              (2, 1000, 2, 2, False, [1000, 333], 3), (3, 600, 2, 1, True, [0, 65, 600], 2),
              (1, 64, 1, 1, True, None, 1), (1, 1, 1, 1, False, None, 1), (1, 300, 3, 1, True, [129], 256)]
 
@@ -247,6 +248,17 @@ def test_dq_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d):
     sim = run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d)
     stored = {m for _, _, m, _, _ in sim.stores}
     assert stored <= ({"dqkv", "delta", "quads", None} if compute_d else {"dqkv", None})
+    # D and the row values of every item go to its (batch, head)'s own rows: one descriptor
+    # per (b, h) covering exactly S floats of delta / SP*2 floats of row values
+    sp = (S + 31) // 32 * 32
+    for _, _, m, base, nrec in sim.stores:
+        if m == "delta":
+            assert nrec == 4 * S and (base - DELTA) % (4 * S) == 0, (hex(base), nrec)
+        elif m == "quads":
+            assert nrec == 8 * sp and (base - QUADS) % (8 * sp) == 0, (hex(base), nrec)
+    if compute_d:
+        heads = {(base - DELTA) // (4 * S) for _, _, m, base, _ in sim.stores if m == "delta"}
+        assert heads == set(range(B * Hq))
     ldb = (Hq + 2 * Hkv) * 256
     heads = {(base - DQKV) % ldb // 256 for _, _, m, base, _ in sim.stores if m == "dqkv"}
     assert heads == set(range(Hq))

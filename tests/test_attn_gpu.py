@@ -89,6 +89,46 @@ def test_config3_bf16(gpu):
     _assert_ok(run_gpu_case(gpu, 4, 2048, 16, 16, 128, dtype="bf16", causal=True, f64=False))
 
 
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+@pytest.mark.parametrize("B,S", [(4, 2048), (8, 1000)], ids=["B4S2048", "B8S1000"])
+def test_workspace_row_values(gpu, causal, B, S):
+    """After the dQ stage that computes D (config 3: two items per workgroup, so item
+    boundaries are exercised; S=1000 adds padding rows), the workspace holds D = <O, dO> per row
+    and, per (batch, head)
+    in tiles of 32 rows, -LSE*log2(e) then -D, padding rows zero.  D is checked against fp64
+    sums of the same fp16 O and dO (fp32 accumulation order differs: rtol 1e-5)."""
+    import torch
+    from tokamak_amd import attn
+    H, D = 16, 128
+    log(f"[case] workspace row values B{B} S{S} H{H} D{D} causal={int(causal)}")
+    g = torch.Generator(device=gpu)
+    g.manual_seed(3)
+    qkv = torch.randn(B, S, 3 * H * D, device=gpu, generator=g).half()
+    dout = torch.randn(B, S, H * D, device=gpu, generator=g).half()
+    o, lse = attn.gqa_fwd(qkv, B, S, H, H, D, causal=causal)
+    nbytes = attn.bwd_workspace_bytes(B, S, H)
+    ws = torch.full((nbytes,), 0x7F, dtype=torch.uint8, device=gpu)
+    dqkv = torch.empty_like(qkv)
+    attn.gqa_bwd(qkv, o, dout, lse, B, S, H, H, D, causal, None, dqkv=dqkv, workspace=ws,
+                 stage=attn.BWD_DQ_DELTA)
+    torch.cuda.synchronize()
+    wsf = ws.view(torch.float32).cpu().numpy()
+    o64 = o.float().cpu().numpy().astype(np.float64).reshape(B, S, H, D)
+    do64 = dout.float().cpu().numpy().astype(np.float64).reshape(B, S, H, D)
+    d_ref = np.einsum("bshd,bshd->bhs", o64, do64)                 # [B][H][S]
+    d_gpu = wsf[:B * H * S].reshape(B, H, S)
+    assert np.allclose(d_gpu, d_ref, rtol=1e-5, atol=1e-5), float(np.abs(d_gpu - d_ref).max())
+    sp = (S + 31) // 32 * 32
+    off = ((B * H * S * 4 + 255) // 256 * 256) // 4
+    rows = wsf[off:off + B * H * sp * 2].reshape(B, H, sp // 32, 2, 32)
+    nl2 = -lse.cpu().numpy().astype(np.float64) * 1.4426950408889634
+    got_l = rows[:, :, :, 0, :].reshape(B, H, sp)
+    got_d = rows[:, :, :, 1, :].reshape(B, H, sp)
+    assert np.allclose(got_l[:, :, :S], nl2, rtol=1e-6, atol=1e-6)
+    assert np.allclose(got_d[:, :, :S], -d_ref, rtol=1e-5, atol=1e-5)
+    assert not got_l[:, :, S:].any() and not got_d[:, :, S:].any()
+
+
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_stage_schedules(gpu, D, dtype):

@@ -598,7 +598,10 @@ class Body:
         RD, RQD = S_TMP + 8, S_TMP + 16
         NREC, C4, T = S_TMP + 2, S_TMP + 1, S_TMP + 3
         E8, NQ = S_TMP + 12, S_TMP + 13
+        assert bh not in (NREC, C4, T)
         s(f"s_mul_i32 {sr(T)}, {sr(bh)}, {sr(S_SEQ)}", S(bh) + S(S_SEQ), S(T))
+        s(f"s_mov_b32 {sr(C4)}, 4", [], S(C4))
+        s(f"s_lshl_b32 {sr(NREC)}, {sr(S_SEQ)}, 2", S(S_SEQ), S(NREC))
         self.rsrc(RD, S_DELTA, T, C4, None, NREC)
         s(f"s_mul_i32 {sr(T)}, {sr(bh)}, {sr(S_SP)}", S(bh) + S(S_SP), S(T))
         s(f"s_mov_b32 {sr(E8)}, 8", [], S(E8))
