@@ -76,6 +76,7 @@ class Wave:
         self.pc = 0
         self.wg, self.wave = wg, wave
         self.done = False
+        self.loads = []         # (destination operand, descriptor base) of plain buffer loads
 
     def get(self, o, w64=False):
         kind, i, n = o
@@ -276,6 +277,7 @@ class Sim:
         if op.startswith("buffer_load"):
             base, nrec, _ = self._desc(w, a[2])
             self._inside(base, nrec, text)
+            w.loads.append((a[0], base))
             return
         if op.startswith("buffer_store"):
             base, nrec, _ = self._desc(w, a[2])

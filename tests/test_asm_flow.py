@@ -99,12 +99,27 @@ def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, overflow=()):
         return []
 
     stored = {}
+    next_q = {}
+    checked = [0]
 
     def on_event(w, words):
         if words[0] == "epilogue":
             b, h, _, q0, _ = item_of(w)
             key = (b, h, q0)
             stored[key] = stored.get(key, 0) + 1
+        elif words[0] == "next" and words[1] == "q":
+            # the next item's Q, loaded into the next-item AGPRs during this item
+            next_q[(w.wg, w.wave)] = [(o, base) for o, base in w.loads if o[0] == "a"]
+            w.loads.clear()
+        elif words[0] == "start" and (w.wg, w.wave) in next_q:
+            b, h, _, _, _ = item_of(w)
+            loads = next_q.pop((w.wg, w.wave))
+            regs = sorted(o[1] for o, _ in loads)
+            if regs != list(range(attn_fwd.A_QN, attn_fwd.A_QN + 64, 4)):
+                raise Fail(f"next-item Q loads into {regs}")
+            if {base for _, base in loads} != {QKV + b * S * ldb + h * 256}:
+                raise Fail(f"next-item Q loads of another head: {sorted({base for _, base in loads})}")
+            checked[0] += 1
 
     sim = Sim(fwd_lines(), args, mem, kv, n_wg, expect, on_event, overflow=overflow)
     sim.run()
@@ -113,6 +128,8 @@ def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, overflow=()):
         (len(stored), len(want), [k for k, c in stored.items() if c != 1][:4])
     # O and LSE stores of each wave target its item's rows
     assert {m for _, _, m, _, _ in sim.stores} <= {"out", "lse", None}
+    # every item after a workgroup's first found its Q loaded during the previous item
+    assert checked[0] == 4 * (n_items - n_wg) and not next_q, (checked[0], n_items, n_wg)
     return sim
 
 

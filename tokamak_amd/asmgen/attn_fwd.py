@@ -948,6 +948,7 @@ def _boundary(b: Body, u: int):
     b.item_index(S_KA, I, S_TMP + 12)
     s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
     p.branch("s_cbranch_scc1 .Lexit", [("scc", 0)], skip_xdl=ACC)
+    p.comment("next q")
     b.decode_a(I, f"b{u}")
     s(f"s_mov_b32 {sr(S_PASS)}, 0", [], S(S_PASS))
     b.q_prescale(True)
