@@ -21,7 +21,11 @@
 namespace tkm {
 
 // ---------------------------------------------------------------- D = rowsum(O * dO)
-// One thread per 8 head-dim elements; D/8 consecutive lanes reduce one (row, head).
+// One workgroup per (batch, head, tile of 32 rows).  D/8 lanes per row each load 16 bytes of
+// O and dO and reduce by shuffles; the tile's 32 sums meet in LDS and leave as one 128-byte
+// run of delta and one 256-byte row-value tile (zeros for the padding rows S..SP-1), so
+// every write is a whole contiguous run.
+
 // Row values of the workspace: per (batch, head) the rows are padded to SP (a multiple of 32)
 // and stored in tiles of 32 rows, 256 bytes each: -LSE*log2(e) of the tile's rows, then -D of
 // the same rows.  Index of row i's -LSE*log2(e) (its -D is 32 floats further).
@@ -36,42 +40,42 @@ __global__ __launch_bounds__(256) void fa_bwd_delta_kernel(const uint16_t* __res
                                                            float* __restrict__ delta,
                                                            float* __restrict__ quads, int B,
                                                            int S, int Hq) {
-    constexpr int DC = D / 8;
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const size_t total = (size_t)B * S * Hq * DC;
-    const int SP = (S + 31) & ~31;
-    if (idx >= total) {  // threads past the rows zero the padding rows S..SP-1 of every head
-        const size_t p = idx - total, npad = (size_t)B * Hq * (SP - S);
-        if (p < npad) {
-            const size_t bh = p / (SP - S);
-            const int i = S + (int)(p % (SP - S));
-            float* qd = quads + row_tile_index(bh, SP, i);
-            qd[0] = 0.f;
-            qd[32] = 0.f;
-        }
-        return;
-    }
-    float acc = 0.f;
-    {
-        const u32x4 x = ld_global16(o + idx * 8), y = ld_global16(dout + idx * 8);
+    constexpr int DC = D / 8;          // lanes per row
+    constexpr int RPP = 256 / DC;      // rows per pass
+    static_assert(32 % RPP == 0 && DC <= 64, "delta tiling");
+    __shared__ float sums[32];
+    const int SP = (S + 31) & ~31, ntile = SP / 32;
+    const int tile = (int)(blockIdx.x % ntile);
+    const size_t bh = blockIdx.x / ntile;
+    const int b = (int)(bh / Hq), h = (int)(bh % Hq);
+    const int g = threadIdx.x / DC, c = threadIdx.x % DC;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            acc += to_f32<DT>((uint16_t)(x[w] & 0xffffu)) * to_f32<DT>((uint16_t)(y[w] & 0xffffu));
-            acc += to_f32<DT>((uint16_t)(x[w] >> 16)) * to_f32<DT>((uint16_t)(y[w] >> 16));
-        }
-    }
+    for (int p = 0; p < 32 / RPP; ++p) {
+        const int r = p * RPP + g, i = tile * 32 + r;
+        float acc = 0.f;
+        if (i < S) {
+            const size_t off = (((size_t)b * S + i) * Hq + h) * D + c * 8;
+            const u32x4 x = ld_global16(o + off), y = ld_global16(dout + off);
 #pragma unroll
-    for (int off = DC / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if ((idx % DC) == 0) {
-        const size_t rh = idx / DC;  // (b*S + i)*Hq + h
-        const int h = (int)(rh % Hq);
-        const size_t row = rh / Hq;
-        const int i = (int)(row % S), b = (int)(row / S);
-        const size_t li = ((size_t)b * Hq + h) * S + i;
-        delta[li] = acc;
-        float* qd = quads + row_tile_index((size_t)b * Hq + h, SP, i);
-        qd[0] = -lse[li] * 1.4426950408889634f;
-        qd[32] = -acc;
+            for (int w = 0; w < 4; ++w) {
+                acc += to_f32<DT>((uint16_t)(x[w] & 0xffffu)) * to_f32<DT>((uint16_t)(y[w] & 0xffffu));
+                acc += to_f32<DT>((uint16_t)(x[w] >> 16)) * to_f32<DT>((uint16_t)(y[w] >> 16));
+            }
+        }
+#pragma unroll
+        for (int off = DC / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+        if (c == 0) sums[r] = acc;
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < 32) {
+        const int i = tile * 32 + t;
+        if (i < S) delta[bh * S + i] = sums[t];
+    } else if (t < 96) {
+        const int k = t - 32, r = k & 31, i = tile * 32 + r;   // k < 32: -LSE*log2e, else -D
+        float v = 0.f;
+        if (i < S) v = k < 32 ? -lse[bh * S + i] * 1.4426950408889634f : -sums[r];
+        quads[row_tile_index(bh, SP, i) + (k & 32)] = v;
     }
 }
 
@@ -494,9 +498,7 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
 // ---------------------------------------------------------------- launchers
 template <int D, int DT>
 static int launch_delta_t(const BwdArgs& a) {
-    const size_t total = (size_t)a.B * a.S * a.Hq * (D / 8) +
-                         (size_t)a.B * a.Hq * (((a.S + 31) & ~31) - a.S);  // + padding rows
-    dim3 grid((unsigned)((total + 255) / 256)), block(256);
+    dim3 grid((unsigned)((size_t)a.B * a.Hq * ((a.S + 31) / 32))), block(256);
     hipLaunchKernelGGL((fa_bwd_delta_kernel<D, DT>), grid, block, 0, (hipStream_t)a.stream,
                        (const uint16_t*)a.o, (const uint16_t*)a.dout, a.lse, a.delta, a.ld,
                        a.B, a.S, a.Hq);
