@@ -200,11 +200,29 @@ def run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg):
                        n_items, bh, reciprocal(bh, n_items), reciprocal(Hkv, bh))
     assert len(args) == attn_dkdv.KERNARG_BYTES
     stored = {}
+    next_kv = {}
+    checked = [0]
+    spare = range(attn_dkdv.A_NK, attn_dkdv.A_NV + 32)
 
     def on_event(w, words):
         if words[0] == "epilogue":
             key = (w.s[attn_dkdv.S_BA], w.s[attn_dkdv.S_KVHA], w.s[attn_dkdv.S_KW0])
             stored[key] = stored.get(key, 0) + 1
+        elif words[0] == "next" and words[1] == "kv":
+            # the next item's K and V, loaded into the spare AGPRs before this boundary
+            next_kv[(w.wg, w.wave)] = [(o, base) for o, base in w.loads if o[0] == "a" and o[1] in spare]
+            w.loads.clear()
+        elif words[0] == "item":
+            b, kvh, kw0 = w.s[attn_dkdv.S_BA], w.s[attn_dkdv.S_KVHA], w.s[attn_dkdv.S_KW0]
+            loads = next_kv.pop((w.wg, w.wave))
+            if sorted(o[1] for o, _ in loads) != list(range(attn_dkdv.A_NK, attn_dkdv.A_NV + 32, 4)):
+                raise Fail(f"next-item K/V loads into {sorted(o[1] for o, _ in loads)}")
+            k_base = QKV + (b * S + kw0) * ldb + (Hq + kvh) * 256
+            for o, base in loads:
+                want = k_base + (Hkv * 256 if o[1] >= attn_dkdv.A_NV else 0)
+                if base != want:
+                    raise Fail(f"next-item {'V' if o[1] >= attn_dkdv.A_NV else 'K'} load from {base:#x}, expected {want:#x}")
+            checked[0] += 1
 
     sim = Sim(_gen_lines(attn_dkdv), args, _bwd_mem(B, S, Hq, Hkv, kv), kv, n_wg, None, on_event,
               wave_vgpr=attn_dkdv.V_PT)
@@ -212,6 +230,8 @@ def run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg):
     want = {(b, h, 128 * z + 32 * w) for b in range(B) for h in range(Hkv) for z in range(n_kblk) for w in range(4)}
     assert set(stored) == want and all(c == 1 for c in stored.values()), \
         (len(stored), len(want), [k for k, c in stored.items() if c != 1][:4])
+    # every item after a workgroup's first found its K, V loaded during the previous item
+    assert checked[0] == 4 * (n_items - n_wg) and not next_kv, (checked[0], n_items, n_wg)
     return sim
 
 

@@ -935,7 +935,9 @@ def _boundary(b: Body, u: int):
     s(f"s_add_u32 {sr(S_KA)}, {sr(S_KA)}, 1", S(S_KA), S(S_KA))
     s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
     p.branch("s_cbranch_scc1 .Lexit", [("scc", 0)], skip_xdl=ACC)
+    p.comment("next kv")
     b.decode_a(I, f"b{u}")
+    p.comment("item")
     b.zero_acc()
     b.kv_take()
     b.start_item(u, f"b{u}")
