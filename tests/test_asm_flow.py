@@ -247,11 +247,28 @@ def run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d):
                        reciprocal(Hq, bhq), reciprocal(G, Hq), int(compute_d))
     assert len(args) == attn_dq.KERNARG_BYTES
     stored = {}
+    checked = [0]
 
     def on_event(w, words):
         if words[0] == "epilogue":
             key = (w.s[attn_dq.S_BA], w.s[attn_dq.S_HA], w.s[attn_dq.S_Q0])
             stored[key] = stored.get(key, 0) + 1
+        elif words[0] == "next" and words[1] == "rows":
+            w.loads.clear()
+        elif words[0] == "item":
+            # the rows requested before the epilogue are the new item's: Q -> v0..63,
+            # dO -> its AGPRs, O -> v64..127 (computing D), LSE -> two VGPRs
+            b, h = w.s[attn_dq.S_BA], w.s[attn_dq.S_HA]
+            row, col = b * S, h * 256
+            want = sorted([(("v", 4 * k, 4), QKV + row * ldb + col) for k in range(16)] +
+                          [(("a", attn_dq.A_O + 4 * k, 4), DOUT + row * ldo + col) for k in range(16)] +
+                          [(("v", attn_dq.V_T + 5 + k, 1), LSE + (b * Hq + h) * S * 4) for k in range(2)] +
+                          ([(("v", 64 + 4 * k, 4), O_ + row * ldo + col) for k in range(16)] if compute_d else []))
+            got = sorted(w.loads)
+            if got != want:
+                raise Fail(f"next-item row loads {got[:3]}..., expected {want[:3]}...")
+            w.loads.clear()
+            checked[0] += 1
 
     sim = Sim(_gen_lines(attn_dq), args, _bwd_mem(B, S, Hq, Hkv, kv), kv, n_wg, None, on_event,
               wave_vgpr=attn_dq.V_PT)
@@ -259,6 +276,8 @@ def run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d):
     want = {(b, h, 256 * z + 64 * w) for b in range(B) for h in range(Hq) for z in range(n_qblk) for w in range(4)}
     assert set(stored) == want and all(c == 1 for c in stored.values()), \
         (len(stored), len(want), [k for k, c in stored.items() if c != 1][:4])
+    # every item after a workgroup's first found its rows requested before the epilogue
+    assert checked[0] == 4 * (n_items - n_wg), (checked[0], n_items, n_wg)
     return sim
 
 

@@ -841,6 +841,7 @@ def _boundary(b: Body, u: int):
     b.item_index(K1, I)
     s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
     p.branch(f"s_cbranch_scc1 .Lnopf{u}", [("scc", 0)], skip_xdl=ACC)
+    p.comment("next rows")
     b.rows_prefetch(I, f"b{u}")
     p.label(f".Lnopf{u}")
     b.epilogue(EPI_BASE)
@@ -848,6 +849,7 @@ def _boundary(b: Body, u: int):
     s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
     p.branch("s_cbranch_scc1 .Lexit", [("scc", 0)], skip_xdl=ACC)
     b.decode_a(I, f"b{u}")
+    p.comment("item")
     p.waitcnt(vm=0)
     b.rows_d(True, f"b{u}")
     b.zero_acc()
