@@ -89,6 +89,40 @@ def test_config3_bf16(gpu):
     _assert_ok(run_gpu_case(gpu, 4, 2048, 16, 16, 128, dtype="bf16", causal=True, f64=False))
 
 
+def test_config5_fwdbwd_heads(gpu):
+    """BASELINE config 5: fp16 non-causal B2 H32 S8192 D128 with per-batch kv_len {8192, 5000}
+    (3192 padded keys, a partial last tile), forward + backward at full size.  Heads are
+    independent (Hq = Hkv), so the oracle checks four of them as the four-head problem made
+    of their Q, K, V and dO columns: O, LSE, dQ, dK and dV of every row of both batches."""
+    import torch
+    from tokamak_amd import attn
+    B, S, H, D, kvl = 2, 8192, 32, 128, [8192, 5000]
+    heads = [0, 7, 20, 31]
+    log(f"[case] config 5 B{B} S{S} Hq{H} Hkv{H} D{D} f16 causal=0 kv_len={kvl}; oracle on heads {heads}")
+    inp = oracle.make_inputs(B, S, H, H, D, "f16", seed_qkv=5, seed_do=6)
+    qkv = to_device(inp["qkv_bits"], "f16", gpu)
+    dout = to_device(inp["dout_bits"], "f16", gpu)
+    kv = torch.tensor(kvl, dtype=torch.int32, device=gpu)
+    o, lse = attn.gqa_fwd(qkv, B, S, H, H, D, causal=False, kv_len=kv)
+    dqkv = attn.gqa_bwd(qkv, o, dout, lse, B, S, H, H, D, causal=False, kv_len=kv)
+    torch.cuda.synchronize()
+
+    def cols(first):
+        return np.concatenate([np.arange((first + h) * D, (first + h + 1) * D) for h in heads])
+    n, qkv_cols = len(heads), np.concatenate([cols(0), cols(H), cols(2 * H)])
+    o_ref, lse_ref = oracle.fwd(inp["qkv"][:, :, qkv_cols], B, S, n, n, D, causal=False, kv_len=kvl)
+    res = [compare("O", from_device(o)[:, :, cols(0)], o_ref, TOL_FWD),
+           compare("LSE", from_device(lse)[:, heads, :], lse_ref, TOL_FWD)]
+    d_ref = oracle.bwd(inp["qkv"][:, :, qkv_cols], oracle.round_to(o_ref, "f16")[0], inp["dout"][:, :, cols(0)],
+                       lse_ref, B, S, n, n, D, causal=False, kv_len=kvl)
+    got = from_device(dqkv)[:, :, qkv_cols]
+    for nm, g, r in zip(("dQ", "dK", "dV"), split_dqkv(got, B, S, n, n, D), split_dqkv(d_ref, B, S, n, n, D)):
+        res.append(compare(nm, g, r, TOL_BWD))
+    for st in res:
+        log(f"    {st['name']:>3}: max_abs={st['max_abs']:.3e} max_rel={st['max_rel']:.3e} bad={st['n_bad']}/{st['n']}")
+    _assert_ok(res)
+
+
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
 @pytest.mark.parametrize("B,S", [(4, 2048), (8, 1000)], ids=["B4S2048", "B8S1000"])
 def test_workspace_row_values(gpu, causal, B, S):
