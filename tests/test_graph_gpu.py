@@ -59,11 +59,17 @@ def _layer(dev, B, S, Hq, Hkv, D, dtype):
 OUTPUTS = ("qkv", "xhat", "istd", "o", "lse", "dqkv", "din", "dgamma", "dbias")
 
 
-@pytest.mark.parametrize("dtype", ["f16", "bf16"])
-def test_layer_step_graph_replays_match_eager(gpu, dtype):
+@pytest.mark.parametrize("shape,dtype", [((2, 384, 4, 2, 64), "f16"), ((2, 384, 4, 2, 64), "bf16"),
+                                         ((8, 512, 8, 8, 64), "bf16")],
+                         ids=["gqa-f16", "gqa-bf16", "config4-bf16"])
+def test_layer_step_graph_replays_match_eager(gpu, shape, dtype):
+    """The layer step (qkv-prep forward, attention forward and backward, qkv-prep backward)
+    captured once and replayed: every replay bit-equal to the eager step, both within the
+    oracles' tolerances.  The last case is BASELINE config 4's attention layer: batch 8,
+    sequence 512, 8 heads of 64, bf16."""
     import torch
     from tokamak_amd import prep
-    B, S, Hq, Hkv, D = 2, 384, 4, 2, 64
+    B, S, Hq, Hkv, D = shape
     log(f"[case] graph step B{B} S{S} Hq{Hq} Hkv{Hkv} D{D} {dtype}")
     P, host, buf, step = _layer(gpu, B, S, Hq, Hkv, D, dtype)
     stream = torch.cuda.Stream(device=gpu)
@@ -104,9 +110,11 @@ def test_layer_step_graph_replays_match_eager(gpu, dtype):
     din_r, dg_r, db_r = oracle.prep_bwd(dq_st.reshape(rows, C), xh_r, is_r, host["gamma"], f, rows, S, Hq, Hkv,
                                         D, True, True, dtype)
     res.append(compare("din", from_device(eager["din"]), din_r, TOL_BWD))
-    # sums over 768 rows of din, each within the dqkv bar: a plausibility bound
-    res.append(compare("dbias", eager["dbias"].cpu().numpy(), db_r, (1e-1, 2e-2)))
-    res.append(compare("dgamma", eager["dgamma"].cpu().numpy(), dg_r, (1e-1, 2e-2)))
+    # sums over all rows of din, each within the dqkv bar: a plausibility bound whose absolute
+    # part grows like the square root of the row count (0.1 at 768 rows)
+    sum_tol = (1e-1 * np.sqrt(rows / 768), 2e-2)
+    res.append(compare("dbias", eager["dbias"].cpu().numpy(), db_r, sum_tol))
+    res.append(compare("dgamma", eager["dgamma"].cpu().numpy(), dg_r, sum_tol))
     for st in res:
         log(f"    {st['name']}: max_abs={st['max_abs']:.3e} bad={st['n_bad']}/{st['n']}")
     assert not [r for r in res if r["n_bad"]], res
