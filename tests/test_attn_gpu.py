@@ -89,6 +89,37 @@ def test_config3_bf16(gpu):
     _assert_ok(run_gpu_case(gpu, 4, 2048, 16, 16, 128, dtype="bf16", causal=True, f64=False))
 
 
+def test_gqa_equals_repeated_heads_full_size(gpu):
+    """Config 3's size with GQA (Hq 16, Hkv 4): O, LSE and dQ are bit-equal to those of the MHA
+    problem whose K and V heads repeat each kv head over its group of 4 (every q-head sees
+    the same keys in the same order), and dK, dV equal that problem's per-head gradients
+    summed over each group (fp32 sums on the host, so within rounding)."""
+    import torch
+    from tokamak_amd import attn
+    B, S, Hq, Hkv, D = 4, 2048, 16, 4, 128
+    g = Hq // Hkv
+    log(f"[case] GQA vs repeated heads B{B} S{S} Hq{Hq} Hkv{Hkv} D{D} f16 causal")
+    inp = oracle.make_inputs(B, S, Hq, Hkv, D, "f16", seed_qkv=21, seed_do=22)
+    bits = inp["qkv_bits"].reshape(B, S, Hq + 2 * Hkv, D)
+    rep = np.repeat(np.arange(Hkv), g)
+    mha = np.concatenate([bits[:, :, :Hq], bits[:, :, Hq + rep], bits[:, :, Hq + Hkv + rep]], axis=2)
+    dout = to_device(inp["dout_bits"], "f16", gpu)
+    outs = {}
+    for name, x, hkv in (("gqa", inp["qkv_bits"], Hkv), ("mha", mha.reshape(B, S, -1), Hq)):
+        qkv = to_device(x, "f16", gpu)
+        o, lse = attn.gqa_fwd(qkv, B, S, Hq, hkv, D, causal=True)
+        dqkv = attn.gqa_bwd(qkv, o, dout, lse, B, S, Hq, hkv, D, causal=True)
+        torch.cuda.synchronize()
+        outs[name] = (from_device(o), from_device(lse), split_dqkv(from_device(dqkv), B, S, Hq, hkv, D))
+    (o1, l1, (dq1, dk1, dv1)), (o2, l2, (dq2, dk2, dv2)) = outs["gqa"], outs["mha"]
+    assert np.array_equal(o1, o2) and np.array_equal(l1, l2) and np.array_equal(dq1, dq2)
+    for nm, got, per_head in (("dK", dk1, dk2), ("dV", dv1, dv2)):
+        summed = per_head.reshape(B, S, Hkv, g, D).sum(axis=3)
+        st = compare(nm, got, summed, TOL_BWD)
+        log(f"    {nm}: max_abs={st['max_abs']:.3e} bad={st['n_bad']}/{st['n']}")
+        assert not st["n_bad"], st
+
+
 def test_config5_fwdbwd_heads(gpu):
     """BASELINE config 5: fp16 non-causal B2 H32 S8192 D128 with per-batch kv_len {8192, 5000}
     (3192 padded keys, a partial last tile), forward + backward at full size.  Heads are
