@@ -54,7 +54,10 @@ enum {
     TKM_ATTN_EUNSUPPORTED = -2, /* D not in {64, 128}, unknown dtype, size beyond int range */
     TKM_ATTN_EALIGN = -3,       /* misaligned pointer */
     TKM_ATTN_EWORKSPACE = -4,   /* workspace missing or smaller than required */
-    TKM_ATTN_ELAUNCH = -5       /* the HIP runtime rejected a kernel launch */
+    TKM_ATTN_ELAUNCH = -5,      /* the HIP runtime rejected a kernel launch */
+    TKM_ATTN_ECOMPILE = -6,     /* hipRTC rejected a generated source */
+    TKM_ATTN_EDEVICE = -7       /* no device current, a HIP module/graph call failed, or the
+                                   gfx950 assembly kernels failed to load */
 };
 
 /* Backward stages.  Two valid schedules:
@@ -92,6 +95,33 @@ TKM_ATTN_API int tkm_attn_bwd_stage(int stage, const void *qkv, const void *o, c
                                     int B, int S, int Hq, int Hkv, int D, float scale, int causal,
                                     int dtype, void *workspace, size_t workspace_bytes,
                                     void *stream);
+
+/* Loads this library's gfx950 assembly kernels (fp16, D = 128) on the current device.  Call
+ * it once per device before capturing a graph, as the runtime does at ignite; otherwise the
+ * first call on a device loads them (inside a capture, with the thread's capture mode
+ * relaxed so that nothing is recorded).  Returns TKM_ATTN_OK (also on a device that is not
+ * gfx950, where the HIP kernels serve every shape) or TKM_ATTN_EDEVICE when a code object
+ * fails to load; the calls that need them then fail with TKM_ATTN_EDEVICE too, they never
+ * switch to the slower kernels.  No reference counterpart (the reference JIT-compiles its
+ * generated kernels at ignite, src/tkm_gpu.cu:1047-1078; its attention kernels are
+ * compiled ahead of time). */
+TKM_ATTN_API int tkm_attn_init(void);
+
+/* 1 if the assembly kernels are loaded on the current device (gfx950), else 0. */
+TKM_ATTN_API int tkm_attn_asm_available(void);
+
+/* Kernels launched by the calling thread's last tkm_attn_fwd / _bwd / _bwd_stage call
+ * (OR of the bits below; 0 after a call that failed validation).  No reference counterpart. */
+enum {
+    TKM_ATTN_K_FWD_ASM = 1,     /* tkm_fa_fwd_d128_f16 (assembly) */
+    TKM_ATTN_K_FWD_HIP = 2,     /* fa_fwd_kernel (HIP) */
+    TKM_ATTN_K_DQ_ASM = 4,      /* tkm_fa_bwd_dq_d128_f16 (assembly) */
+    TKM_ATTN_K_DQ_HIP = 8,      /* fa_bwd_dq_kernel (HIP) */
+    TKM_ATTN_K_DKDV_ASM = 16,   /* tkm_fa_bwd_dkdv_d128_f16 (assembly) */
+    TKM_ATTN_K_DKDV_HIP = 32,   /* fa_bwd_dkdv_kernel (HIP) */
+    TKM_ATTN_K_DELTA_HIP = 64   /* fa_bwd_delta_kernel (HIP) */
+};
+TKM_ATTN_API unsigned tkm_attn_last_kernels(void);
 
 /* Static description of a status code, and the last failure message of this thread. */
 TKM_ATTN_API const char *tkm_attn_status_string(int status);

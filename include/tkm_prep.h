@@ -53,11 +53,6 @@
 extern "C" {
 #endif
 
-enum {
-    TKM_ATTN_ECOMPILE = -6,     /* hipRTC rejected the generated source */
-    TKM_ATTN_EDEVICE = -7       /* no gfx950 device current, or a HIP module/graph call failed */
-};
-
 /* What the runtime copies out of the reference's qkv_prep TkmNode (tkm_registry.c:750-765)
  * and its plasma group (tkm_core.c:494-505). */
 typedef struct tkm_prep_desc {

@@ -12,6 +12,7 @@ import sys
 import numpy as np
 
 import oracle
+from parity_checks import compare  # noqa: F401  (NaN-safe; re-exported for the tests)
 
 TOL_FWD = (2e-3, 1e-2)
 TOL_BWD = (5e-3, 2e-2)
@@ -31,31 +32,6 @@ def to_device(bits: np.ndarray, dtype: str, device):
 def from_device(t) -> np.ndarray:
     import torch
     return t.detach().to(torch.float32).cpu().numpy()
-
-
-def compare(name: str, got: np.ndarray, ref: np.ndarray, tol) -> dict:
-    atol, rtol = tol
-    got = np.asarray(got, dtype=np.float64)
-    ref = np.asarray(ref, dtype=np.float64)
-    assert got.shape == ref.shape, (name, got.shape, ref.shape)
-    finite = np.isfinite(ref)
-    # equal infinities (LSE of fully masked rows) compare equal
-    inf_ok = np.all(got[~finite] == ref[~finite])
-    diff = np.abs(got[finite] - ref[finite])
-    bound = atol + rtol * np.abs(ref[finite])
-    bad = diff > bound
-    stats = {
-        "name": name,
-        "max_abs": float(diff.max()) if diff.size else 0.0,
-        "max_rel": float((diff / np.maximum(np.abs(ref[finite]), 1e-6)).max()) if diff.size else 0.0,
-        "n_bad": int(bad.sum()) + (0 if inf_ok else 1),
-        "n": int(ref.size),
-    }
-    if stats["n_bad"]:
-        idx = np.argwhere(np.abs(got - ref) > atol + rtol * np.abs(ref))[:5]
-        stats["examples"] = [(tuple(int(i) for i in ix), float(got[tuple(ix)]), float(ref[tuple(ix)]))
-                             for ix in idx]
-    return stats
 
 
 def split_dqkv(dqkv: np.ndarray, B, S, Hq, Hkv, D):

@@ -18,7 +18,8 @@ def test_library_exports_header_functions():
     names = attn.header_functions()
     assert set(names) >= {"tkm_attn_fwd", "tkm_attn_bwd", "tkm_attn_bwd_stage",
                           "tkm_attn_bwd_workspace_bytes", "tkm_attn_status_string",
-                          "tkm_attn_last_error", "tkm_attn_version"}
+                          "tkm_attn_last_error", "tkm_attn_version", "tkm_attn_init",
+                          "tkm_attn_asm_available", "tkm_attn_last_kernels"}
     L = attn.lib()
     for n in names:
         assert hasattr(L, n), n
@@ -36,9 +37,9 @@ def test_library_exports_header_functions():
 
 def test_version_and_status_strings():
     L = attn.lib()
-    assert L.tkm_attn_version() == 100
+    assert L.tkm_attn_version() == 200
     assert L.tkm_attn_status_string(OK) == b"ok"
-    for st in (EINVAL, EUNSUPPORTED, EALIGN, EWORKSPACE, -5):
+    for st in (EINVAL, EUNSUPPORTED, EALIGN, EWORKSPACE, -5, -6, -7):
         assert L.tkm_attn_status_string(st) not in (b"ok", b"unknown status")
     assert L.tkm_attn_status_string(-99) == b"unknown status"
 
@@ -68,6 +69,7 @@ def fwd(qkv=P16, o=P16B, lse=None, kv=None, B=1, S=8, Hq=2, Hkv=1, D=64, scale=0
 def test_fwd_rejects(kw, status, msg):
     assert fwd(**kw) == status
     assert msg in attn.lib().tkm_attn_last_error()
+    assert attn.lib().tkm_attn_last_kernels() == 0  # nothing launched
 
 
 def bwd(stage=None, ws=P16, wsb=None, B=1, S=8, Hq=2, Hkv=1, D=64, lse=P16, dout=P16, scale=0.125):

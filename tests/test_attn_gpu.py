@@ -120,16 +120,16 @@ def test_gqa_equals_repeated_heads_full_size(gpu):
         assert not st["n_bad"], st
 
 
-def test_config5_fwdbwd_heads(gpu):
+def test_config5_fwdbwd_all_heads(gpu):
     """BASELINE config 5: fp16 non-causal B2 H32 S8192 D128 with per-batch kv_len {8192, 5000}
-    (3192 padded keys, a partial last tile), forward + backward at full size.  Heads are
-    independent (Hq = Hkv), so the oracle checks four of them as the four-head problem made
-    of their Q, K, V and dO columns: O, LSE, dQ, dK and dV of every row of both batches."""
+    (3192 padded keys, a partial last tile), forward + backward at full size.  Every head is
+    checked: heads are independent (Hq = Hkv), so the oracle runs on groups of 8 heads as the
+    8-head problem made of their Q, K, V and dO columns, covering O, LSE, dQ, dK and dV of
+    every row of both batches."""
     import torch
     from tokamak_amd import attn
     B, S, H, D, kvl = 2, 8192, 32, 128, [8192, 5000]
-    heads = [0, 7, 20, 31]
-    log(f"[case] config 5 B{B} S{S} Hq{H} Hkv{H} D{D} f16 causal=0 kv_len={kvl}; oracle on heads {heads}")
+    log(f"[case] config 5 B{B} S{S} Hq{H} Hkv{H} D{D} f16 causal=0 kv_len={kvl}; oracle on all heads")
     inp = oracle.make_inputs(B, S, H, H, D, "f16", seed_qkv=5, seed_do=6)
     qkv = to_device(inp["qkv_bits"], "f16", gpu)
     dout = to_device(inp["dout_bits"], "f16", gpu)
@@ -137,20 +137,27 @@ def test_config5_fwdbwd_heads(gpu):
     o, lse = attn.gqa_fwd(qkv, B, S, H, H, D, causal=False, kv_len=kv)
     dqkv = attn.gqa_bwd(qkv, o, dout, lse, B, S, H, H, D, causal=False, kv_len=kv)
     torch.cuda.synchronize()
+    o_g, lse_g, d_g = from_device(o), from_device(lse), from_device(dqkv)
+    del qkv, dout, o, lse, dqkv
+    res = []
+    for h0 in range(0, H, 8):
+        heads = list(range(h0, h0 + 8))
 
-    def cols(first):
-        return np.concatenate([np.arange((first + h) * D, (first + h + 1) * D) for h in heads])
-    n, qkv_cols = len(heads), np.concatenate([cols(0), cols(H), cols(2 * H)])
-    o_ref, lse_ref = oracle.fwd(inp["qkv"][:, :, qkv_cols], B, S, n, n, D, causal=False, kv_len=kvl)
-    res = [compare("O", from_device(o)[:, :, cols(0)], o_ref, TOL_FWD),
-           compare("LSE", from_device(lse)[:, heads, :], lse_ref, TOL_FWD)]
-    d_ref = oracle.bwd(inp["qkv"][:, :, qkv_cols], oracle.round_to(o_ref, "f16")[0], inp["dout"][:, :, cols(0)],
-                       lse_ref, B, S, n, n, D, causal=False, kv_len=kvl)
-    got = from_device(dqkv)[:, :, qkv_cols]
-    for nm, g, r in zip(("dQ", "dK", "dV"), split_dqkv(got, B, S, n, n, D), split_dqkv(d_ref, B, S, n, n, D)):
-        res.append(compare(nm, g, r, TOL_BWD))
-    for st in res:
-        log(f"    {st['name']:>3}: max_abs={st['max_abs']:.3e} max_rel={st['max_rel']:.3e} bad={st['n_bad']}/{st['n']}")
+        def cols(first):
+            return np.concatenate([np.arange((first + h) * D, (first + h + 1) * D) for h in heads])
+        n, qkv_cols = len(heads), np.concatenate([cols(0), cols(H), cols(2 * H)])
+        o_ref, lse_ref = oracle.fwd(inp["qkv"][:, :, qkv_cols], B, S, n, n, D, causal=False, kv_len=kvl)
+        part = [compare(f"O[h{h0}+]", o_g[:, :, cols(0)], o_ref, TOL_FWD),
+                compare(f"LSE[h{h0}+]", lse_g[:, heads, :], lse_ref, TOL_FWD)]
+        d_ref = oracle.bwd(inp["qkv"][:, :, qkv_cols], oracle.round_to(o_ref, "f16")[0],
+                           inp["dout"][:, :, cols(0)], lse_ref, B, S, n, n, D, causal=False, kv_len=kvl)
+        for nm, g, r in zip(("dQ", "dK", "dV"), split_dqkv(d_g[:, :, qkv_cols], B, S, n, n, D),
+                            split_dqkv(d_ref, B, S, n, n, D)):
+            part.append(compare(f"{nm}[h{h0}+]", g, r, TOL_BWD))
+        for st in part:
+            log(f"    {st['name']:>9}: max_abs={st['max_abs']:.3e} max_rel={st['max_rel']:.3e} "
+                f"bad={st['n_bad']}/{st['n']}")
+        res += part
     _assert_ok(res)
 
 
@@ -287,3 +294,32 @@ def test_growing_scores_redo_path(gpu, causal, dtype):
     for st in res:
         log(f"    {st['name']}: max_abs={st['max_abs']:.3e} bad={st['n_bad']}")
     _assert_ok(res)
+
+
+def test_kernel_paths(gpu):
+    """Which kernels each configuration runs (tkm_attn_last_kernels): fp16 D=128 -- the
+    config-3 hot path -- takes the three gfx950 assembly kernels, and only it; bf16 and D=64
+    take the HIP kernels.  tkm_attn_init loads the code objects (the runtime calls it before
+    capturing a step)."""
+    import torch
+    from tokamak_amd import attn
+    attn.init()
+    assert attn.asm_available()
+    B, S, Hq, Hkv = 1, 300, 4, 2
+    cases = [(128, torch.float16, ["fwd_asm"], ["dq_asm", "dkdv_asm"]),
+             (128, torch.bfloat16, ["fwd_hip"], ["dq_hip", "dkdv_hip"]),
+             (64, torch.float16, ["fwd_hip"], ["dq_hip", "dkdv_hip"]),
+             (64, torch.bfloat16, ["fwd_hip"], ["dq_hip", "dkdv_hip"])]
+    for D, dt, k_fwd, k_bwd in cases:
+        log(f"[case] kernel path D{D} {dt}")
+        qkv = torch.randn((B, S, (Hq + 2 * Hkv) * D), device=gpu).to(dt)
+        dout = torch.randn((B, S, Hq * D), device=gpu).to(dt)
+        o, lse = attn.gqa_fwd(qkv, B, S, Hq, Hkv, D, causal=True)
+        assert attn.last_kernels() == k_fwd, (D, dt, attn.last_kernels())
+        attn.gqa_bwd(qkv, o, dout, lse, B, S, Hq, Hkv, D, causal=True)
+        assert attn.last_kernels() == k_bwd, (D, dt, attn.last_kernels())
+        ws = torch.empty(attn.bwd_workspace_bytes(B, S, Hq), dtype=torch.uint8, device=gpu)
+        attn.gqa_bwd(qkv, o, dout, lse, B, S, Hq, Hkv, D, causal=True, workspace=ws,
+                     stage=attn.BWD_DELTA)
+        assert attn.last_kernels() == ["delta_hip"]
+    torch.cuda.synchronize()

@@ -60,13 +60,14 @@ OUTPUTS = ("qkv", "xhat", "istd", "o", "lse", "dqkv", "din", "dgamma", "dbias")
 
 
 @pytest.mark.parametrize("shape,dtype", [((2, 384, 4, 2, 64), "f16"), ((2, 384, 4, 2, 64), "bf16"),
-                                         ((8, 512, 8, 8, 64), "bf16")],
-                         ids=["gqa-f16", "gqa-bf16", "config4-bf16"])
+                                         ((8, 512, 8, 8, 64), "bf16"), ((2, 512, 4, 2, 128), "f16")],
+                         ids=["gqa-f16", "gqa-bf16", "config4-bf16", "gqa-f16-d128-asm"])
 def test_layer_step_graph_replays_match_eager(gpu, shape, dtype):
     """The layer step (qkv-prep forward, attention forward and backward, qkv-prep backward)
     captured once and replayed: every replay bit-equal to the eager step, both within the
-    oracles' tolerances.  The last case is BASELINE config 4's attention layer: batch 8,
-    sequence 512, 8 heads of 64, bf16."""
+    oracles' tolerances.  The third case is BASELINE config 4's attention layer: batch 8,
+    sequence 512, 8 heads of 64, bf16; the last one captures the gfx950 assembly kernels
+    (fp16, D = 128, launched through hipModuleLaunchKernel)."""
     import torch
     from tokamak_amd import prep
     B, S, Hq, Hkv, D = shape
@@ -77,6 +78,9 @@ def test_layer_step_graph_replays_match_eager(gpu, shape, dtype):
         step(stream)
     torch.cuda.synchronize()
     eager = {k: buf[k].clone() for k in OUTPUTS}
+    if D == 128 and dtype == "f16":
+        from tokamak_amd import attn
+        assert attn.last_kernels() == ["dq_asm", "dkdv_asm"], attn.last_kernels()
 
     prep.Graph.begin(stream)
     try:
@@ -119,3 +123,19 @@ def test_layer_step_graph_replays_match_eager(gpu, shape, dtype):
         log(f"    {st['name']}: max_abs={st['max_abs']:.3e} bad={st['n_bad']}/{st['n']}")
     assert not [r for r in res if r["n_bad"]], res
     P.close()
+
+
+def test_first_attention_call_inside_capture():
+    """A fresh process whose very first attention call is inside a global-mode capture (the
+    reference captures its first step): the code objects load without being recorded, the
+    assembly kernels are the ones captured, and three replays equal the eager run bit for
+    bit.  Runs tests/graph_first_call_child.py as a child process (a fresh HIP context)."""
+    import os
+    import subprocess
+    import sys
+    child = os.path.join(os.path.dirname(os.path.abspath(__file__)), "graph_first_call_child.py")
+    log("[case] first attention call inside a capture (child process)")
+    r = subprocess.run([sys.executable, "-u", child], capture_output=True, text=True, timeout=300)
+    for line in (r.stdout + r.stderr).splitlines()[-12:]:
+        log("    " + line)
+    assert r.returncode == 0 and r.stdout.strip().endswith("OK"), r.stdout + r.stderr

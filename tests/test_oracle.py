@@ -237,6 +237,49 @@ def test_finite_differences_fp64():
         assert abs(fd - an) <= 2e-3 * max(1.0, abs(an)), (part, fd, an)
 
 
+def test_finite_differences_config1():
+    """BASELINE config 1 (fp32 B2 H4 S128 D64, causal, Q/K/V seed 0, dO seed 1): the oracle's
+    dQ, dK, dV against central differences of L = sum(O * dO) in float64, along random
+    directions confined to Q, K and V of each batch, and at 48 single coordinates drawn from
+    every part (the first query row, the last key row, a masked-out-early key).  The oracle
+    takes and returns fp32, so L carries about 1e-5 of rounding noise: eps = 1e-2 keeps the
+    truncation error (~eps^2) and that noise (~1e-5 / eps) below the bars."""
+    B, S, Hq, Hkv, D = 2, 128, 4, 4, 64
+    inp = oracle.make_inputs(B, S, Hq, Hkv, D, "f32", seed_qkv=0, seed_do=1)
+    x = inp["qkv"].astype(np.float64)
+    w = inp["dout"].astype(np.float64)
+
+    def loss(xx):
+        o, _ = oracle.fwd(xx, B, S, Hq, Hkv, D, causal=True, f64=True)
+        return float((o.astype(np.float64) * w).sum())
+
+    o, lse = oracle.fwd(inp["qkv"], B, S, Hq, Hkv, D, causal=True, f64=True)
+    g = oracle.bwd(inp["qkv"], o, inp["dout"], lse, B, S, Hq, Hkv, D, causal=True,
+                   f64=True).astype(np.float64)
+    rng = np.random.default_rng(11)
+    x4 = x.reshape(B, S, Hq + 2 * Hkv, D)
+    parts = [slice(0, Hq), slice(Hq, Hq + Hkv), slice(Hq + Hkv, Hq + 2 * Hkv)]
+    eps = 1e-2
+    for b in range(B):
+        for part in parts:
+            u = np.zeros_like(x4)
+            u[b, :, part] = rng.standard_normal(u[b, :, part].shape)
+            u = u.reshape(x.shape)
+            fd = (loss(x + eps * u) - loss(x - eps * u)) / (2 * eps)
+            an = float((g * u).sum())
+            assert abs(fd - an) <= 2e-3 * max(1.0, abs(an)), (b, part, fd, an)
+    coords = [(0, 0, 0, 3), (1, S - 1, Hq, 5), (0, 0, Hq + 1, 7), (1, 64, Hq + Hkv + 2, 1)]
+    coords += [(int(rng.integers(B)), int(rng.integers(S)), int(rng.integers(Hq + 2 * Hkv)),
+                int(rng.integers(D))) for _ in range(44)]
+    g4 = g.reshape(x4.shape)
+    for c in coords:
+        e = np.zeros_like(x4)
+        e[c] = 1.0
+        e = e.reshape(x.shape)
+        fd = (loss(x + eps * e) - loss(x - eps * e)) / (2 * eps)
+        assert abs(fd - g4[c]) <= 1e-4 + 2e-3 * abs(g4[c]), (c, fd, g4[c])
+
+
 # -------------------------------------------------------------------------- invariants
 def test_invariants():
     B, S, H, D = 2, 24, 2, 64

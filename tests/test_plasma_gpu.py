@@ -15,24 +15,15 @@ import pytest
 
 import oracle
 from attn_cases import from_device, log, to_device
+from parity_checks import check16_mask
 
 pytestmark = pytest.mark.gpu
 
 
-def ulp(ref, dtype):
-    p, emin = (11, -14) if dtype == "f16" else (8, -126)
-    a = np.maximum(np.abs(ref.astype(np.float64)), 2.0 ** (emin - 30))
-    return 2.0 ** (np.maximum(np.floor(np.log2(a)), emin) - (p - 1))
-
-
 def check16(name, got, ref, dtype):
-    got = np.asarray(got, np.float64)
-    ref = np.asarray(ref, np.float64)
-    assert got.shape == ref.shape, (name, got.shape, ref.shape)
-    bound = 2 * ulp(ref, dtype) + 1e-4 * max(1.0, float(np.abs(ref).max(initial=0.0)))
-    diff = np.abs(got - ref)
-    bad = diff > bound
-    log(f"    {name}: max_abs={diff.max(initial=0.0):.3e} n_bad={int(bad.sum())}/{ref.size}")
+    bad = check16_mask(got, ref, dtype, n_ulp=2, rel_floor=1e-4)
+    diff = np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))
+    log(f"    {name}: max_abs={np.nanmax(diff, initial=0.0):.3e} n_bad={int(bad.sum())}/{bad.size}")
     if bad.any():
         i = tuple(np.argwhere(bad)[0])
         pytest.fail(f"{name}: {int(bad.sum())} elements off, e.g. {i}: gpu {got[i]} ref {ref[i]}")

@@ -67,8 +67,32 @@ def lib() -> ctypes.CDLL:
     L.tkm_attn_status_string.restype = ctypes.c_char_p
     L.tkm_attn_last_error.restype = ctypes.c_char_p
     L.tkm_attn_version.restype = _i
+    L.tkm_attn_init.restype = _i
+    L.tkm_attn_asm_available.restype = _i
+    L.tkm_attn_last_kernels.restype = ctypes.c_uint
     _lib = L
     return L
+
+
+# Bits of tkm_attn_last_kernels (include/tkm_attn.h)
+KERNEL_BITS = {"fwd_asm": 1, "fwd_hip": 2, "dq_asm": 4, "dq_hip": 8, "dkdv_asm": 16,
+               "dkdv_hip": 32, "delta_hip": 64}
+
+
+def init() -> None:
+    """Load the gfx950 assembly kernels on the current device (tkm_attn_init); raises if a
+    code object fails to load."""
+    _check("tkm_attn_init", lib().tkm_attn_init())
+
+
+def asm_available() -> bool:
+    return bool(lib().tkm_attn_asm_available())
+
+
+def last_kernels() -> list:
+    """Names of the kernels the calling thread's last tkm_attn_* call launched."""
+    bits = int(lib().tkm_attn_last_kernels())
+    return [n for n, b in KERNEL_BITS.items() if bits & b]
 
 
 def _check(fn: str, rc: int) -> None:
@@ -172,6 +196,6 @@ def attention_flops(B, S, Hq, D, causal, kv_len=None, mode="fwd") -> float:
     return {"fwd": f, "bwd": 2.5 * f, "fwdbwd": 3.5 * f}[mode]
 
 
-__all__ = ["gqa_fwd", "gqa_bwd", "bwd_workspace_bytes", "attention_flops", "default_scale",
+__all__ = ["gqa_fwd", "gqa_bwd", "init", "asm_available", "last_kernels", "KERNEL_BITS", "bwd_workspace_bytes", "attention_flops", "default_scale",
            "lib", "header_functions", "AttnError", "F16", "BF16", "BWD_DELTA", "BWD_DKDV",
            "BWD_DQ", "BWD_DQ_DELTA"]

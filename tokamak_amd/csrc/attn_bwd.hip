@@ -537,18 +537,34 @@ static int launch_dq_write_t(const BwdArgs& a) { return launch_dq_t<D, DT, true>
     ((a).D == 128 ? ((a).dtype == DT_F16 ? FN<128, DT_F16>(a) : FN<128, DT_BF16>(a))        \
                   : ((a).dtype == DT_F16 ? FN<64, DT_F16>(a) : FN<64, DT_BF16>(a)))
 
-int launch_bwd_delta(const BwdArgs& a) { return TKM_DISPATCH(launch_delta_t, a); }
+// Each stage tries its assembly kernel first (D = 128 fp16); 1 from it means "not handled
+// there" and selects the HIP kernel, any other status is final.
+static int settle(int r, unsigned asm_bit) {
+    if (r == 0) note_kernels(asm_bit);
+    return r;
+}
+
+int launch_bwd_delta(const BwdArgs& a) {
+    note_kernels(kDeltaHip);
+    return TKM_DISPATCH(launch_delta_t, a);
+}
 int launch_bwd_dkdv(const BwdArgs& a) {
     const int r = launch_bwd_dkdv_asm(a);
-    return r != 1 ? r : TKM_DISPATCH(launch_dkdv_t, a);
+    if (r != 1) return settle(r, kDkdvAsm);
+    note_kernels(kDkdvHip);
+    return TKM_DISPATCH(launch_dkdv_t, a);
 }
 int launch_bwd_dq(const BwdArgs& a) {
     const int r = launch_bwd_dq_asm(a, false);
-    return r != 1 ? r : TKM_DISPATCH(launch_dq_read_t, a);
+    if (r != 1) return settle(r, kDqAsm);
+    note_kernels(kDqHip);
+    return TKM_DISPATCH(launch_dq_read_t, a);
 }
 int launch_bwd_dq_delta(const BwdArgs& a) {
     const int r = launch_bwd_dq_asm(a, true);
-    return r != 1 ? r : TKM_DISPATCH(launch_dq_write_t, a);
+    if (r != 1) return settle(r, kDqAsm);
+    note_kernels(kDqHip);
+    return TKM_DISPATCH(launch_dq_write_t, a);
 }
 
 }  // namespace tkm

@@ -38,12 +38,6 @@
 #include "attn_common.h"
 #include "attn_launch.h"
 
-#ifndef FWD_QB
-#define FWD_QB 1
-#endif
-#ifndef FWD_LEAD
-#define FWD_LEAD 2  // LDS operand reads in flight ahead of their MFMAs
-#endif
 
 namespace tkm {
 
@@ -52,11 +46,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
                    float* __restrict__ lse, const int32_t* __restrict__ kv_len, int B, int S,
                    int Hq, int Hkv, float sl2, int causal, int n_qblk) {
-#ifdef TKM_DEBUG_NO_PRE
-    constexpr bool PRE = false;
-#else
     constexpr bool PRE = (DT == DT_F16);  // scale folded into Q, -m into the accumulator
-#endif
     constexpr bool SPL = Split<DT>::on;   // bf16: P as hi + lo
     constexpr int NW = 4;                 // waves per workgroup (two workgroups per CU)
     constexpr int WR = 32 * QB;           // query rows per wave
@@ -404,7 +394,7 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
 
 template <int D, int DT>
 static int launch_fwd_t(const FwdArgs& a) {
-    constexpr int QB = FWD_QB;
+    constexpr int QB = 1;  // 32-row blocks per wave
     constexpr int BM = 128 * QB;
     const int n_qblk = (a.S + BM - 1) / BM;
     dim3 grid((unsigned)(a.B * a.Hq * n_qblk)), block(256);
@@ -416,7 +406,11 @@ static int launch_fwd_t(const FwdArgs& a) {
 
 int launch_fwd(const FwdArgs& a) {
     const int rc = launch_fwd_asm(a);  // D = 128 fp16: hand-scheduled assembly kernel
-    if (rc != 1) return rc;
+    if (rc != 1) {
+        if (rc == 0) note_kernels(kFwdAsm);
+        return rc;
+    }
+    note_kernels(kFwdHip);
     if (a.D == 128) return a.dtype == DT_F16 ? launch_fwd_t<128, DT_F16>(a) : launch_fwd_t<128, DT_BF16>(a);
     return a.dtype == DT_F16 ? launch_fwd_t<64, DT_F16>(a) : launch_fwd_t<64, DT_BF16>(a);
 }

@@ -32,8 +32,24 @@ struct BwdArgs {
     void* stream;
 };
 
+// Kernels a call launched (tkm_attn_last_kernels); values of the TKM_ATTN_K_* bits of
+// include/tkm_attn.h.
+enum KernelBit : unsigned {
+    kFwdAsm = 1u, kFwdHip = 2u, kDqAsm = 4u, kDqHip = 8u, kDkdvAsm = 16u, kDkdvHip = 32u,
+    kDeltaHip = 64u
+};
+void note_kernels(unsigned bits);  // ORs bits into the calling thread's record
+
+// Assembly code objects: load on the current device (0, or -2 with asm_load_error()),
+// and whether the assembly path exists there (gfx950, loaded).
+int asm_init_current_device();
+bool asm_available_current_device();
+const char* asm_load_error();
+
+// Launchers return 0 (launched), -1 (HIP launch error) or -2 (the assembly code objects
+// failed to load on a gfx950 device).
 int launch_fwd(const FwdArgs& a);
-int launch_fwd_asm(const FwdArgs& a);  // 1 = configuration not handled there
+int launch_fwd_asm(const FwdArgs& a);  // also 1 = configuration not handled there
 int launch_bwd_delta(const BwdArgs& a);
 int launch_bwd_dkdv(const BwdArgs& a);
 int launch_bwd_dkdv_asm(const BwdArgs& a);  // 1 = configuration not handled there

@@ -11,6 +11,14 @@
 #include "tkm_attn.h"
 #include "tkm_prep_internal.h"
 
+namespace tkm {
+namespace {
+thread_local unsigned t_kernels = 0;  // kernels launched by this thread's current/last call
+}  // namespace
+void note_kernels(unsigned bits) { t_kernels |= bits; }
+}  // namespace tkm
+
+
 namespace {
 
 int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -51,6 +59,15 @@ int check_shape(int B, int S, int Hq, int Hkv, int D, int causal, int dtype) {
     return TKM_ATTN_OK;
 }
 
+// Status of a launcher (0, -1 launch error, -2 code objects failed to load) as an ABI status.
+int launch_status(int rc, const char* what) {
+    if (rc == 0) return TKM_ATTN_OK;
+    if (rc == -2)
+        return fail(TKM_ATTN_EDEVICE, "%s: gfx950 assembly kernels failed to load (%s)", what,
+                    tkm::asm_load_error());
+    return fail(TKM_ATTN_ELAUNCH, "%s: kernel launch failed", what);
+}
+
 int run_bwd_stage(int stage, const tkm::BwdArgs& a) {
     int rc = 0;
     switch (stage) {
@@ -60,14 +77,16 @@ int run_bwd_stage(int stage, const tkm::BwdArgs& a) {
         case TKM_ATTN_BWD_DQ_DELTA: rc = tkm::launch_bwd_dq_delta(a); break;
         default: return fail(TKM_ATTN_EINVAL, "unknown backward stage %d", stage);
     }
-    if (rc != 0) return fail(TKM_ATTN_ELAUNCH, "kernel launch failed in backward stage %d", stage);
-    return TKM_ATTN_OK;
+    if (rc == 0) return TKM_ATTN_OK;
+    char what[48];
+    snprintf(what, sizeof what, "backward stage %d", stage);
+    return launch_status(rc, what);
 }
 
-int prepare_bwd(tkm::BwdArgs& a, const void* qkv, const void* o, const void* dout,
-                const float* lse, void* dqkv, const int32_t* kv_len, int B, int S, int Hq,
-                int Hkv, int D, float scale, int causal, int dtype, void* workspace,
-                size_t workspace_bytes, void* stream) {
+// Checks of the backward's arguments other than the workspace.
+int check_bwd_args(const void* qkv, const void* o, const void* dout, const float* lse,
+                   void* dqkv, const int32_t* kv_len, int B, int S, int Hq, int Hkv, int D,
+                   float scale, int causal, int dtype) {
     if (!qkv || !o || !dout || !lse || !dqkv)
         return fail(TKM_ATTN_EINVAL, "qkv, o, dout, lse and dqkv must be non-null");
     int rc = check_shape(B, S, Hq, Hkv, D, causal, dtype);
@@ -75,12 +94,21 @@ int prepare_bwd(tkm::BwdArgs& a, const void* qkv, const void* o, const void* dou
     if (!aligned(qkv, 16) || !aligned(o, 16) || !aligned(dout, 16) || !aligned(dqkv, 16) ||
         !aligned(lse, 4) || (kv_len && !aligned(kv_len, 4)))
         return fail(TKM_ATTN_EALIGN, "16-bit tensors must be 16-byte aligned, lse/kv_len 4-byte");
+    if (!(scale > 0.f) || scale == INFINITY) return fail(TKM_ATTN_EINVAL, "scale must be positive and finite");
+    return TKM_ATTN_OK;
+}
+
+int prepare_bwd(tkm::BwdArgs& a, const void* qkv, const void* o, const void* dout,
+                const float* lse, void* dqkv, const int32_t* kv_len, int B, int S, int Hq,
+                int Hkv, int D, float scale, int causal, int dtype, void* workspace,
+                size_t workspace_bytes, void* stream) {
+    int rc = check_bwd_args(qkv, o, dout, lse, dqkv, kv_len, B, S, Hq, Hkv, D, scale, causal, dtype);
+    if (rc) return rc;
     const size_t need = tkm_attn_bwd_workspace_bytes(B, S, Hq);
     if (!workspace || workspace_bytes < need)
         return fail(TKM_ATTN_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
                     workspace ? workspace_bytes : (size_t)0);
     if (!aligned(workspace, 16)) return fail(TKM_ATTN_EALIGN, "workspace must be 16-byte aligned");
-    if (!(scale > 0.f) || scale == INFINITY) return fail(TKM_ATTN_EINVAL, "scale must be positive and finite");
     a = tkm::BwdArgs{qkv, o, dout, lse, dqkv, kv_len, (float*)workspace,
                      (float*)((char*)workspace + tkm_ws_pairs_offset(B, S, Hq)),
                      B, S, Hq, Hkv, D, scale, causal, dtype, stream};
@@ -94,6 +122,7 @@ extern "C" {
 TKM_ATTN_API int tkm_attn_fwd(const void* qkv, void* o, float* lse, const int32_t* kv_len, int B,
                               int S, int Hq, int Hkv, int D, float scale, int causal, int dtype,
                               void* stream) {
+    tkm::t_kernels = 0;
     if (!qkv || !o) return fail(TKM_ATTN_EINVAL, "qkv and o must be non-null");
     int rc = check_shape(B, S, Hq, Hkv, D, causal, dtype);
     if (rc) return rc;
@@ -102,8 +131,7 @@ TKM_ATTN_API int tkm_attn_fwd(const void* qkv, void* o, float* lse, const int32_
         return fail(TKM_ATTN_EALIGN, "16-bit tensors must be 16-byte aligned, lse/kv_len 4-byte");
     if (!(scale > 0.f) || scale == INFINITY) return fail(TKM_ATTN_EINVAL, "scale must be positive and finite");
     tkm::FwdArgs a{qkv, o, lse, kv_len, B, S, Hq, Hkv, D, scale, causal, dtype, stream};
-    if (tkm::launch_fwd(a) != 0) return fail(TKM_ATTN_ELAUNCH, "forward kernel launch failed");
-    return TKM_ATTN_OK;
+    return launch_status(tkm::launch_fwd(a), "forward");
 }
 
 TKM_ATTN_API size_t tkm_attn_bwd_workspace_bytes(int B, int S, int Hq) {
@@ -115,6 +143,7 @@ TKM_ATTN_API int tkm_attn_bwd(const void* qkv, const void* o, const void* dout, 
                               void* dqkv, const int32_t* kv_len, int B, int S, int Hq, int Hkv,
                               int D, float scale, int causal, int dtype, void* workspace,
                               size_t workspace_bytes, void* stream) {
+    tkm::t_kernels = 0;
     tkm::BwdArgs a;
     int rc = prepare_bwd(a, qkv, o, dout, lse, dqkv, kv_len, B, S, Hq, Hkv, D, scale, causal,
                          dtype, workspace, workspace_bytes, stream);
@@ -131,6 +160,7 @@ TKM_ATTN_API int tkm_attn_bwd_stage(int stage, const void* qkv, const void* o, c
                                     int S, int Hq, int Hkv, int D, float scale, int causal,
                                     int dtype, void* workspace, size_t workspace_bytes,
                                     void* stream) {
+    tkm::t_kernels = 0;
     if (stage < TKM_ATTN_BWD_DELTA || stage > TKM_ATTN_BWD_DQ_DELTA)
         return fail(TKM_ATTN_EINVAL, "unknown backward stage %d", stage);
     tkm::BwdArgs a;
@@ -154,6 +184,22 @@ TKM_ATTN_API const char* tkm_attn_status_string(int status) {
     }
 }
 
-TKM_ATTN_API int tkm_attn_version(void) { return 100; }
+TKM_ATTN_API int tkm_attn_init(void) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(TKM_ATTN_EDEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+    if (tkm::asm_init_current_device() != 0)
+        return fail(TKM_ATTN_EDEVICE, "gfx950 assembly kernels failed to load on device %d (%s)",
+                    dev, tkm::asm_load_error());
+    return TKM_ATTN_OK;
+}
+
+TKM_ATTN_API int tkm_attn_asm_available(void) {
+    return tkm::asm_available_current_device() ? 1 : 0;
+}
+
+TKM_ATTN_API unsigned tkm_attn_last_kernels(void) { return tkm::t_kernels; }
+
+TKM_ATTN_API int tkm_attn_version(void) { return 200; }
 
 }  // extern "C"
