@@ -87,6 +87,23 @@ TKM_ATTN_API int tkm_attn_bwd(const void *qkv, const void *o, const void *dout,
                               int B, int S, int Hq, int Hkv, int D, float scale, int causal,
                               int dtype, void *workspace, size_t workspace_bytes, void *stream);
 
+/* tkm_attn_bwd without a workspace argument and without any allocation: the workspace is a
+ * static device array of TKM_ATTN_NOALLOC_SCRATCH_BYTES (16 MiB) that each GPU holds from
+ * the library's first use on it until the process ends.  No reference counterpart: it is
+ * for callers that cannot allocate (code under graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Results equal tkm_attn_bwd's bit for bit.
+ * Limits: tkm_attn_bwd_workspace_bytes(B, S, Hq) must not exceed the scratch size (about
+ * 1.4 million (batch, head, row) triples; config 5's 524288 fit), else TKM_ATTN_EWORKSPACE
+ * and nothing runs.  Every call on one GPU shares that GPU's array: calls that overlap on
+ * one GPU (other streams, other threads) race, so serialize them.  Nothing needs clearing
+ * between calls (the dQ stage writes all the dK/dV stage reads).  tkm_attn_init sets the
+ * array up per device; call it before capturing, else the first call on a device does. */
+#define TKM_ATTN_NOALLOC_SCRATCH_BYTES (16 << 20)
+TKM_ATTN_API int tkm_attn_bwd_noalloc(const void *qkv, const void *o, const void *dout,
+                                      const float *lse, void *dqkv, const int32_t *kv_len,
+                                      int B, int S, int Hq, int Hkv, int D, float scale,
+                                      int causal, int dtype, void *stream);
+
 /* One stage of tkm_attn_bwd (same arguments), for callers that split the backward across
  * streams or time its kernels separately.  No reference counterpart (the reference backward
  * is a single kernel). */

@@ -124,3 +124,18 @@ def test_header_compiles_as_c():
                        input='#include "tkm_attn.h"\nint main(void){return TKM_ATTN_OK;}\n',
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_noalloc_rejects_beyond_scratch_without_device():
+    """tkm_attn_bwd_noalloc checks its size against the static scratch before it touches the
+    device: a workspace need above 16 MiB fails with TKM_ATTN_EWORKSPACE."""
+    L = attn.lib()
+    L.tkm_attn_bwd_noalloc.restype = ctypes.c_int
+    B, S, Hq = 8, 65536, 4
+    assert L.tkm_attn_bwd_workspace_bytes(B, S, Hq) > 16 << 20
+    rc = L.tkm_attn_bwd_noalloc(P16, P16, P16, P16, P16B, None, B, S, Hq, Hq, 128,
+                                ctypes.c_float(0.088), 1, 0, None)
+    assert rc == EWORKSPACE and b"scratch" in L.tkm_attn_last_error()
+    rc = L.tkm_attn_bwd_noalloc(None, P16, P16, P16, P16B, None, 1, 8, 2, 1, 64,
+                                ctypes.c_float(0.125), 1, 0, None)
+    assert rc == EINVAL  # argument checks also come before any device call

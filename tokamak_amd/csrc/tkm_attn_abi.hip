@@ -5,6 +5,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
+
 #include <hip/hip_runtime.h>
 
 #include "attn_launch.h"
@@ -18,6 +20,18 @@ thread_local unsigned t_kernels = 0;  // kernels launched by this thread's curre
 void note_kernels(unsigned bits) { t_kernels |= bits; }
 }  // namespace tkm
 
+// Backward workspace of tkm_attn_bwd_noalloc: a static device array, one per GPU (each
+// device holds its own copy, at its own address, until the process ends).  Host code never
+// uses the name `scratch` as an address (on the host it is only a stand-in symbol): it uses
+// the per-device address that hipGetSymbolAddress returns, kept in g_scratch_ptr.  Nothing
+// in it needs to start at zero: the dQ stage writes every byte the dK/dV stage reads.
+static __device__ __align__(256) unsigned char scratch[TKM_ATTN_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch` on each device
+}  // namespace
 
 namespace {
 
@@ -115,6 +129,22 @@ int prepare_bwd(tkm::BwdArgs& a, const void* qkv, const void* o, const void* dou
     return TKM_ATTN_OK;
 }
 
+// Resolves the current device's address of `scratch` once (with that device current).
+int scratch_setup(int dev) {
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return fail(TKM_ATTN_EDEVICE, "device %d beyond the %d the scratch table holds", dev,
+                    kMaxScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev]) return TKM_ATTN_OK;
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+        return fail(TKM_ATTN_EDEVICE, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                    hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+    return TKM_ATTN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -147,6 +177,37 @@ TKM_ATTN_API int tkm_attn_bwd(const void* qkv, const void* o, const void* dout, 
     tkm::BwdArgs a;
     int rc = prepare_bwd(a, qkv, o, dout, lse, dqkv, kv_len, B, S, Hq, Hkv, D, scale, causal,
                          dtype, workspace, workspace_bytes, stream);
+    if (rc) return rc;
+    for (int stage : {TKM_ATTN_BWD_DQ_DELTA, TKM_ATTN_BWD_DKDV}) {
+        rc = run_bwd_stage(stage, a);
+        if (rc) return rc;
+    }
+    return TKM_ATTN_OK;
+}
+
+TKM_ATTN_API int tkm_attn_bwd_noalloc(const void* qkv, const void* o, const void* dout,
+                                      const float* lse, void* dqkv, const int32_t* kv_len, int B,
+                                      int S, int Hq, int Hkv, int D, float scale, int causal,
+                                      int dtype, void* stream) {
+    tkm::t_kernels = 0;
+    const size_t need = tkm_attn_bwd_workspace_bytes(B, S, Hq);
+    if (need > (size_t)TKM_ATTN_NOALLOC_SCRATCH_BYTES)
+        return fail(TKM_ATTN_EWORKSPACE,
+                    "tkm_attn_bwd_noalloc: B=%d S=%d Hq=%d needs %zu bytes of scratch, the static "
+                    "scratch holds %d (use tkm_attn_bwd with a workspace)",
+                    B, S, Hq, need, (int)TKM_ATTN_NOALLOC_SCRATCH_BYTES);
+    // Everything that needs no device is checked before the device is touched.
+    int rc = check_bwd_args(qkv, o, dout, lse, dqkv, kv_len, B, S, Hq, Hkv, D, scale, causal, dtype);
+    if (rc) return rc;
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(TKM_ATTN_EDEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+    rc = scratch_setup(dev);  // first call on this device only (tkm_attn_init does it too)
+    if (rc) return rc;
+    void* ws = g_scratch_ptr[dev];
+    tkm::BwdArgs a;
+    rc = prepare_bwd(a, qkv, o, dout, lse, dqkv, kv_len, B, S, Hq, Hkv, D, scale, causal, dtype,
+                     ws, need, stream);
     if (rc) return rc;
     for (int stage : {TKM_ATTN_BWD_DQ_DELTA, TKM_ATTN_BWD_DKDV}) {
         rc = run_bwd_stage(stage, a);
@@ -191,7 +252,7 @@ TKM_ATTN_API int tkm_attn_init(void) {
     if (tkm::asm_init_current_device() != 0)
         return fail(TKM_ATTN_EDEVICE, "gfx950 assembly kernels failed to load on device %d (%s)",
                     dev, tkm::asm_load_error());
-    return TKM_ATTN_OK;
+    return scratch_setup(dev);
 }
 
 TKM_ATTN_API int tkm_attn_asm_available(void) {
