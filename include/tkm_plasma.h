@@ -24,7 +24,8 @@
  *     feeds later ops the wrong input.
  *   - Parameter gradients are reduced without atomics, in a fixed order (bitwise reproducible).
  *   - Twin chains hold pointwise and parameterized pointwise ops only (no norm, no Add).
- *   - Dropout (which needs the step seed and a mask) is not available.
+ *   - The replay also applies Drop from its saved mask; the reference's replay skips Drop
+ *     (src/tkm_codegen.c:478-479), so ops after a Drop would see its input.
  *
  * Kernel arguments are resolved by the caller, as the reference's resolve_arg_ptr does
  * (src/tkm_gpu.cu:1142-1164): tkm_plasma_num_args / tkm_plasma_arg describe the pointer list
@@ -56,6 +57,9 @@ enum {
     TKM_OP_SOFTPLUS,        /* log(1 + exp(x))                                                */
     TKM_OP_SNAKE,           /* x + sin^2(fval x) / fval                                       */
     TKM_OP_ADD,             /* residual: x + branch_in                       (branch tensor)  */
+    TKM_OP_DROP,            /* Drop: keep with probability 1 - fval, scaled by 1 / (1 - fval); the
+                               mask is drawn per channel pair from the node's generator, seeded by
+                               the step seed (registry src/tkm_registry.c:426-434)  (mask, seed) */
     TKM_OP_COUNT
 };
 
@@ -74,7 +78,10 @@ enum {
     TKM_ARG_DBRANCH,        /* [rows][C] 16-bit gradient of the residual input */
     TKM_ARG_DWEIGHT,        /* C floats */
     TKM_ARG_DBETA,          /* C floats */
-    TKM_ARG_DBIAS           /* C floats */
+    TKM_ARG_DBIAS,          /* C floats */
+    TKM_ARG_SAVE_MASK,      /* [rows][C/2] uint16: Drop's keep bits of a channel pair (bit 0 of
+                               byte 0: even channel, byte 1: odd channel) */
+    TKM_ARG_SEED            /* one uint32: the step seed (advanced by the runtime's SGD) */
 };
 
 /* Accumulation flags of tkm_plasma_bwd (the reference: a plain group accumulates din, a twin
@@ -86,6 +93,10 @@ enum { TKM_PLASMA_ACC_DIN = 1, TKM_PLASMA_ACC_PARAMS = 2, TKM_PLASMA_ACC_BRANCH 
 typedef struct tkm_plasma_node {
     int op;                 /* TKM_OP_* */
     float fval;             /* the op's constant (registry default if unsure) */
+    int rng_type;           /* Drop: generator, the TkmRngType values 1..4 (xorshift32,
+                               wang_xorshift32, pcg32, philox); 0 = wang_xorshift32 */
+    int node_id;            /* Drop: the graph node id; the generator is seeded with
+                               step_seed ^ (node_id * 19937 + 1) (src/tkm_codegen.c:310-313) */
 } tkm_plasma_node;
 
 typedef struct tkm_plasma_desc {

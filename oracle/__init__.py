@@ -63,6 +63,10 @@ def lib():
         L.pr_op_fwd.restype = ctypes.c_double
         L.pr_op_grad.argtypes = [ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_double, _f64p]
         L.pr_op_grad.restype = ctypes.c_double
+        L.pr_rng_u32.argtypes = [ctypes.c_int, ctypes.c_uint, ctypes.c_uint, ctypes.c_int,
+                                 ctypes.POINTER(ctypes.c_uint)]
+        L.pr_drop_keep.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_float, ctypes.POINTER(ctypes.c_ubyte)]
         _lib = L
     return _lib
 
@@ -252,10 +256,31 @@ class _PrNode(ctypes.Structure):
 
 class _PrParams(ctypes.Structure):
     _fields_ = [("w", ctypes.POINTER(_f32p)), ("beta", ctypes.POINTER(_f32p)),
-                ("bias", ctypes.POINTER(_f32p)), ("branch", ctypes.POINTER(_f32p))]
+                ("bias", ctypes.POINTER(_f32p)), ("branch", ctypes.POINTER(_f32p)),
+                ("keep", ctypes.POINTER(ctypes.POINTER(ctypes.c_ubyte)))]
 
 
-PR_W, PR_BETA, PR_BIAS, PR_NORM, PR_BRANCH = 1, 2, 4, 8, 16
+PR_W, PR_BETA, PR_BIAS, PR_NORM, PR_BRANCH, PR_MASK = 1, 2, 4, 8, 16, 32
+
+
+def rng_u32(rng_type: int, seed: int, idx: int, n: int) -> np.ndarray:
+    """n draws of the prelude's generator `rng_type` (1..4) after rng_init(seed, idx)."""
+    out = np.zeros(n, np.uint32)
+    rc = lib().pr_rng_u32(rng_type, seed & 0xFFFFFFFF, idx & 0xFFFFFFFF, n,
+                          out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint)))
+    if rc:
+        raise ValueError("pr_rng_u32 rejected its arguments")
+    return out
+
+
+def drop_keep(rows: int, C: int, step_seed: int, node_id: int, rng_type: int, p: float) -> np.ndarray:
+    """Drop's keep bits [rows][C] (uint8 0/1) for a step seed, node and generator."""
+    keep = np.zeros((rows, C), np.uint8)
+    rc = lib().pr_drop_keep(rows, C, step_seed & 0xFFFFFFFF, node_id, rng_type, p,
+                            keep.ctypes.data_as(ctypes.POINTER(ctypes.c_ubyte)))
+    if rc:
+        raise ValueError("pr_drop_keep rejected its arguments")
+    return keep
 
 
 def plasma_flags(op: int) -> int:
@@ -292,6 +317,16 @@ def _params(nodes, params):
         arr, kp = _ptr_array(n, lambda k, f=field: params.get((f, k)))
         keep += kp + [arr]
         setattr(P, field, ctypes.cast(arr, ctypes.POINTER(_f32p)))
+    _u8p = ctypes.POINTER(ctypes.c_ubyte)
+    karr = (_u8p * max(n, 1))()
+    for k in range(n):
+        m = params.get(("keep", k))
+        if m is not None:
+            m = np.ascontiguousarray(m, dtype=np.uint8)
+            keep.append(m)
+            karr[k] = m.ctypes.data_as(_u8p)
+    keep.append(karr)
+    P.keep = ctypes.cast(karr, ctypes.POINTER(_u8p))
     return P, keep
 
 

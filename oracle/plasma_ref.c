@@ -12,7 +12,9 @@
  *   twin (gated) groups               src/tkm_codegen.c:509-515, 548-584
  * Norm statistics (F7): sums over aligned 64-channel groups when C > 64 (the whole row when
  * C <= 64), divided by C.  Deliberate differences: istd per (row, group) (the reference keeps
- * group 0's value per row); a residual Add is applied in the replay (the reference skips it).
+ * group 0's value per row); a residual Add and a Drop are applied in the replay (the reference
+ * skips both, src/tkm_codegen.c:478-479).  Drop (registry src/tkm_registry.c:426-434) takes
+ * its keep bits from pr_drop_keep, which restates the prelude's generators.
  *
  * Arithmetic in double from the rounded inputs; outputs rounded once to the storage type.
  * dtype: 0 fp16, 1 bf16, 2 fp32.
@@ -24,7 +26,9 @@
 #include "plasma_ref.h"
 #include "qkv_prep_ref.h"
 
-enum { F_W = 1, F_BETA = 2, F_BIAS = 4, F_NORM = 8, F_BRANCH = 16 };
+#include <stdint.h>
+
+enum { F_W = 1, F_BETA = 2, F_BIAS = 4, F_NORM = 8, F_BRANCH = 16, F_MASK = 32 };
 
 static int op_flags(int op) {
     switch (op) {
@@ -34,11 +38,111 @@ static int op_flags(int op) {
         case PR_L2NORM: return F_NORM;
         case PR_LAYERSCALE: case PR_DYT: case PR_PRELU: case PR_XATLU: return F_W;
         case PR_ADD: return F_BRANCH;
+        case PR_DROP: return F_MASK;
         default: return 0;
     }
 }
 
 int pr_op_flags(int op) { return op >= 0 && op < PR_OP_COUNT ? op_flags(op) : -1; }
+
+/* ---- the prelude's generators (reference src/tkm_gpu.cu:751-800), restated ---------- */
+typedef struct {
+    int type;
+    uint32_t s;                 /* xorshift32 state */
+    uint64_t state, inc;        /* PCG32 */
+    uint32_t ctr, key, sub;     /* counter generator */
+} pr_rng;
+
+static uint32_t xorshift32(uint32_t x) {  /* Marsaglia's (13, 17, 5) */
+    x ^= x << 13;
+    x ^= x >> 17;
+    x ^= x << 5;
+    return x;
+}
+
+static uint32_t pcg_step(pr_rng *r) {      /* PCG32 XSH-RR (O'Neill) */
+    const uint64_t old = r->state;
+    r->state = old * 6364136223846793005ULL + r->inc;
+    const uint32_t xsh = (uint32_t)(((old >> 18u) ^ old) >> 27u), rot = (uint32_t)(old >> 59u);
+    return (xsh >> rot) | (xsh << ((32u - rot) & 31u));
+}
+
+static void rng_init(pr_rng *r, int type, uint32_t seed, uint32_t idx) {
+    memset(r, 0, sizeof *r);
+    r->type = type;
+    switch (type) {
+        case 1: {
+            const uint32_t x = seed ^ (idx * 0x9E3779B9u + 0x7F4A7C15u);
+            r->s = x ? x : 1u;
+            break;
+        }
+        case 3:   /* pcg32_srandom(seed ^ 0x853C49E6748FEA9B, idx) */
+            r->inc = ((uint64_t)idx << 1u) | 1u;
+            (void)pcg_step(r);
+            r->state += (uint64_t)seed ^ 0x853C49E6748FEA9BULL;
+            (void)pcg_step(r);
+            break;
+        case 4:
+            r->ctr = idx;
+            r->key = seed;
+            r->sub = 0;
+            break;
+        default: {  /* Thomas Wang's 32-bit integer hash of seed ^ idx */
+            r->type = 2;
+            uint32_t k = seed ^ idx;
+            k = ~k + (k << 18);
+            k ^= k >> 31;
+            k = (k + (k << 2)) + (k << 4);
+            k ^= k >> 11;
+            k += k << 6;
+            k ^= k >> 22;
+            r->s = k ? k : 1u;
+        }
+    }
+}
+
+static uint32_t rng_next(pr_rng *r) {
+    if (r->type == 3) return pcg_step(r);
+    if (r->type == 4) {
+        uint32_t c0 = r->ctr, c1 = r->sub++, k0 = r->key;
+        for (int i = 0; i < 7; i++) {
+            const uint64_t prod = (uint64_t)0xD2511F53u * c0;
+            const uint32_t hi = (uint32_t)(prod >> 32), lo = (uint32_t)prod;
+            c0 = hi ^ c1 ^ k0;
+            c1 = lo;
+            k0 += 0x9E3779B9u;
+        }
+        return c0;
+    }
+    return r->s = xorshift32(r->s);
+}
+
+int pr_rng_u32(int type, unsigned seed, unsigned idx, int n, unsigned *out) {
+    if (!out || n < 0 || type < 0 || type > 4) return -1;
+    pr_rng r;
+    rng_init(&r, type, seed, idx);
+    for (int i = 0; i < n; ++i) out[i] = rng_next(&r);
+    return 0;
+}
+
+int pr_drop_keep(int rows, int C, unsigned step_seed, int node_id, int rng_type, float p, unsigned char *keep) {
+    if (!keep || rows < 0 || C <= 0 || C % 2 || !(p >= 0.0f && p < 1.0f) || rng_type < 0 || rng_type > 4) return -1;
+    const float kp = 1.0f - p;
+    const uint32_t sd = (uint32_t)step_seed ^ ((uint32_t)node_id * 19937u + 1u);
+    for (int r = 0; r < rows; ++r)
+        for (int t = 0; t < C / 2; ++t) {
+            pr_rng g;
+            rng_init(&g, rng_type, sd, (uint32_t)((size_t)r * (C / 2) + t));
+            for (int e = 0; e < 2; ++e) {
+                const float u = (float)(rng_next(&g) >> 8) * (1.0f / 16777216.0f);
+                keep[(size_t)r * C + 2 * t + e] = u < kp;
+            }
+        }
+    return 0;
+}
+
+/* Drop's scale 1 / (1 - p), as the fp32 constant of the registry's snippet */
+static double drop_scale(double p) { return (double)(1.0f / (1.0f - (float)p)); }
 
 static double sigm(double x) { return 1.0 / (1.0 + exp(-x)); }
 
@@ -154,6 +258,9 @@ static void apply_node(const pr_node *n, int k, double *v, int C, int r, const p
         norm_fwd(n->op, n->fval, v, C, P->w[k], P->beta[k], dtype, xhat[k] + (size_t)r * C, istd[k] + (size_t)r * NG);
     } else if (f & F_BRANCH) {
         for (int c = 0; c < C; ++c) v[c] += P->branch[k][(size_t)r * C + c];
+    } else if (f & F_MASK) {
+        const double ikp = drop_scale(n->fval);
+        for (int c = 0; c < C; ++c) v[c] = P->keep[k][(size_t)r * C + c] ? v[c] * ikp : 0.0;
     } else {
         for (int c = 0; c < C; ++c)
             v[c] = pr_op_fwd(n->op, n->fval, v[c], (f & F_W) ? P->w[k][c] : 0.0, (f & F_BIAS) ? P->bias[k][c] : 0.0);
@@ -230,6 +337,9 @@ int pr_bwd(const float *dout, const float *in, int rows, int C, int twin, const 
                            : (n->op == PR_RMSNORM ? xh[c] * (double)P->w[k][c] : xh[c]);
             } else if (f & F_BRANCH) {
                 for (int c = 0; c < C; ++c) x[c] += P->branch[k][(size_t)r * C + c];
+            } else if (f & F_MASK) {   /* replayed from the saved keep bits */
+                const double ikp = drop_scale(n->fval);
+                for (int c = 0; c < C; ++c) x[c] = P->keep[k][(size_t)r * C + c] ? x[c] * ikp : 0.0;
             } else {
                 for (int c = 0; c < C; ++c)
                     x[c] = pr_op_fwd(n->op, n->fval, x[c], (f & F_W) ? P->w[k][c] : 0.0, (f & F_BIAS) ? P->bias[k][c] : 0.0);
@@ -281,6 +391,9 @@ int pr_bwd(const float *dout, const float *in, int rows, int C, int twin, const 
                         const double prev = (acc_flags & 4) ? dbranch[k][i] : 0.0;
                         dbranch[k][i] = (float)qp_round(prev + gg[c], dtype);
                     }
+                } else if (f & F_MASK) {
+                    const double ikp = drop_scale(n->fval);
+                    for (int c = 0; c < C; ++c) gg[c] *= P->keep[k][(size_t)r * C + c] ? ikp : 0.0;
                 } else {
                     for (int c = 0; c < C; ++c) {
                         double dwe;

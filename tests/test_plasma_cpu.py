@@ -27,24 +27,24 @@ from tokamak_amd import plasma, prep
 
 RNG = np.random.default_rng(77)
 OPS = plasma.OPS
-POINTWISE = [n for n in plasma.OP_NAMES if n not in ("RMSNorm", "LN", "BN", "L2Norm", "Add")]
+POINTWISE = [n for n in plasma.OP_NAMES if n not in ("RMSNorm", "LN", "BN", "L2Norm", "Add", "Drop")]
 
 
 # ---- op table ----------------------------------------------------------------------------
 
 def test_op_numbering_and_flags_agree():
-    assert len(plasma.OP_NAMES) == 29
+    assert len(plasma.OP_NAMES) == 30
     want = {"Bias": oracle.PR_BIAS, "RMSNorm": oracle.PR_W | oracle.PR_NORM,
             "LN": oracle.PR_W | oracle.PR_BETA | oracle.PR_NORM, "BN": oracle.PR_W | oracle.PR_BETA | oracle.PR_NORM,
             "L2Norm": oracle.PR_NORM, "LayerScale": oracle.PR_W, "DyT": oracle.PR_W, "PReLU": oracle.PR_W,
-            "xATLU": oracle.PR_W, "Add": oracle.PR_BRANCH}
+            "xATLU": oracle.PR_W, "Add": oracle.PR_BRANCH, "Drop": oracle.PR_MASK}
     for name, code in OPS.items():
         assert oracle.plasma_flags(code) == want.get(name, 0), name
     # defaults of the registry (src/tkm_registry.c)
     L = plasma.lib()
     defaults = {"BN": 1e-2, "LN": 1e-5, "RMSNorm": 1e-5, "L2Norm": 1e-5, "LeakyReLU": 0.01, "ELU": 1.0,
                 "SwishBeta": 1.5, "Sin": 1.0, "SoftCap": 30.0, "Clamp": 6.0, "Scale": 1.0, "LayerScale": 1e-4,
-                "DyT": 0.5, "PReLU": 0.25, "xATLU": 0.5, "Snake": 1.0, "SiLU": 0.0}
+                "DyT": 0.5, "PReLU": 0.25, "xATLU": 0.5, "Snake": 1.0, "SiLU": 0.0, "Drop": 0.1}
     for name, v in defaults.items():
         assert L.tkm_plasma_default_fval(OPS[name]) == pytest.approx(v, rel=1e-7), name
 
@@ -320,7 +320,10 @@ def test_emitted_chain_compiles(c, dtype, tmp_path):
 
 
 @pytest.mark.parametrize("kw,msg", [
-    (dict(channels=20, chain=["SiLU"]), "multiple of 8"),
+    (dict(channels=21, chain=["SiLU"]), "even"),
+    (dict(channels=20, chain=["RMSNorm"]), "multiple of 8"),
+    (dict(channels=20, chain=["SiLU", ("Drop", 1.0, 3, 5)]), "Drop needs"),
+    (dict(channels=20, chain=["Bias", "SiLU", ("Drop", 0.2, 3, 5), "Add"]), None),
     (dict(channels=64, chain=["SiLU"] * 9), "chain lengths"),
     (dict(channels=64, twin=True, left=["RMSNorm"]), "twin gate"),
     (dict(channels=64, twin=True, right=["Add"]), "twin gate"),

@@ -3,6 +3,7 @@
 #define TKM_PLASMA_INTERNAL_H
 
 #include "tkm_plasma.h"
+#include "tkm_codegen_internal.h"
 #include "tkm_prep_internal.h"
 
 #ifdef __cplusplus
@@ -19,7 +20,7 @@ typedef struct {
 } tkm_plasma_argd;
 
 typedef struct {
-    int C, CH;          /* channels, 8-channel chunks per row */
+    int C, CW, CH;      /* channels, channels per lane chunk (8, or 2 when C % 8 != 0), chunks per row */
     int L, RW, XB;      /* lanes per row, rows per wave, blocks across a row */
     int NGL, NG;        /* lanes per norm group, norm groups per row */
     int n_nodes;
@@ -30,6 +31,15 @@ typedef struct {
 
 TKM_HIDDEN int tkm_plasma_check_desc(const tkm_plasma_desc *d);
 TKM_HIDDEN void tkm_plasma_geometry(const tkm_plasma_desc *d, tkm_plasma_geom *g);
+
+/* Internal argument list of the forward (pass 0) or backward (pass 1) kernel: pointer
+ * arguments, then the scalars (forward: rows; backward: part, rows, band, acc_flags).
+ * `out` holds TKM_KPLAN_MAX entries; returns the count. */
+TKM_HIDDEN int tkm_plasma_need(const tkm_plasma_desc *d, int pass, tkm_kparam *out);
+/* Appends the group's constants and kernels to s (no prelude); plans may be NULL (internal
+ * order); `scoped` confines helpers and macros so that many groups share one source. */
+TKM_HIDDEN int tkm_plasma_emit(tkm_sbuf *s, const tkm_plasma_desc *d, const tkm_kplan *fwd_plan,
+                               const tkm_kplan *bwd_plan, int scoped);
 
 #ifdef __cplusplus
 }

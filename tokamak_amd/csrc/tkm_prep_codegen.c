@@ -26,30 +26,12 @@
 #include <string.h>
 
 #include "tkm_prep.h"
+#include "tkm_codegen_internal.h"
+#include "tkm_plasma.h"
 #include "tkm_prep_internal.h"
 
-typedef struct {
-    char *buf;
-    size_t len, cap;
-    int failed;
-} sbuf;
-
-static void sb_add(sbuf *s, const char *fmt, ...) {
-    if (s->failed) return;
-    for (;;) {
-        va_list ap;
-        va_start(ap, fmt);
-        int n = vsnprintf(s->buf + s->len, s->cap - s->len, fmt, ap);
-        va_end(ap);
-        if (n < 0) { s->failed = 1; return; }
-        if ((size_t)n < s->cap - s->len) { s->len += (size_t)n; return; }
-        size_t cap = (s->cap + (size_t)n + 1) * 2;
-        char *nb = (char *)realloc(s->buf, cap);
-        if (!nb) { s->failed = 1; return; }
-        s->buf = nb;
-        s->cap = cap;
-    }
-}
+typedef tkm_sbuf sbuf;
+#define sb_add tkm_sb_add
 
 void tkm_prep_desc_init(tkm_prep_desc *d) {
     if (!d) return;
@@ -206,11 +188,50 @@ static void emit_lane_setup(sbuf *s, const tkm_prep_desc *d, int need_bias) {
     }
 }
 
-static void emit_fwd(sbuf *s, const tkm_prep_desc *d, const tkm_prep_geom *g) {
+/* Internal argument lists of the two kernels (kinds of include/tkm_plasma.h, node 0 = the
+ * qkv_prep node), in the order of the standalone API. */
+int tkm_prep_need(int pass, tkm_kparam *out) {
+    static const tkm_kparam fwd[] = {
+        {TKM_ARG_IN, -1, "const uint4 *", "in"},
+        {TKM_ARG_OUT, -1, "uint4 *", "out"},
+        {TKM_ARG_BIAS, 0, "const float4 *__restrict__", "bias"},
+        {TKM_ARG_WEIGHT, 0, "const float4 *__restrict__", "gamma"},
+        {TKM_ARG_SAVE_ISTD, 0, "float *__restrict__", "save_istd"},
+        {TKM_ARG_SAVE_XHAT, 0, "uint4 *__restrict__", "save_xhat"},
+        {TKM_KP_ROWS, -1, "int", "rows"}};
+    static const tkm_kparam bwd[] = {
+        {TKM_ARG_DOUT, -1, "const uint4 *__restrict__", "dout"},
+        {TKM_ARG_DIN, -1, "uint4 *__restrict__", "din"},
+        {TKM_ARG_SAVE_XHAT, 0, "const uint4 *__restrict__", "save_xhat"},
+        {TKM_ARG_SAVE_ISTD, 0, "const float *__restrict__", "save_istd"},
+        {TKM_ARG_WEIGHT, 0, "const float4 *__restrict__", "gamma"},
+        {TKM_KP_PART, -1, "float *__restrict__", "part"},
+        {TKM_KP_ROWS, -1, "int", "rows"},
+        {TKM_KP_BAND, -1, "int", "band"},
+        {TKM_KP_ACC, -1, "int", "accumulate"}};
+    const tkm_kparam *src = pass ? bwd : fwd;
+    const int n = pass ? (int)(sizeof bwd / sizeof bwd[0]) : (int)(sizeof fwd / sizeof fwd[0]);
+    for (int i = 0; i < n; ++i) out[i] = src[i];
+    return n;
+}
+
+static int emit_header(sbuf *s, const tkm_prep_desc *d, int pass, const tkm_kplan *plan) {
+    tkm_kparam need[16];
+    const int n = tkm_prep_need(pass, need);
+    tkm_kplan def;
+    if (!plan) {
+        def.n = 0;
+        for (int i = 0; i < n; ++i) tkm_kplan_add(&def, need[i].kind, need[i].node, need[i].decl, need[i].name);
+        plan = &def;
+    }
+    sb_add(s, "extern \"C\" __global__ __launch_bounds__(256) void tkm_plasma_%s_g%d", pass ? "bwd" : "fwd",
+           d->group_id);
+    return tkm_emit_plan_params(s, plan, need, n);
+}
+
+static int emit_fwd(sbuf *s, const tkm_prep_desc *d, const tkm_prep_geom *g, const tkm_kplan *plan) {
     const char *k = kind(d);
-    sb_add(s, "extern \"C\" __global__ __launch_bounds__(256) void tkm_plasma_fwd_g%d(\n", d->group_id);
-    sb_add(s, "    const uint4 *in, uint4 *out, const float4 *__restrict__ bias, const float4 *__restrict__ gamma,\n");
-    sb_add(s, "    float *__restrict__ save_istd, uint4 *__restrict__ save_xhat, int rows)\n{\n");
+    if (emit_header(s, d, 0, plan)) return -1;
     if (!d->has_qknorm) sb_add(s, "    (void)gamma; (void)save_istd; (void)save_xhat;\n");
     emit_lane_setup(s, d, 1);
     sb_add(s, "    const int r0 = blockIdx.y * %d + wave;\n", 4 * TKM_PREP_FWD_RPW);
@@ -249,15 +270,13 @@ static void emit_fwd(sbuf *s, const tkm_prep_desc *d, const tkm_prep_geom *g) {
     }
     sb_add(s, "        if (ok) out[(size_t)r * TKM_CH + ch] = tkm_pack_%s(v);\n", k);
     sb_add(s, "    }\n}\n\n");
+    return 0;
 }
 
-static void emit_bwd(sbuf *s, const tkm_prep_desc *d, const tkm_prep_geom *g) {
+static int emit_bwd(sbuf *s, const tkm_prep_desc *d, const tkm_prep_geom *g, const tkm_kplan *plan) {
     const char *k = kind(d);
     const int B = TKM_PREP_BWD_BATCH;
-    sb_add(s, "extern \"C\" __global__ __launch_bounds__(256) void tkm_plasma_bwd_g%d(\n", d->group_id);
-    sb_add(s, "    const uint4 *__restrict__ dout, uint4 *__restrict__ din, const uint4 *__restrict__ save_xhat,\n");
-    sb_add(s, "    const float *__restrict__ save_istd, const float4 *__restrict__ gamma, float *__restrict__ part,\n");
-    sb_add(s, "    int rows, int band, int accumulate)\n{\n");
+    if (emit_header(s, d, 1, plan)) return -1;
     if (!d->has_qknorm) sb_add(s, "    (void)save_xhat; (void)save_istd; (void)gamma;\n");
     emit_lane_setup(s, d, 0);
     sb_add(s, "    float adb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};\n");
@@ -362,20 +381,33 @@ static void emit_bwd(sbuf *s, const tkm_prep_desc *d, const tkm_prep_geom *g) {
         sb_add(s, "    float *dst = dbias + c;\n");
     sb_add(s, "    *dst = accumulate ? *dst + t : t;\n");
     sb_add(s, "}\n");
+    return 0;
+}
+
+int tkm_prep_emit(tkm_sbuf *s, const tkm_prep_desc *d, const tkm_kplan *fwd_plan, const tkm_kplan *bwd_plan,
+                  int scoped) {
+    int rc = tkm_prep_check_desc(d);
+    if (rc) return rc;
+    tkm_prep_geom g;
+    tkm_prep_geometry(d, &g);
+    if (scoped) sb_add(s, "namespace tkm_g%d {\n", d->group_id);
+    emit_constants(s, d, &g);
+    if (emit_fwd(s, d, &g, fwd_plan) || emit_bwd(s, d, &g, bwd_plan))
+        return tkm_set_error(TKM_ATTN_EINVAL, "qkv-prep group %d: a kernel argument is missing from its plan",
+                             d->group_id);
+    if (scoped) {
+        sb_add(s, "}  /* namespace tkm_g%d */\n", d->group_id);
+        sb_add(s, "#undef TKM_CH\n#undef TKM_QKCH\n#undef TKM_NH\n#undef TKM_G\n#undef TKM_S\n#undef TKM_PW\n"
+                  "#undef TKM_C\n\n");
+    }
+    return s->failed ? tkm_set_error(TKM_ATTN_EINVAL, "out of host memory while emitting source") : TKM_ATTN_OK;
 }
 
 char *tkm_prep_source(const tkm_prep_desc *d) {
-    if (tkm_prep_check_desc(d) != TKM_ATTN_OK) return NULL;
-    tkm_prep_geom g;
-    tkm_prep_geometry(d, &g);
     sbuf s = {0};
     sb_add(&s, "%s", tkm_hip_prelude());
-    emit_constants(&s, d, &g);
-    emit_fwd(&s, d, &g);
-    emit_bwd(&s, d, &g);
-    if (s.failed) {
+    if (tkm_prep_emit(&s, d, NULL, NULL, 0) != TKM_ATTN_OK) {
         free(s.buf);
-        tkm_set_error(TKM_ATTN_EINVAL, "out of host memory while emitting source");
         return NULL;
     }
     return s.buf;

@@ -19,10 +19,10 @@ HEADER = os.path.join(attn.ROOT, "include", "tkm_plasma.h")
 
 OP_NAMES = ["Bias", "RMSNorm", "LN", "BN", "L2Norm", "SiLU", "ReLU", "ReLU2", "LeakyReLU", "ELU", "GELU",
             "Mish", "HardSwish", "HardSigmoid", "Tanh", "Sigmoid", "SwishBeta", "Sin", "CosGate", "SoftCap",
-            "Clamp", "Scale", "LayerScale", "DyT", "PReLU", "xATLU", "Softplus", "Snake", "Add"]
+            "Clamp", "Scale", "LayerScale", "DyT", "PReLU", "xATLU", "Softplus", "Snake", "Add", "Drop"]
 OPS = {n: i for i, n in enumerate(OP_NAMES)}
 ARG_KINDS = ["in", "out", "dout", "din", "w", "beta", "bias", "xhat", "istd", "branch", "dbranch",
-             "dw", "dbeta", "dbias"]
+             "dw", "dbeta", "dbias", "mask", "seed"]
 ACC_DIN, ACC_PARAMS, ACC_BRANCH = 1, 2, 4
 MAX_NODES = 8
 
@@ -32,7 +32,7 @@ _configured = False
 
 
 class Node(ctypes.Structure):
-    _fields_ = [("op", _i), ("fval", ctypes.c_float)]
+    _fields_ = [("op", _i), ("fval", ctypes.c_float), ("rng_type", _i), ("node_id", _i)]
 
 
 class Desc(ctypes.Structure):
@@ -79,11 +79,15 @@ def _check(fn, rc):
 
 
 def _nodes(chain):
+    """(op, fval, rng_type, node_id) per item; an item is a name, (name, fval) or, for Drop,
+    (name, fval, rng_type, node_id)."""
     out = []
     for item in chain:
-        name, fval = (item, None) if isinstance(item, str) else item
+        item = (item,) if isinstance(item, str) else tuple(item)
+        name, fval = item[0], (item[1] if len(item) > 1 else None)
+        rng, node = (item[2], item[3]) if len(item) > 3 else (0, 0)
         op = OPS[name]
-        out.append((op, lib().tkm_plasma_default_fval(op) if fval is None else float(fval)))
+        out.append((op, lib().tkm_plasma_default_fval(op) if fval is None else float(fval), int(rng), int(node)))
     return out
 
 
@@ -98,8 +102,8 @@ def make_desc(channels, chain=(), twin=False, left=(), right=(), dtype="f16", gr
             raise ValueError(f"at most {MAX_NODES} ops per chain")
         setattr(d, count, len(nodes))
         arr = getattr(d, field)
-        for k, (op, fv) in enumerate(nodes):
-            arr[k].op, arr[k].fval = op, fv
+        for k, (op, fv, rng, node) in enumerate(nodes):
+            arr[k].op, arr[k].fval, arr[k].rng_type, arr[k].node_id = op, fv, rng, node
     return d
 
 
