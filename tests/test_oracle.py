@@ -375,3 +375,46 @@ def test_checks_catch_planted_mistakes():
     # backward fed with LSE off by one unit
     d7 = oracle.bwd(inp["qkv"], o, inp["dout"], lse + 1.0, B, S, Hq, Hkv, D, causal=True, f64=True)
     assert not close(d7, db)
+
+
+# ----------------------------------------------------------------------------- Drop's generators
+def test_drop_xorshift32_known_answer():
+    """Generator 1 is Marsaglia's xorshift32 (13, 17, 5) ("Xorshift RNGs", J. Stat. Softw. 2003):
+    from y = 2463534242 its first output is 723471715.  rng_init(seed, idx) starts it at
+    seed ^ (idx * 0x9E3779B9 + 0x7F4A7C15), so idx 0 and seed = y ^ 0x7F4A7C15 start it at y."""
+    got = oracle.rng_u32(1, 2463534242 ^ 0x7F4A7C15, 0, 3)
+    assert int(got[0]) == 723471715
+    y, want = 2463534242, []
+    for _ in range(3):
+        y ^= (y << 13) & 0xFFFFFFFF
+        y ^= y >> 17
+        y ^= (y << 5) & 0xFFFFFFFF
+        want.append(y)
+    assert [int(v) for v in got] == want
+
+
+def test_drop_pcg32_is_pcg32_srandom():
+    """Generator 3 (the front end's default) is pcg32_srandom(seed ^ 0x853C49E6748FEA9B, idx); the
+    oracle's PCG32 stream is pinned to O'Neill's demo vector above."""
+    for seed, idx in ((0, 0), (1234, 77), (0x13579BDF, 123456)):
+        got = oracle.rng_u32(3, seed, idx, 8)
+        want = oracle.pcg32_sequence(seed ^ 0x853C49E6748FEA9B, idx, 8)
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("rng_type", [1, 2, 3, 4])
+def test_drop_keep_rate_and_pairs(rng_type):
+    """The keep fraction is 1 - p within 5 sigma for every generator (the Wang-hash and
+    counter generators have no published vectors: their bits are parity unpinned beyond this),
+    and the two channels of a pair come from consecutive draws of one stream."""
+    rows, C, p = 256, 64, 0.3
+    keep = oracle.drop_keep(rows, C, 0x13579BDF, 17, rng_type, p)
+    n = keep.size
+    assert abs(keep.mean() - (1 - p)) < 5 * np.sqrt(p * (1 - p) / n)
+    sd = (0x13579BDF ^ (17 * 19937 + 1)) & 0xFFFFFFFF
+    for r, t in ((0, 0), (3, 5), (255, 31)):
+        u = (oracle.rng_u32(rng_type, sd, r * (C // 2) + t, 2) >> 8).astype(np.float64) / 16777216.0
+        assert list(keep[r, 2 * t:2 * t + 2]) == [int(v < 1 - p) for v in u]
+    # another node or step seed gives another mask
+    assert not np.array_equal(keep, oracle.drop_keep(rows, C, 0x13579BDF, 18, rng_type, p))
+    assert not np.array_equal(keep, oracle.drop_keep(rows, C, 0x13579BDF + 0x9E3779B9, 17, rng_type, p))

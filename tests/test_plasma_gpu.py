@@ -41,13 +41,19 @@ CHAINS = [
     dict(C=1536, twin=True, left=["SiLU"], right=[], chain=[("Scale", 0.5), "Add"], acc=6),
     dict(C=64, twin=True, left=["Bias", "GELU"], right=["Bias", "LayerScale"], chain=["RMSNorm"], acc=2),
     dict(C=32, twin=True, left=["Sigmoid"], right=["Tanh"], chain=[], acc=0),
+    # a Drop between a gate and a residual add that a norm closes (exotic_llama's group shape)
+    dict(C=512, chain=["Bias", ("DyT", 0.5), ("Drop", 0.1, 3, 131), "Add", "RMSNorm"], acc=7),
+    dict(C=64, twin=True, left=["Bias", ("Drop", 0.2, 1, 7)], right=["SiLU"], chain=[("Drop", 0.3, 4, 9), "LN"], acc=3),
 ]
+
+
+DROP_SEED = 0x2468ACE1
 
 
 def _nodes(c):
     from tokamak_amd import plasma
     def norm(lst):
-        return [(x, None) if isinstance(x, str) else x for x in lst]
+        return [(x, None) if isinstance(x, str) else tuple(x[:2]) for x in lst]
     items = (norm(c["left"]) + norm(c["right"]) + norm(c["chain"])) if c.get("twin") else norm(c["chain"])
     L = plasma.lib()
     return [(plasma.OPS[n], float(L.tkm_plasma_default_fval(plasma.OPS[n])) if fv is None else float(fv))
@@ -63,6 +69,7 @@ def run_chain(dev, c, rows, dtype, seed):
     log(f"[case] plasma C{C} twin={int(twin)} chain={c.get('left', [])}|{c.get('right', [])}|{c['chain']} "
         f"{dtype} rows={rows} acc={acc} seed={seed}")
     nodes = _nodes(c)
+    items = (list(c["left"]) + list(c["right"]) + list(c["chain"])) if twin else list(c["chain"])
     P = plasma.Plasma(C, c["chain"], twin, c.get("left", ()), c.get("right", ()), dtype, group_id=seed)
     rng = np.random.default_rng(seed)
     W = 2 * C if twin else C
@@ -85,6 +92,11 @@ def run_chain(dev, c, rows, dtype, seed):
             p_r, p_b = oracle.round_to(rng.standard_normal((rows, C)).astype(np.float32), dtype)
             params[("dbranch_prev", k)] = p_r
             tens[("dbranch", k)] = to_device(p_b, dtype, dev)
+        if fl & oracle.PR_MASK:
+            _, p, rng_type, node_id = items[k]
+            params[("keep", k)] = oracle.drop_keep(rows, C, DROP_SEED, node_id, rng_type, p)
+            tens[("mask", k)] = torch.zeros(rows * C, dtype=torch.uint8, device=dev)
+            tens[("seed", k)] = torch.from_numpy(np.array([DROP_SEED], np.uint32).view(np.int32)).to(dev)
         if fl & oracle.PR_NORM:
             tens[("xhat", k)] = torch.empty((rows, C), dtype=t16, device=dev)
             tens[("istd", k)] = torch.empty((rows, NG), dtype=torch.float32, device=dev)
@@ -99,7 +111,7 @@ def run_chain(dev, c, rows, dtype, seed):
 
     P.fwd(tens, rows)
     torch.cuda.synchronize()
-    plain = {k: v for k, v in params.items() if k[0] in ("w", "beta", "bias", "branch")}
+    plain = {k: v for k, v in params.items() if k[0] in ("w", "beta", "bias", "branch", "keep")}
     ro, rxh, ris = oracle.plasma_fwd(x_r, rows, C, nodes, plain, twin, nl, nr, dtype)
     check16("out", from_device(tens["out"]), ro, dtype)
     gxh, gis = {}, {}
@@ -169,4 +181,47 @@ def test_plasma_deterministic(gpu):
         runs.append({k: v.clone() for k, v in t.items()})
     for k in runs[0]:
         assert torch.equal(runs[0][k], runs[1][k]), k
+    P.close()
+
+
+@pytest.mark.parametrize("rng_type", [1, 2, 3, 4])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_plasma_drop_parity(gpu, rng_type, dtype):
+    """Drop inside a chain (Bias, Drop, Add): the keep bits the kernel draws from the step seed,
+    the node id and the generator equal oracle.drop_keep's bit for bit (a flipped bit moves an
+    element by x / (1 - p), far outside the 2-ulp bar); the backward reuses the saved mask."""
+    import torch
+    from tokamak_amd import plasma
+    C, rows, p, node, seed = 192, 333, 0.25, 41, 0x13579BDF
+    log(f"[case] plasma Drop rng_type={rng_type} {dtype} C{C} rows={rows}")
+    P = plasma.Plasma(C, ["Bias", ("Drop", p, rng_type, node), "Add"], dtype=dtype, group_id=rng_type)
+    assert ("mask", 1) in P.fwd_args and ("seed", 1) in P.fwd_args and ("mask", 1) in P.bwd_args
+    rng = np.random.default_rng(rng_type)
+    x_r, x_b = oracle.round_to(rng.standard_normal((rows, C)).astype(np.float32), dtype)
+    b_r, b_b = oracle.round_to(rng.standard_normal((rows, C)).astype(np.float32), dtype)
+    g_r, g_b = oracle.round_to(rng.standard_normal((rows, C)).astype(np.float32), dtype)
+    bias = (0.2 * rng.standard_normal(C)).astype(np.float32)
+    t16 = torch.float16 if dtype == "f16" else torch.bfloat16
+    tens = {"in": to_device(x_b, dtype, gpu), "dout": to_device(g_b, dtype, gpu), ("branch", 2): to_device(b_b, dtype, gpu),
+            ("bias", 0): torch.from_numpy(bias).to(gpu), ("mask", 1): torch.zeros(rows * C, dtype=torch.uint8, device=gpu),
+            ("seed", 1): torch.from_numpy(np.array([seed], np.uint32).view(np.int32)).to(gpu),
+            "out": torch.empty((rows, C), dtype=t16, device=gpu), "din": torch.empty((rows, C), dtype=t16, device=gpu),
+            ("dbranch", 2): torch.zeros((rows, C), dtype=t16, device=gpu), ("dbias", 0): torch.zeros(C, device=gpu)}
+    P.fwd(tens, rows)
+    P.bwd(tens, rows, 0)
+    torch.cuda.synchronize()
+    keep = oracle.drop_keep(rows, C, seed, node, rng_type, p)
+    nodes = [(plasma.OPS["Bias"], 0.0), (plasma.OPS["Drop"], p), (plasma.OPS["Add"], 0.0)]
+    params = {("bias", 0): bias, ("keep", 1): keep, ("branch", 2): b_r}
+    ro, _, _ = oracle.plasma_fwd(x_r, rows, C, nodes, params, dtype=dtype)
+    check16("out", from_device(tens["out"]), ro, dtype)
+    din, dbr, grads = oracle.plasma_bwd(g_r, x_r, rows, C, nodes, params, {}, {}, dtype=dtype, acc_flags=0)
+    check16("din", from_device(tens["din"]), din, dtype)
+    check16("dbranch2", from_device(tens[("dbranch", 2)]), dbr[2], dtype)
+    got = tens[("dbias", 0)].cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(got - grads[("dbias", 0)]) <= 1e-4 * np.abs(grads[("dbias", 0)]) + 1e-6 * rows)
+    # the dropped elements: din is exactly zero where keep is 0
+    assert np.all(from_device(tens["din"])[keep == 0] == 0)
+    frac = keep.mean()
+    log(f"    kept {frac:.4f} (1 - p = {1 - p})")
     P.close()
