@@ -245,7 +245,7 @@ def _chained_case(name, dtype):
 
 @pytest.mark.parametrize("name,dtype", [("llama_small", "f16"), ("llama_small", "bf16"), ("exotic_llama", "f16")])
 def test_step_matches_chained_oracle(gpu, name, dtype):
-    """One step at lr 0.05 from the same weights on both sides: the loss within 2e-3 (relative),
+    """One step at lr 0.05 from the same weights on both sides: the loss within 1e-4 (relative),
     the input gradient within 2e-2 of its largest magnitude, and every learnable tensor's
     update (new - old, fp32 masters) within 3e-2 of that tensor's largest update.  The oracle
     stores every arena slot in the same 16-bit type, so what remains is summation order and
@@ -263,7 +263,7 @@ def test_step_matches_chained_oracle(gpu, name, dtype):
     ref = gs.step(x, y, lr)
     rel = abs(loss - ref["loss"]) / abs(ref["loss"])
     log(f"    loss gpu {loss:.6f} oracle {ref['loss']:.6f} rel {rel:.2e}")
-    assert rel < 2e-3
+    assert rel < 1e-4
     r0 = ref["grad"][0]
     e = np.abs(g0 - r0).max() / np.abs(r0).max()
     log(f"    input gradient: max |gpu - oracle| / max |oracle| = {e:.2e}")
@@ -280,3 +280,73 @@ def test_step_matches_chained_oracle(gpu, name, dtype):
     log(f"    updates of {len(w0)} tensors: worst relative error {worst[0]:.2e} at {worst[1]}")
     rt.close()
 
+
+
+def _epoch_lr(peak, min_ratio, step, total, warmup):
+    """src/tkm_gpu.cu:1793-1800: linear warm-up, then cosine decay to min_ratio of the peak."""
+    w = (step + 1) / warmup if (warmup > 0 and step < warmup) else 1.0
+    prog = min(step / (total - 1), 1.0) if total > 1 else 1.0
+    return peak * w * (min_ratio + (1 - min_ratio) * 0.5 * (1 + math.cos(math.pi * prog)))
+
+
+@pytest.mark.parametrize("schedule", ["constant", "warmup_cosine"])
+def test_resident_epoch_matches_steps(gpu, schedule):
+    """tkm_runtime_train_epoch over a device-resident dataset (src/tkm_gpu.cu:1767-1997) equals
+    the same batches stepped one at a time in sample order `order`: at a constant rate the weights
+    agree bit for bit and the epoch's mean loss is the mean of the step losses; under warm-up and
+    cosine decay the rates are fp32 on the device and fp64 here, so within 1e-5.  The samples past
+    the last full batch are left out, as the reference does."""
+    import ctypes
+    from tokamak_amd import runtime as R
+    log(f"[case] fused_check: resident epoch, {schedule} rate")
+    L = R.lib()
+    B, C, nb = 4, 8, 6
+    rng = np.random.default_rng(21)
+    N = B * nb + 3
+    images = rng.standard_normal((N, C)).astype(np.float32)
+    labels = rng.integers(0, 4, N).astype(np.uint8)
+    order = rng.permutation(N).astype(np.uint32)
+    peak, min_ratio, warm = (0.05, 1.0, 0) if schedule == "constant" else (0.05, 0.2, 2)
+    a = R.Runtime(graph("fused_check"), init_seed=5)
+    b = R.Runtime(graph("fused_check"), init_seed=5)
+    ds = L.tkm_dataset_create(a.rt, images.ctypes.data, labels.ctypes.data, N)
+    assert ds and L.tkm_dataset_is_resident(ds)
+    avg = ctypes.c_float()
+    assert L.tkm_runtime_train_epoch(a.rt, ds, order.ctypes.data, peak, min_ratio, 0, nb, warm, ctypes.byref(avg))
+    losses = []
+    for k in range(nb):
+        idx = order[k * B:(k + 1) * B]
+        losses.append(b.step(images[idx].ravel(), labels[idx], _epoch_lr(peak, min_ratio, k, nb, warm)))
+    wa, wb = R.parse_weights(a.save_weights()), R.parse_weights(b.save_weights())
+    log(f"    epoch mean loss {avg.value:.6f}, steps {np.mean(losses):.6f}")
+    assert all(np.isfinite(losses))
+    if schedule == "constant":
+        assert all(np.array_equal(x, y) for x, y in zip(wa, wb))
+        assert avg.value == pytest.approx(float(np.mean(losses)), rel=1e-6)
+    else:
+        for x, y in zip(wa, wb):
+            np.testing.assert_allclose(x, y, rtol=1e-5, atol=1e-7)
+        assert avg.value == pytest.approx(float(np.mean(losses)), rel=1e-5)
+    L.tkm_dataset_free(ds)
+    a.close()
+    b.close()
+
+
+def test_eval_counts_first_maximal_logit(gpu):
+    """tkm_runtime_eval (src/tkm_gpu.cu:1535-1575) counts the rows whose first maximal logit is the
+    label, and only the first `count` rows of a partial batch."""
+    import oracle
+    from tokamak_amd import runtime as R
+    log("[case] fused_check: eval")
+    rt = R.Runtime(graph("fused_check"), init_seed=9)
+    x = np.random.default_rng(4).standard_normal(32).astype(np.float32)
+    rt.eval(x, np.zeros(4, np.uint8), 4)
+    logits_node = gjson("fused_check")["nodes"][18]["in0"]
+    bits = np.frombuffer(_read_device(rt.node_device(logits_node), 4 * 4 * 2), np.uint16).copy()
+    logits = oracle.widen(bits, "f16").reshape(4, 4)
+    assert np.all(np.isfinite(logits))
+    pred = logits.argmax(axis=1).astype(np.uint8)          # numpy's argmax is the first maximum
+    assert rt.eval(x, pred, 4) == 4
+    assert rt.eval(x, pred, 3) == 3
+    assert rt.eval(x, ((pred + 1) % 4).astype(np.uint8), 4) == 0
+    rt.close()

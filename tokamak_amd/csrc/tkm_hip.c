@@ -840,11 +840,15 @@ static int ensure_step_graph(TkmRuntime *rt, int variant) {
     return 1;
 }
 
+/* The learning rate goes to the device as a fill kernel's argument: the value is taken at
+ * launch, so steps enqueued back to back (epochs, tkm_runtime_step_device) each read their own
+ * rate, which a copy from one reused host word would not guarantee. */
 static int set_lr(TkmRuntime *rt, float lr) {
     if (lr == rt->last_lr) return 1;
     rt->last_lr = lr;
-    *rt->h_pin_lr = lr;
-    return HIP_OK(hipMemcpyAsync(rt->d_lr, rt->h_pin_lr, sizeof(float), hipMemcpyHostToDevice, rt->stream));
+    uint32_t bits;
+    memcpy(&bits, &lr, sizeof bits);
+    return tkm_rt_fill_u32(rt->d_lr, sizeof(float), bits, rt->stream) == 0;
 }
 
 int tkm_runtime_upload(TkmRuntime *rt, const float *h_input, const void *h_labels, size_t n_labels) {
