@@ -1,0 +1,43 @@
+"""The runtime as a drop-in for C callers: tests/c_api/tkm_c_driver.c uses only tkm.h, is
+compiled against the reference's own header and linked with the reference's unchanged front end
+(src/tkm_core.c, src/tkm_registry.c) and libtkm_hip.so (oracle/Makefile, target `driver`, built
+in the build container; the binary travels under oracle/_ref/).  On the GPU it runs the
+reference CLI's gradient-check protocol through tkm_load_string, and trains a model file
+loaded with tkm_load_file, saving and reloading its TKM1 weights."""
+import os
+import subprocess
+
+import pytest
+
+from attn_cases import log
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+DRIVER = os.path.join(os.path.dirname(HERE), "oracle", "_ref", "tkm_c_driver")
+
+needs_driver = pytest.mark.skipif(not os.path.exists(DRIVER),
+                                  reason="oracle/_ref/tkm_c_driver is built only where the reference sources exist")
+
+
+def _run(args, tmp_path):
+    log(f"[case] tkm_c_driver {' '.join(args)}")
+    r = subprocess.run([DRIVER] + args, capture_output=True, text=True, timeout=240, cwd=tmp_path)
+    log(r.stdout[-4000:])
+    if r.stderr:
+        log(r.stderr[-2000:])
+    return r
+
+
+@needs_driver
+def test_c_driver_numcheck(gpu, tmp_path):
+    r = _run(["numcheck"], tmp_path)
+    assert r.returncode == 0 and "numcheck: 0 failing" in r.stdout
+    assert r.stdout.count("PASS") == 23
+
+
+@needs_driver
+def test_c_driver_trains_model_file(gpu, tmp_path):
+    model = os.path.join(HERE, "golden", "models", "llama_small.tkm")
+    r = _run(["train", model, "2", "6", "0.01", str(tmp_path / "w.bin")], tmp_path)
+    assert r.returncode == 0 and "PASS" in r.stdout
