@@ -13,7 +13,7 @@ launch / its average duration, against MI355X dense fp16 MFMA peak 2516.6 TFLOP/
 cpu_baseline = the CPU oracle (oracle/attn_ref.c, fp32, OpenMP) timed on a bounded sample
 of the same workload on this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3|cfg2|cfg5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3|cfg3-bf16|cfg2|cfg4|cfg4-attn|cfg5]
 """
 from __future__ import annotations
 
@@ -27,10 +27,13 @@ PEAK_FP16_TFLOPS = 2516.6   # 256 CU x 4096 FLOP/clk x 2.4 GHz, dense
 PEAK_HBM_GBPS = 8000.0
 
 CONFIGS = {
-    # name: (B, S, Hq, Hkv, D, causal, kv_len, backward, qkv scale)
-    "cfg3": (4, 2048, 16, 16, 128, True, None, True, 1.0),
-    "cfg2": (4, 1024, 8, 8, 64, True, None, False, 0.5),
-    "cfg5": (2, 8192, 32, 32, 128, False, [8192, 5000], True, 1.0),
+    # name: (B, S, Hq, Hkv, D, causal, kv_len, backward, qkv scale, dtype)
+    "cfg3": (4, 2048, 16, 16, 128, True, None, True, 1.0, "f16"),
+    "cfg3-bf16": (4, 2048, 16, 16, 128, True, None, True, 1.0, "bf16"),
+    "cfg2": (4, 1024, 8, 8, 64, True, None, False, 0.5, "f16"),
+    # config 4's attention layer alone (the full step: --config cfg4)
+    "cfg4-attn": (8, 512, 8, 8, 64, True, None, True, 1.0, "bf16"),
+    "cfg5": (2, 8192, 32, 32, 128, False, [8192, 5000], True, 1.0, "f16"),
 }
 METRIC = "FlashAttn fwd+bwd TFLOP/s & % fp16 MFMA peak, B4 H16 S2048 D128 causal"
 
@@ -53,7 +56,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", default="cfg3",
-                    choices=sorted(CONFIGS) + sorted(PREP_CONFIGS) + sorted(PLASMA_CONFIGS))
+                    choices=sorted(CONFIGS) + sorted(PREP_CONFIGS) + sorted(PLASMA_CONFIGS) + ["cfg4"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="threads for the CPU baseline (default: min(16, online CPUs); the GPU "
@@ -73,7 +76,7 @@ def cpu_baseline(cfg, threads, max_heads, runs=3):
     import numpy as np
 
     import oracle
-    B, S, Hq, Hkv, D, causal, kv_len, backward, mul = cfg
+    B, S, Hq, Hkv, D, causal, kv_len, backward, mul, _ = cfg
     hs = min(Hq, max_heads)
     oracle.set_threads(threads)
     inp = oracle.make_inputs(B, S, hs, hs, D, "f16", mul=mul, with_dout=backward)
@@ -353,6 +356,140 @@ def cpu_baseline_plasma(name, max_rows):
                       f"(bytes counted as 3 x (in + out) rows), {t:.2f} s"}
 
 
+def step_flops(js):
+    """Algorithmic FLOPs of one training step of a graph fixture: every live GEMM three times
+    (forward, dW, dX: 2*rows*K*N each) and every attention node 3.5 F_fwd (causal S^2/2)."""
+    nodes = js["nodes"]
+    B = js["batch_size"]
+    gemm = attn_f = 0.0
+    for n in nodes:
+        if n["dead"]:
+            continue
+        rows = B * n["H"] * n["W"]
+        if n["op"] in (3, 4, 5):
+            gemm += 3 * 2.0 * rows * nodes[n["in0"]]["C"] * n["C"]
+        elif n["op"] == 6:
+            S = n["H"] * n["W"]
+            attn_f += 3.5 * 4.0 * B * n["q_heads"] * S * S * n["head_dim"] * (0.5 if n["causal"] else 1.0)
+    return gemm, attn_f
+
+
+def run_step(args):
+    """one full training step (forward, backward, SGD) of the 8-layer
+    Llama-style decoder (d_model 512, 8 heads x 64, SwiGLU 1376, vocabulary 8192, S 512, B 8),
+    bf16 storage with fp32 master weights and int32 next-token labels, through libtkm_hip.so
+    (the tkm.h runtime on HIP): one hipGraph replay per step on inputs already in HBM.  The
+    graph is the reference front end's IR of tests/golden/models/cfg4_llama.tkm (fixture
+    tests/golden/tkm_graphs.npz).  value = tokens/s; the attention share is config 4's attention
+    layer (tkm_attn_fwd + tkm_attn_bwd at B8 S512 H8 D64 bf16) timed alone, times 8 layers,
+    over the step time."""
+    import numpy as np
+    import torch
+
+    from tokamak_amd import attn
+    from tokamak_amd import runtime as R
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    fx = np.load(os.path.join(here, "tests", "golden", "tkm_graphs.npz"))
+    js = json.loads(bytes(fx["cfg4/json"]).decode())
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    rt = R.Runtime(R.graph_buffer(fx["cfg4/graph"].tobytes()), dtype=attn.BF16, token_labels=True)
+    B, S, C, V = js["batch_size"], 512, 512, 8192
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(B * S * C).astype(np.float32)
+    y = rng.integers(0, V, B * S).astype(np.int32)
+    rt.upload(x, y)
+    lr = 1e-4
+    stream = torch.cuda.ExternalStream(rt.stream())
+    for _ in range(args.warmup):
+        rt.step_device(lr)
+    torch.cuda.synchronize()
+    K = args.steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    wall0 = time.perf_counter()
+    ev[0].record(stream)
+    for k in range(K):
+        rt.step_device(lr)
+        ev[k + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    step_ms = np.array([ev[k].elapsed_time(ev[k + 1]) for k in range(K)])
+    ms = float(step_ms.mean())
+    loss = rt.last_loss()
+
+    # config 4's attention layer alone, same shape and type, eager
+    Hq = D = None
+    for n in js["nodes"]:
+        if n["op"] == 6 and not n["dead"]:
+            Hq, Hkv, D = n["q_heads"], n["kv_heads"], n["head_dim"]
+    n_attn = sum(1 for n in js["nodes"] if n["op"] == 6 and not n["dead"])
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    qkv = torch.randn((B, S, (Hq + 2 * Hkv) * D), generator=g, device=dev).to(torch.bfloat16)
+    dout = torch.randn((B, S, Hq * D), generator=g, device=dev).to(torch.bfloat16)
+    o = torch.empty((B, S, Hq * D), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
+    dqkv = torch.empty_like(qkv)
+    ws = torch.empty(attn.bwd_workspace_bytes(B, S, Hq), dtype=torch.uint8, device=dev)
+    cur = torch.cuda.current_stream()
+
+    def layer():
+        attn.gqa_fwd(qkv, B, S, Hq, Hkv, D, True, None, out=o, lse=lse)
+        attn.gqa_bwd(qkv, o, dout, lse, B, S, Hq, Hkv, D, True, None, dqkv=dqkv, workspace=ws)
+    for _ in range(50):
+        layer()
+    torch.cuda.synchronize()
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a0.record(cur)
+    for _ in range(100):
+        layer()
+    a1.record(cur)
+    torch.cuda.synchronize()
+    attn_ms = a0.elapsed_time(a1) / 100
+    kpath = {"fwd": None, "bwd": None}
+    attn.gqa_fwd(qkv, B, S, Hq, Hkv, D, True, None, out=o, lse=lse)
+    kpath["fwd"] = attn.last_kernels()
+    attn.gqa_bwd(qkv, o, dout, lse, B, S, Hq, Hkv, D, True, None, dqkv=dqkv, workspace=ws)
+    kpath["bwd"] = attn.last_kernels()
+    torch.cuda.synchronize()
+
+    gemm_f, attn_f = step_flops(js)
+    total_f = gemm_f + attn_f
+    ach = total_f / (ms * 1e-3) / 1e12
+    res = {
+        "metric": "config 4 training step tokens/s (8-layer Llama-style decoder, bf16, one hipGraph)",
+        "value": round(B * S / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: input rows ~ N(0,1), token labels uniform in [0, 8192) (numpy seed 0); "
+                "random-init weights (the runtime's seeded PCG32)",
+        "config": {"workload": "cfg4: full training step (forward, backward, SGD), 8 layers",
+                   "B": B, "S": S, "d_model": C, "heads": Hq, "head_dim": D, "ffn": 1376, "vocab": V,
+                   "launches_per_step": rt.kernel_count()},
+        "step_ms_p10_p50_p90": [round(float(np.percentile(step_ms, p)), 5) for p in (10, 50, 90)],
+        "attention": {"layer_fwd_bwd_ms": round(attn_ms, 5), "layers": n_attn,
+                      "share_of_step": round(n_attn * attn_ms / ms, 4),
+                      "layer_tflops": round(attn_f / n_attn / (attn_ms * 1e-3) / 1e12, 2),
+                      "kernel_path": kpath},
+        "roofline": {"kernel": "whole step (GEMMs + attention, algorithmic FLOPs)", "bound": "mfma",
+                     "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(ach / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                     "flops_per_step": total_f, "gemm_flops": gemm_f, "attention_flops": attn_f},
+        "last_loss": round(float(loss), 5),
+        "wall_s": round(wall, 3),
+    }
+    rt.close()
+    print(json.dumps(res))
+
+
 def measured_traffic(name):
     """HBM bytes per launch of a kernel at config 3, from the FETCH_SIZE / WRITE_SIZE counter
     runs summarized in profiles/attn_cfg3_traffic.md (None if absent)."""
@@ -382,21 +519,25 @@ def main():
     if args.config in PLASMA_CONFIGS:
         run_plasma(args)
         return
+    if args.config == "cfg4":
+        run_step(args)
+        return
     import numpy as np
     import torch
 
     from tokamak_amd import attn
 
     cfg = CONFIGS[args.config]
-    B, S, Hq, Hkv, D, causal, kv_len, backward, mul = cfg
+    B, S, Hq, Hkv, D, causal, kv_len, backward, mul, dtype = cfg
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     g = torch.Generator(device=dev)
     g.manual_seed(0)
-    qkv = (torch.randn((B, S, (Hq + 2 * Hkv) * D), generator=g, device=dev) * mul).half()
+    qkv = (torch.randn((B, S, (Hq + 2 * Hkv) * D), generator=g, device=dev) * mul).to(tdt)
     g.manual_seed(1)
-    dout = torch.randn((B, S, Hq * D), generator=g, device=dev).half()
-    o = torch.empty((B, S, Hq * D), dtype=torch.float16, device=dev)
+    dout = torch.randn((B, S, Hq * D), generator=g, device=dev).to(tdt)
+    o = torch.empty((B, S, Hq * D), dtype=tdt, device=dev)
     lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
     dqkv = torch.empty_like(qkv)
     ws = torch.empty(attn.bwd_workspace_bytes(B, S, Hq), dtype=torch.uint8, device=dev)
@@ -499,8 +640,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
-        "data": "synthetic: Q/K/V, dO ~ N(0,1) (torch.randn on device, seeds 0/1), fp16",
+        "dtype": dtype,
+        "data": f"synthetic: Q/K/V, dO ~ N(0,1) (torch.randn on device, seeds 0/1), {dtype}",
         "config": {"workload": f"{args.config}: GQA attention {'fwd+bwd' if backward else 'fwd'}",
                    "B": B, "S": S, "Hq": Hq, "Hkv": Hkv, "D": D, "causal": causal,
                    "kv_len": kv_len, "scale": "1/sqrt(D)"},
