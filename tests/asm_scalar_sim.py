@@ -11,6 +11,13 @@ What the kernels under test must show: every workgroup terminates; each DMA and 
 descriptor stays inside its tensor; and, through '; <event>' comment lines the generators
 emit, the LDS tile a wave is about to read was written by DMA in an earlier barrier phase
 with the expected rows, and is not written by any wave in the phase that reads it.
+
+Lane reach: where the caller names, for a VGPR that holds per-lane offsets, the largest
+offset any lane adds (lane_max: vgpr -> bytes, or a tuple of bytes per wave), an instruction `v_add_u32_e32 vX, sY, vZ`
+records vX = sY + lanes(vZ); a buffer access through vX with `offen` must then touch no byte
+past the end of the tensor the descriptor covers.  Lanes are taken to touch rows 0..k of the
+tensor's pitch at columns up to lanes(vZ) mod pitch; offsets at or past num_records are
+dropped by the hardware.
 """
 from __future__ import annotations
 
@@ -77,6 +84,7 @@ class Wave:
         self.wg, self.wave = wg, wave
         self.done = False
         self.loads = []         # (destination operand, descriptor base) of plain buffer loads
+        self.vscal = {}         # vgpr -> (scalar offset, largest lane offset) (lane reach)
 
     def get(self, o, w64=False):
         kind, i, n = o
@@ -127,8 +135,9 @@ class Sim:
     the VGPR holding v0 >> 6 when the prologue reads the wave index from it."""
 
     def __init__(self, lines, kernarg, mem, kv_len, n_wg, expect, on_event=None, overflow=(),
-                 tile_bytes=16384, max_steps=2_000_000, wave_vgpr=64):
+                 tile_bytes=16384, max_steps=2_000_000, wave_vgpr=64, lane_max=None):
         self.ins, self.labels = parse(lines)
+        self.lane_max = dict(lane_max or {})
         self.wave_vgpr = wave_vgpr
         self.kernarg = kernarg
         self.mem = mem
@@ -147,6 +156,31 @@ class Sim:
         kind, i, n = o
         w0, w1, w2, w3 = (w.get(("s", i + k, 1)) for k in range(4))
         return w0 | ((w1 & 0xFFFF) << 32), w2, w3
+
+    def _reach(self, w, vop, base, nrec, text):
+        """Lane reach of a buffer access with offen through VGPR vop (see the module notes)."""
+        if vop is None or vop[0] != "v":
+            return
+        got = w.vscal.get(vop[1])
+        if got is None:
+            return
+        scal, lanes = got
+        for name, (b0, size, pitch, _) in self.mem.items():
+            if b0 <= base < b0 + size:
+                # lanes touch rows 0..k of `pitch` bytes at columns up to `col`; offsets at or
+                # past num_records are dropped
+                k_top, col = divmod(lanes, pitch)
+                if scal + lanes < nrec:
+                    last = base + scal + lanes
+                else:
+                    k = (nrec - 1 - scal) // pitch
+                    if k < 0:
+                        return
+                    last = base + min(scal + min(k, k_top) * pitch + col, nrec - 1)
+                if last >= b0 + size:
+                    raise Fail(f"{text}: a lane reaches {last - (b0 + size) + 1} bytes past the end of {name} "
+                               f"(offset {scal:#x} + lanes {lanes:#x}, num_records {nrec:#x})")
+                return
 
     def _inside(self, base, nrec, what):
         """The tensor a descriptor lies in.  A descriptor covers whole rows of pitch bytes of
@@ -237,8 +271,18 @@ class Sim:
 
     def _exec(self, w, op, a, text, phase):
         g = w.get
+        if op == "v_add_u32_e32" and a[0][0] == "v" and a[1][0] == "s" and a[2][0] == "v":
+            if a[2][1] in self.lane_max:
+                lm = self.lane_max[a[2][1]]
+                w.vscal[a[0][1]] = (g(a[1]), lm[w.wave] if isinstance(lm, (tuple, list)) else lm)
+            else:
+                w.vscal.pop(a[0][1], None)
+            return
         if op in ("s_waitcnt", "s_nop", "s_setprio") or op.startswith("v_") and not (
                 op == "v_readfirstlane_b32" or (op.startswith("v_cmp") and op.endswith("_e64"))):
+            if op.startswith("v_") and a and a[0] and a[0][0] == "v":
+                for k in range(a[0][2]):
+                    w.vscal.pop(a[0][1] + k, None)
             return
         if op == "v_readfirstlane_b32":
             src = a[1]
@@ -270,6 +314,8 @@ class Sim:
         if op.startswith("buffer_load") and any(x and x[0] == "mod" and x[1] == "lds" for x in a):
             base, nrec, w3 = self._desc(w, a[1])
             self._inside(base, nrec, text)
+            if any(x and x[0] == "mod" and x[1] == "offen" for x in a):
+                self._reach(w, a[0], base, nrec, text)
             slot = w.m0 // 1024
             self.lds[slot] = (phase, base, nrec, (w.m0 % self.tile_bytes) // 256)
             self.writes.setdefault(phase, set()).add(slot)

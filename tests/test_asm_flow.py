@@ -142,6 +142,7 @@ def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, overflow=()):
     (1, 64, 1, 1, True, None, 1),
     (1, 1, 1, 1, False, None, 1),
     (2, 2048, 4, 4, True, None, 7),
+    (1, 512, 4, 2, True, None, 8),          # one item per workgroup: the DMA stream runs past the last item
     (1, 300, 3, 1, True, [129], 256),
 ])
 def test_fwd_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg):
@@ -224,8 +225,13 @@ def run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg):
                     raise Fail(f"next-item {'V' if o[1] >= attn_dkdv.A_NV else 'K'} load from {base:#x}, expected {want:#x}")
             checked[0] += 1
 
+    # largest lane offset of each DMA address register: rows wave*8 + 4i + 0..3 of a tile, 256 B
+    reach = {attn_dkdv.V_LOFF: 255}
+    for i in range(2):
+        reach[attn_dkdv.V_DOFF + i] = tuple((8 * w + 4 * i + 3) * ldb + 255 for w in range(4))
+        reach[attn_dkdv.V_DOFF + 2 + i] = tuple((8 * w + 4 * i + 3) * ldo + 255 for w in range(4))
     sim = Sim(_gen_lines(attn_dkdv), args, _bwd_mem(B, S, Hq, Hkv, kv), kv, n_wg, None, on_event,
-              wave_vgpr=attn_dkdv.V_PT)
+              wave_vgpr=attn_dkdv.V_PT, lane_max=reach)
     sim.run()
     want = {(b, h, 128 * z + 32 * w) for b in range(B) for h in range(Hkv) for z in range(n_kblk) for w in range(4)}
     assert set(stored) == want and all(c == 1 for c in stored.values()), \

@@ -333,7 +333,7 @@ def test_resident_epoch_matches_steps(gpu, schedule):
 
 
 def test_eval_counts_first_maximal_logit(gpu):
-    """tkm_runtime_eval (src/tkm_gpu.cu:1535-1575) counts the rows whose first maximal logit is the
+    """tkm_runtime_eval (src/tkm_gpu.cu:1598-1631) counts the rows whose first maximal logit is the
     label, and only the first `count` rows of a partial batch."""
     import oracle
     from tokamak_amd import runtime as R

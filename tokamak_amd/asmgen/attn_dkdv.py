@@ -15,8 +15,8 @@ Work decomposition: grid (Hkv, B, n_kblk), one workgroup = 4 waves = one (batch,
 block of 128 keys); one wave per SIMD.  A wave owns 32 keys: K (prescaled by
 scale*log2(e)) and V of those keys sit in AGPRs as the B operands of S = Q K^T and
 dP = dO V^T, and the accumulators dV^T, dK^T (C[m = head dim][n = key]) in AGPRs.  The
-workgroup walks the query tiles (32 rows) of every q-head of the group (causal: from its own
-key block on); each tile's Q and dO rows go HBM -> LDS by buffer DMA into one of four buffers
+workgroup walks the query tiles (32 rows) of every q-head of the group from the last one down
+(causal: to its own key block's first); each tile's Q and dO rows go HBM -> LDS by buffer DMA into one of four buffers
 (tile t in buffer t % 4, requested three tiles ahead); each wave also copies the tile's 256
 bytes of row values into its own slot.  The DMA descriptors are fixed for the kernel (whole batch, so rows
 past S read as zero); a tile's position enters as an offset added to the lane offsets.
@@ -74,7 +74,7 @@ S_TQ, S_TO, S_TL = 5, 6, 7             # offsets of the requested tile (Q, dO, r
 S_LDB32, S_LDO32 = 88, 89              # 32 rows of qkv / dO in bytes
 S_MAGBH, S_MAGHKV = 90, 91             # ceil(2^32 / (B*Hkv)), ceil(2^32 / Hkv) (0 for 1)
 S_BA, S_KVHA, S_ITERSD, S_QTBD = 92, 93, 94, 95   # current item's batch, kv head; DMA item's tiles
-S_WAVE, S_KVL, S_KB0, S_KW0, S_QTB, S_QTE, S_ITERS, S_IT = 32, 33, 34, 35, 36, 37, 38, 39
+S_WAVE, S_KVL, S_KB0, S_KW0, S_QTB, S_QTL, S_ITERS, S_IT = 32, 33, 34, 35, 36, 37, 38, 39
 S_BQKV, S_BDO, S_BLD = 40, 42, 44      # 64-bit bases of the DMA stream's item
 S_CODE, S_KWACT = 46, 47               # variant of the current body; wave has a key < kv_len
 S_RQ, S_RO, S_RL = 48, 52, 56          # DMA descriptors of the DMA stream's item
@@ -325,18 +325,22 @@ class Body:
         self.s(f"s_cmp_ge_u32 {sr(T)}, {sr(S_KWEFF)}", S(T) + S(S_KWEFF), [("scc", 0)])
         self.s(f"s_cselect_b32 {sr(dst)}, {sr(S_KWACT)}, 0", S(S_KWACT) + [("scc", 0)], S(dst))
 
+    # Query tiles are walked from the last (S_QTL) down to the item's first visible one, so
+    # that the items of one (batch, kv head) that run at the same time on one XCD (key blocks
+    # z, z+1, ... of a round) read the same Q / dO tiles together and share them in its L2;
+    # walked upwards, they start at their own diagonals and read each tile at different times.
     def advance_qt(self, qt):
         s = self.s
-        s(f"s_add_u32 {sr(qt)}, {sr(qt)}, 1", S(qt), S(qt))
-        s(f"s_cmp_ge_u32 {sr(qt)}, {sr(S_QTE)}", S(qt) + S(S_QTE), [("scc", 0)])
-        s(f"s_cselect_b32 {sr(qt)}, {sr(S_QTB)}, {sr(qt)}", S(S_QTB) + S(qt) + [("scc", 0)], S(qt))
+        s(f"s_sub_u32 {sr(qt)}, {sr(qt)}, 1", S(qt), S(qt))
+        s(f"s_cmp_lt_i32 {sr(qt)}, {sr(S_QTB)}", S(qt) + S(S_QTB), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(qt)}, {sr(S_QTL)}, {sr(qt)}", S(S_QTL) + S(qt) + [("scc", 0)], S(qt))
 
     def advance_h(self, h, qt, qtb=S_QTBD):
-        """(h, qt) := (h, qt + 1), or (h + 1, qtb) past the last query tile."""
+        """(h, qt) := (h, qt - 1), or (h + 1, last tile) below the first visible query tile."""
         s = self.s
-        s(f"s_add_u32 {sr(qt)}, {sr(qt)}, 1", S(qt), S(qt))
-        s(f"s_cmp_ge_u32 {sr(qt)}, {sr(S_QTE)}", S(qt) + S(S_QTE), [("scc", 0)])
-        s(f"s_cselect_b32 {sr(qt)}, {sr(qtb)}, {sr(qt)}", S(qtb) + S(qt) + [("scc", 0)], S(qt))
+        s(f"s_sub_u32 {sr(qt)}, {sr(qt)}, 1", S(qt), S(qt))
+        s(f"s_cmp_lt_i32 {sr(qt)}, {sr(qtb)}", S(qt) + S(qtb), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(qt)}, {sr(S_QTL)}, {sr(qt)}", S(S_QTL) + S(qt) + [("scc", 0)], S(qt))
         s(f"s_addc_u32 {sr(h)}, {sr(h)}, 0", S(h) + [("scc", 0)], S(h))
 
     def code(self):
@@ -416,19 +420,22 @@ class Body:
         p.label(label)
 
     def tiles_of(self, kb0, kvl, qtb, iters):
-        """qtb = causal ? kb0/32 : 0; iters = kb0 >= kvl ? 1 : g*(QTE - qtb)."""
+        """qtb = causal ? kb0/32 : 0; iters = kb0 >= kvl ? 1 : g*(QTL + 1 - qtb)."""
         s = self.s
         s(f"s_lshr_b32 {sr(qtb)}, {sr(kb0)}, 5", S(kb0), S(qtb))
         s(f"s_cmp_eq_u32 {sr(S_CAUSAL)}, 0", S(S_CAUSAL), [("scc", 0)])
         s(f"s_cselect_b32 {sr(qtb)}, 0, {sr(qtb)}", S(qtb) + [("scc", 0)], S(qtb))
-        s(f"s_sub_u32 {sr(iters)}, {sr(S_QTE)}, {sr(qtb)}", S(S_QTE) + S(qtb), S(iters))
+        s(f"s_sub_u32 {sr(iters)}, {sr(S_QTL)}, {sr(qtb)}", S(S_QTL) + S(qtb), S(iters))
+        s(f"s_add_u32 {sr(iters)}, {sr(iters)}, 1", S(iters), S(iters))
         s(f"s_mul_i32 {sr(iters)}, {sr(iters)}, {sr(S_G)}", S(iters) + S(S_G), S(iters))
         s(f"s_cmp_ge_u32 {sr(kb0)}, {sr(kvl)}", S(kb0) + S(kvl), [("scc", 0)])
         s(f"s_cselect_b32 {sr(iters)}, 1, {sr(iters)}", S(iters) + [("scc", 0)], S(iters))
 
     def decode_d(self, sfx):
-        """DMA stream: item of round S_KD -> bases, descriptors, QTBD, ITERSD; tile (0, QTBD).
-        Past the last item the stream keeps re-reading its item (in bounds, never used)."""
+        """DMA stream: item of round S_KD -> bases, descriptors, QTBD, ITERSD; tile (0, QTL).
+        Past the last item the stream keeps re-reading its item from head 0's last tile (in
+        bounds, never used): left at the head past the group's last, it would read the rows
+        after the item's (past the end of dO for the last batch and kv head)."""
         p, s = self.p, self.s
         I, Z, B, KVH, KVL, KB0 = (S_TMP + k for k in range(6))
         T0, T1, T2 = S_TMP + 6, S_TMP + 7, S_TMP + 8
@@ -436,6 +443,8 @@ class Body:
         s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
         p.branch(f"s_cbranch_scc0 .Ldd_{sfx}", [("scc", 0)], skip_xdl=ACC)
         s(f"s_mov_b32 {sr(S_ITERSD)}, 0x7fffffff", [], S(S_ITERSD))
+        s(f"s_mov_b32 {sr(S_H3)}, 0", [], S(S_H3))
+        s(f"s_mov_b32 {sr(S_QT3)}, {sr(S_QTL)}", S(S_QTL), S(S_QT3))
         p.branch(f"s_branch .Lde_{sfx}", skip_xdl=ACC)
         p.label(f".Ldd_{sfx}")
         self.decode(I, Z, B, KVH)
@@ -444,7 +453,7 @@ class Body:
         self.tiles_of(KB0, KVL, S_QTBD, S_ITERSD)
         s(f"s_mov_b32 {sr(S_ITD)}, 0", [], S(S_ITD))
         s(f"s_mov_b32 {sr(S_H3)}, 0", [], S(S_H3))
-        s(f"s_mov_b32 {sr(S_QT3)}, {sr(S_QTBD)}", S(S_QTBD), S(S_QT3))
+        s(f"s_mov_b32 {sr(S_QT3)}, {sr(S_QTL)}", S(S_QTL), S(S_QT3))
         # bases: qkv + b*S*ldb + kvh*g*256; dout + b*S*ldo + kvh*g*256; pairs + (b*Hq + kvh*g)*SP*8
         s(f"s_mul_i32 {sr(T0)}, {sr(B)}, {sr(S_SEQ)}", S(B) + S(S_SEQ), S(T0))
         s(f"s_mul_i32 {sr(T1)}, {sr(KVH)}, {sr(S_G)}", S(KVH) + S(S_G), S(T1))
@@ -503,8 +512,8 @@ class Body:
         s(f"s_cselect_b32 {sr(S_KWDIAG)}, -1, {sr(S_KW0)}", S(S_KW0) + [("scc", 0)], S(S_KWDIAG))
         self.tiles_of(S_KB0, S_KVL, S_QTB, S_ITERS)
         s(f"s_mov_b32 {sr(S_IT)}, 0", [], S(S_IT))
-        s(f"s_mov_b32 {sr(S_QT0)}, {sr(S_QTB)}", S(S_QTB), S(S_QT0))
-        s(f"s_mov_b32 {sr(S_QT1)}, {sr(S_QTB)}", S(S_QTB), S(S_QT1))
+        s(f"s_mov_b32 {sr(S_QT0)}, {sr(S_QTL)}", S(S_QTL), S(S_QT0))
+        s(f"s_mov_b32 {sr(S_QT1)}, {sr(S_QTL)}", S(S_QTL), S(S_QT1))
         self.advance_qt(S_QT1)
 
     def kv_load(self):
@@ -788,7 +797,8 @@ def build(check_ldb: int = 12288, check_ldo: int = 4096) -> str:
     p.waitcnt(lgkm=0)
     T0, T3 = S_TMP, S_TMP + 3
     sal(f"s_add_u32 {sr(T0)}, {sr(S_SEQ)}, 31", S(S_SEQ), S(T0))
-    sal(f"s_lshr_b32 {sr(S_QTE)}, {sr(T0)}, 5", S(T0), S(S_QTE))
+    sal(f"s_lshr_b32 {sr(S_QTL)}, {sr(T0)}, 5", S(T0), S(S_QTL))
+    sal(f"s_sub_u32 {sr(S_QTL)}, {sr(S_QTL)}, 1", S(S_QTL), S(S_QTL))          # the last query tile
     sal(f"s_lshl_b32 {sr(S_LDB32)}, {sr(S_LDB)}, 5", S(S_LDB), S(S_LDB32))
     sal(f"s_lshl_b32 {sr(S_LDO32)}, {sr(S_LDO)}, 5", S(S_LDO), S(S_LDO32))
     sal(f"s_lshl_b32 {sr(S_LDSW)}, {sr(S_WAVE)}, 11", S(S_WAVE), S(S_LDSW))       # Q/dO rows wave*8..
