@@ -72,6 +72,7 @@ typedef struct {
     void *mask;
     float *lse;
     tkm_gemm *g_fwd, *g_dw, *g_dx;
+    int dx_first;                       /* GEMM dX is the first writer of grad(in0): beta 0 */
 } rt_node;
 
 typedef struct {
@@ -80,6 +81,7 @@ typedef struct {
     tkm_kplan plan[2];
     int chain[3 * TKM_PLASMA_MAX_NODES], n_chain;
     int rows, twin;
+    int din_first, branch_first;        /* first writer of the gradient slot: overwrite instead of += */
     unsigned gx, gy_fwd, bands, band, gx_red;
     int n_par;                          /* reduce targets (plasma: geometry order; prep: dbias, dgamma) */
     int par_kind[3 * 3 * TKM_PLASMA_MAX_NODES], par_node[3 * 3 * TKM_PLASMA_MAX_NODES];
@@ -99,7 +101,9 @@ struct TkmRuntime {
     rt_node *nodes;
     rt_tensor *tensors;
     int n_tensors;
-    long long total_elems;
+    long long total_elems, sgd_blocks;
+    size_t (*clear)[2];                 /* gradient-arena ranges (offset, bytes) a step clears */
+    int n_clear;
     TkmSgdTensor *d_sgd;
     void *param_block;           /* masters, velocities, GEMM gradients, 16-bit copies */
     float *pgrad_block;          /* gradients of the parameter vectors: cleared each step */
@@ -335,7 +339,7 @@ static int alloc_params(TkmRuntime *rt) {
     }
     rt->n_tensors = nt;
     /* initial values (host), uploaded once */
-    long long off = 0;
+    long long off = 0, blocks = 0;
     TkmSgdTensor *h = (TkmSgdTensor *)calloc((size_t)(nt > 0 ? nt : 1), sizeof(TkmSgdTensor));
     if (!h) return 0;
     for (int k = 0; k < nt; ++k) {
@@ -356,9 +360,12 @@ static int alloc_params(TkmRuntime *rt) {
         h[k].grad = t->grad;
         h[k].offset = off;
         h[k].size = (long long)t->n;
+        h[k].block0 = blocks;
         off += (long long)t->n;
+        blocks += ((long long)t->n + TKM_SGD_CHUNK - 1) / TKM_SGD_CHUNK;
     }
     rt->total_elems = off;
+    rt->sgd_blocks = blocks;
     if (nt > 0) {
         if (!HIP_OK(hipMalloc((void **)&rt->d_sgd, (size_t)nt * sizeof(TkmSgdTensor))) ||
             !HIP_OK(hipMemcpy(rt->d_sgd, h, (size_t)nt * sizeof(TkmSgdTensor), hipMemcpyHostToDevice))) {
@@ -411,6 +418,121 @@ static int alloc_saves(TkmRuntime *rt) {
     return 1;
 }
 
+/* Which kernel writes each gradient slot first in the backward walk (the order record_step
+ * records).  The reference clears the whole gradient arena every step and lets every writer
+ * accumulate; here the first writer of a slot overwrites it instead (GEMM dX with beta 0, a
+ * group's din or residual gradient without its accumulate flag), and only the slots whose
+ * first writer must accumulate, or that are read before any write, are cleared.  A group
+ * whose residual Add reads its own anchor (din and the branch gradient land in one slot)
+ * keeps accumulating. */
+static int plan_grad_writes(TkmRuntime *rt) {
+    const TkmGraph *g = &rt->graph;
+    if (!rt->training) return 1;
+    unsigned char *written = (unsigned char *)calloc((size_t)g->num_nodes, 1);
+    unsigned char *clear = (unsigned char *)calloc((size_t)g->num_nodes, 1);
+    unsigned char done[TKM_MAX_GROUPS] = {0};
+    if (!written || !clear) {
+        free(written);
+        free(clear);
+        return 0;
+    }
+#define TKM_READ(nid) do { if (!written[nid]) { clear[nid] = 1; written[nid] = 1; } } while (0)
+#define TKM_ACCUM(nid) do { if (!written[nid]) { clear[nid] = 1; written[nid] = 1; } } while (0)
+    for (int i = 1; i < g->num_nodes; ++i)      /* the loss writes dlogits in the forward walk */
+        if (!g->nodes[i].dead && is_loss(g->nodes[i].op)) written[g->nodes[i].in0] = 1;
+    for (int i = g->num_nodes - 1; i >= 1; --i) {
+        const TkmNode *n = &g->nodes[i];
+        if (n->dead || is_loss(n->op)) continue;
+        if (n->plasma_grp >= 0) {
+            const int gid = n->plasma_grp;
+            if (done[gid]) continue;
+            done[gid] = 1;
+            rt_group *G = &rt->groups[gid];
+            const PlasmaGroup *pg = &g->groups[gid];
+            G->din_first = G->branch_first = 0;
+            if (G->kind < 0) continue;
+            TKM_READ(pg->out_node_id);
+            const int a = pg->anchor_id;
+            int self_branch = 0, n_add = 0, adds_unwritten = 0;
+            if (G->kind == TKM_HIP_GROUP_PLASMA)
+                for (int k = 0; k < G->n_chain; ++k) {
+                    const TkmNode *c = &g->nodes[G->chain[k]];
+                    if (c->op != OP_ADD) continue;
+                    ++n_add;
+                    if (c->in1 == a) self_branch = 1;
+                    for (int k2 = 0; k2 < k; ++k2)
+                        if (g->nodes[G->chain[k2]].op == OP_ADD && g->nodes[G->chain[k2]].in1 == c->in1) self_branch = 1;
+                    if (!written[c->in1]) ++adds_unwritten;
+                }
+            /* residual gradients (written before din inside the kernel) */
+            if (n_add > 0) {
+                if (!self_branch && adds_unwritten == n_add) {
+                    G->branch_first = 1;
+                    for (int k = 0; k < G->n_chain; ++k)
+                        if (g->nodes[G->chain[k]].op == OP_ADD) written[g->nodes[G->chain[k]].in1] = 1;
+                } else {
+                    for (int k = 0; k < G->n_chain; ++k)
+                        if (g->nodes[G->chain[k]].op == OP_ADD) TKM_ACCUM(g->nodes[G->chain[k]].in1);
+                }
+            }
+            if (G->kind == TKM_HIP_GROUP_PLASMA && G->twin) {
+                written[a] = 1;                 /* a twin group overwrites din */
+            } else if (!written[a] && !self_branch) {
+                G->din_first = 1;
+                written[a] = 1;
+            } else {
+                TKM_ACCUM(a);
+            }
+            continue;
+        }
+        rt_node *st = &rt->nodes[i];
+        if (is_gemm(n->op)) {
+            TKM_READ(i);
+            st->dx_first = !written[n->in0];
+            written[n->in0] = 1;
+        } else if (n->op == OP_GQA_ATTN) {
+            TKM_READ(i);
+            written[n->in0] = 1;
+        } else if (n->op == OP_FLATTEN) {
+            TKM_READ(i);
+            if (n->out_offset != g->nodes[n->in0].out_offset) written[n->in0] = 1;
+        } else if (n->op == OP_SOFTMAX) {
+            TKM_READ(i);
+            TKM_ACCUM(n->in0);
+        }
+    }
+#undef TKM_READ
+#undef TKM_ACCUM
+    /* the slots to clear, as merged byte ranges of the gradient arena */
+    rt->clear = (size_t(*)[2])calloc((size_t)g->num_nodes + 1, sizeof *rt->clear);
+    int nc = 0;
+    if (rt->clear) {
+        for (int i = 0; i < g->num_nodes; ++i) {
+            if (!clear[i] || g->nodes[i].out_bytes == 0) continue;
+            const size_t lo = g->nodes[i].out_offset & ~(size_t)15;
+            const size_t hi = (g->nodes[i].out_offset + g->nodes[i].out_bytes + 15) & ~(size_t)15;
+            int merged = 0;
+            for (int c = 0; c < nc && !merged; ++c)
+                if (lo <= rt->clear[c][0] + rt->clear[c][1] && hi >= rt->clear[c][0]) {
+                    const size_t a0 = lo < rt->clear[c][0] ? lo : rt->clear[c][0];
+                    const size_t a1 = hi > rt->clear[c][0] + rt->clear[c][1] ? hi : rt->clear[c][0] + rt->clear[c][1];
+                    rt->clear[c][0] = a0;
+                    rt->clear[c][1] = a1 - a0;
+                    merged = 1;
+                }
+            if (!merged) {
+                rt->clear[nc][0] = lo;
+                rt->clear[nc][1] = hi - lo;
+                ++nc;
+            }
+        }
+    }
+    rt->n_clear = nc;
+    free(written);
+    free(clear);
+    return rt->clear != NULL;
+}
+
 static int plan_gemms(TkmRuntime *rt) {
     const TkmGraph *g = &rt->graph;
     const int ab = rt->dt == TKM_ATTN_BF16 ? TKM_GEMM_BF16 : TKM_GEMM_F16;
@@ -428,7 +550,9 @@ static int plan_gemms(TkmRuntime *rt) {
         if (rt->training) {
             if (tkm_gemm_create(&st->g_dw, rt->lt, 0, 1, N, K, rows, N, K, N, ab, TKM_GEMM_F32, 0.0f, TKM_GEMM_MAX_WS))
                 goto fail;
-            if (tkm_gemm_create(&st->g_dx, rt->lt, 1, 0, K, rows, N, N, N, K, ab, ab, 1.0f, TKM_GEMM_MAX_WS)) goto fail;
+            if (tkm_gemm_create(&st->g_dx, rt->lt, 1, 0, K, rows, N, N, N, K, ab, ab, st->dx_first ? 0.0f : 1.0f,
+                                TKM_GEMM_MAX_WS))
+                goto fail;
             if (ws < tkm_gemm_workspace(st->g_dw)) ws = tkm_gemm_workspace(st->g_dw);
             if (ws < tkm_gemm_workspace(st->g_dx)) ws = tkm_gemm_workspace(st->g_dx);
         }
@@ -507,6 +631,7 @@ static int plan_groups(TkmRuntime *rt) {
 }
 
 static void free_runtime(TkmRuntime *rt);
+static int tune_gemms(TkmRuntime *rt);
 
 TkmRuntime *tkm_runtime_ignite_ex(const TkmGraph *g, const char *src, const tkm_runtime_opts *o) {
     if (!g) return NULL;
@@ -612,7 +737,9 @@ TkmRuntime *tkm_runtime_ignite_ex(const TkmGraph *g, const char *src, const tkm_
         rt->h_pin_loss = rt->h_pin_lr + 1;
         *rt->h_pin_lr = 1e-3f;
     }
-    if (!alloc_params(rt) || !alloc_saves(rt) || !plan_gemms(rt) || !plan_groups(rt)) goto fail;
+    if (!alloc_params(rt) || !alloc_saves(rt) || !plan_groups(rt) || !plan_grad_writes(rt) || !plan_gemms(rt) ||
+        !tune_gemms(rt))
+        goto fail;
     free(own_src);
     if (opts.verbose)
         printf("  [TKM HIP Engine] Ignited %d hipRTC kernels | %d Learnable Tensors (%lld params) | %.2f MB Arena "
@@ -646,6 +773,26 @@ static uint8_t *grd(TkmRuntime *rt, int nid) { return rt->grad_arena + rt->graph
 static float *tensor_master(TkmRuntime *rt, int t) { return t >= 0 ? rt->tensors[t].master : NULL; }
 static float *tensor_grad(TkmRuntime *rt, int t) { return t >= 0 ? rt->tensors[t].grad : NULL; }
 
+/* Times each GEMM plan's candidate algorithms on the runtime's own buffers and keeps the
+ * fastest (tkm_gemm_tune; outputs are scratch at this point: activations, gradients and the
+ * gradient arena are rewritten by every step). */
+static int tune_gemms(TkmRuntime *rt) {
+    const TkmGraph *g = &rt->graph;
+    for (int i = 1; i < g->num_nodes; ++i) {
+        const TkmNode *n = &g->nodes[i];
+        if (n->dead || !is_gemm(n->op) || n->plasma_grp >= 0) continue;
+        rt_node *st = &rt->nodes[i];
+        rt_tensor *t = &rt->tensors[st->t_w];
+        if (tkm_gemm_tune(st->g_fwd, t->w16, act(rt, n->in0), act(rt, i), rt->gemm_ws, rt->gemm_ws_bytes, rt->stream))
+            return 0;
+        if (!rt->training) continue;
+        if (tkm_gemm_tune(st->g_dw, grd(rt, i), act(rt, n->in0), t->grad, rt->gemm_ws, rt->gemm_ws_bytes, rt->stream) ||
+            tkm_gemm_tune(st->g_dx, t->w16, grd(rt, i), grd(rt, n->in0), rt->gemm_ws, rt->gemm_ws_bytes, rt->stream))
+            return 0;
+    }
+    return HIP_OK(hipStreamSynchronize(rt->stream));
+}
+
 /* Resolves a plan parameter (the reference's resolve_arg_ptr, src/tkm_gpu.cu:1142-1164). */
 static void resolve(TkmRuntime *rt, const rt_group *G, const PlasmaGroup *pg, const tkm_kparam *p, int bwd,
                     void **val, int *ival) {
@@ -671,10 +818,12 @@ static void resolve(TkmRuntime *rt, const rt_group *G, const PlasmaGroup *pg, co
         case TKM_KP_ROWS: *ival = G->rows; break;
         case TKM_KP_BAND: *ival = (int)G->band; break;
         case TKM_KP_ACC:
-            /* plain groups and the qkv-prep accumulate din; a twin group overwrites it
-             * (src/tkm_codegen.c:601-614); residual and parameter gradients accumulate */
-            if (G->kind == TKM_HIP_GROUP_PREP) *ival = 1;
-            else *ival = (G->twin ? 0 : TKM_PLASMA_ACC_DIN) | TKM_PLASMA_ACC_PARAMS | TKM_PLASMA_ACC_BRANCH;
+            /* plain groups and the qkv-prep accumulate din, a twin group overwrites it
+             * (src/tkm_codegen.c:601-614), residual and parameter gradients accumulate; a
+             * group that writes a gradient slot first overwrites it (plan_grad_writes) */
+            if (G->kind == TKM_HIP_GROUP_PREP) *ival = G->din_first ? 0 : 1;
+            else *ival = (G->twin || G->din_first ? 0 : TKM_PLASMA_ACC_DIN) | TKM_PLASMA_ACC_PARAMS |
+                         (G->branch_first ? 0 : TKM_PLASMA_ACC_BRANCH);
             break;
         default: break;
     }
@@ -775,7 +924,9 @@ static void record_step(TkmRuntime *rt, int clear_loss) {
     const TkmGraph *g = &rt->graph;
     const int B = g->batch_size;
     if (clear_loss) note(rt, tkm_rt_fill_u32(rt->d_loss, 4, 0, rt->stream), "loss clear");
-    note(rt, tkm_rt_fill_u32(rt->grad_arena, g->total_arena_bytes, 0, rt->stream), "gradient arena clear");
+    for (int c = 0; c < rt->n_clear; ++c)
+        note(rt, tkm_rt_fill_u32(rt->grad_arena + rt->clear[c][0], rt->clear[c][1], 0, rt->stream),
+             "gradient slot clear");
     if (rt->pgrad_bytes) note(rt, tkm_rt_fill_u32(rt->pgrad_block, rt->pgrad_bytes, 0, rt->stream), "gradient clear");
     forward_pass(rt, 0, B);
     unsigned char done[TKM_MAX_GROUPS] = {0};
@@ -810,7 +961,7 @@ static void record_step(TkmRuntime *rt, int clear_loss) {
         }
     }
     if (rt->total_elems > 0)
-        note(rt, tkm_rt_sgd(rt->d_sgd, rt->n_tensors, rt->total_elems, rt->d_lr, 0.9f, 1e-4f, rt->d_seed, rt->dt,
+        note(rt, tkm_rt_sgd(rt->d_sgd, rt->n_tensors, rt->sgd_blocks, rt->d_lr, 0.9f, 1e-4f, rt->d_seed, rt->dt,
                             rt->stream), "SGD");
 }
 
@@ -1422,6 +1573,7 @@ static void free_runtime(TkmRuntime *rt) {
     hipFree(rt->pgrad_block);
     hipFree(rt->save_block);
     hipFree(rt->d_sgd);
+    free(rt->clear);
     if (rt->h_pin_lr) hipHostFree(rt->h_pin_lr);
     if (rt->stream) hipStreamDestroy(rt->stream);
     free(rt->tensors);

@@ -19,7 +19,11 @@ typedef struct {
     const float *grad;  /* gradient */
     long long offset;   /* first element in the concatenation of all tensors */
     long long size;
+    long long block0;   /* first SGD block (TKM_SGD_CHUNK elements per block) of this tensor */
 } TkmSgdTensor;
+
+/* Elements one SGD block updates (256 threads x 8). */
+#define TKM_SGD_CHUNK 2048
 
 int tkm_rt_f32_to_16(const float *src, void *dst, size_t n, int dtype, void *stream);
 int tkm_rt_16_to_f32(const void *src, float *dst, size_t n, int dtype, void *stream);
@@ -33,7 +37,9 @@ int tkm_rt_softmax_loss(const void *logits, int dtype, const void *labels, int l
                         int acc_correct, void *stream);
 int tkm_rt_softmax_fwd(const void *x, void *y, int rows, int cols, int dtype, void *stream);
 int tkm_rt_softmax_bwd(const void *p, const void *dp, void *din, int rows, int cols, int dtype, void *stream);
-int tkm_rt_sgd(const TkmSgdTensor *tensors, int nt, long long total, const float *d_lr, float momentum, float wd,
+/* Momentum SGD over every tensor: n_blocks = sum over tensors of ceil(size / TKM_SGD_CHUNK),
+ * block0 the prefix sums. */
+int tkm_rt_sgd(const TkmSgdTensor *tensors, int nt, long long n_blocks, const float *d_lr, float momentum, float wd,
                uint32_t *d_seed, int dtype, void *stream);
 int tkm_rt_perturb(void *p, long long i, float delta, int dtype, void *stream);
 int tkm_rt_add_f32(float *acc, const float *v, void *stream);

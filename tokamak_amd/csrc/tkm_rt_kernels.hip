@@ -139,6 +139,126 @@ __global__ __launch_bounds__(256) void k_softmax_loss(const uint16_t* __restrict
     }
 }
 
+// The same per-row softmax and loss for rows of a multiple of 8 columns, at most 8192: the
+// wave reads its row once into registers (16-byte loads, lane l holding columns
+// (64k + l)*8 .. +7 of chunk k) and runs max, sum and gradient from them, writing dlogits as
+// 16-byte stores.  Per element the arithmetic is the scalar kernel's; the sums run over each
+// lane's elements in column order, then over the wave.
+template <int NCH>
+__global__ __launch_bounds__(256) void k_softmax_loss_v(const uint16_t* __restrict__ logits, int dt,
+                                                        const void* __restrict__ labels, int label_i32,
+                                                        uint16_t* __restrict__ dlogits, float* __restrict__ row_loss,
+                                                        int* __restrict__ row_correct, int rows, int cols,
+                                                        int is_eval, int valid_rows, int loss_kind, float gamma) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const size_t base = (size_t)r * cols;
+    const int nchunk = cols / 8;
+    uint4 x[NCH];
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+        const int ch = k * 64 + lane;
+        x[k] = ch < nchunk ? *(const uint4*)(logits + base + (size_t)ch * 8) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    auto val = [&](const uint4& q, int j) __attribute__((always_inline)) {
+        const int wi = j >> 1;
+        const uint32_t w = wi == 0 ? q.x : (wi == 1 ? q.y : (wi == 2 ? q.z : q.w));
+        const uint16_t b = (uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu));
+        return dt == 1 ? __uint_as_float((uint32_t)b << 16) : __half2float(__ushort_as_half(b));
+    };
+    float mx = -1e30f;
+    int pred = 0x7fffffff;
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+        const int ch = k * 64 + lane;
+        if (ch < nchunk) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = val(x[k], j);
+                if (v > mx) { mx = v; pred = ch * 8 + j; }
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float om = __shfl_xor(mx, o, 64);
+        const int op = __shfl_xor(pred, o, 64);
+        if (om > mx || (om == mx && op < pred)) { mx = om; pred = op; }
+    }
+    if (pred == 0x7fffffff) pred = 0;
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < NCH; ++k)
+        if (k * 64 + lane < nchunk) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) sum += expf(val(x[k], j) - mx);
+        }
+    sum = wave_sum(sum);
+    int lbl = 0;
+    if (labels) lbl = label_i32 ? ((const int32_t*)labels)[r] : (int)((const uint8_t*)labels)[r];
+    if (lbl < 0 || lbl >= cols) lbl = 0;
+    if (lane == 0) row_correct[r] = ((!is_eval || r < valid_rows) && pred == lbl) ? 1 : 0;
+    if (is_eval) {
+        if (lane == 0) row_loss[r] = 0.f;
+        return;
+    }
+    const float inv_rows = 1.0f / (float)rows;
+    float tp = expf(ld16(logits, base + lbl, dt) - mx) / sum;
+    tp = fmaxf(tp, 1e-7f);
+    const float fw = powf(1.0f - tp, gamma);
+    const float fscale = loss_kind == 1 ? fw - gamma * tp * powf(1.0f - tp, gamma - 1.0f) * logf(tp) : 1.0f;
+    float brier = 0.f, mse = 0.f;
+    if (loss_kind == 2) {
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) {
+            const int ch = k * 64 + lane;
+            if (ch < nchunk) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float p = expf(val(x[k], j) - mx) / sum;
+                    const float t = ch * 8 + j == lbl ? 1.0f : 0.0f;
+                    brier += p * (p - t);
+                    mse += (p - t) * (p - t) / (float)cols;
+                }
+            }
+        }
+        brier = wave_sum(brier);
+        mse = wave_sum(mse);
+    }
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+        const int ch = k * 64 + lane;
+        if (ch < nchunk) {
+            uint32_t w[4];
+#pragma unroll
+            for (int j2 = 0; j2 < 4; ++j2) {
+                uint16_t h2[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int j = 2 * j2 + e;
+                    const float p = expf(val(x[k], j) - mx) / sum;
+                    const float t = ch * 8 + j == lbl ? 1.0f : 0.0f;
+                    float g;
+                    if (loss_kind == 0) g = p - t;
+                    else if (loss_kind == 1) g = fscale * (p - t);
+                    else g = (2.0f / (float)cols) * p * ((p - t) - brier);
+                    h2[e] = to16(g * inv_rows, dt);
+                }
+                w[j2] = (uint32_t)h2[0] | ((uint32_t)h2[1] << 16);
+            }
+            *(uint4*)(dlogits + base + (size_t)ch * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
+    if (lane == 0) {
+        float l;
+        if (loss_kind == 0) l = -logf(tp);
+        else if (loss_kind == 1) l = -fw * logf(tp);
+        else l = mse;
+        row_loss[r] = l * inv_rows;
+    }
+}
+
 // Sum of the per-row losses and correct flags in row order (one block of 1024 threads: strided
 // partial sums, then a fixed tree); out[0] += loss, *correct += count when accumulate, else =.
 __global__ __launch_bounds__(1024) void k_loss_reduce(const float* __restrict__ row_loss,
@@ -203,31 +323,65 @@ __global__ __launch_bounds__(256) void k_softmax_bwd(const uint16_t* __restrict_
 // Momentum SGD with the reference's update (tkm_gpu.cu:696-720): decoupled-from-nothing weight
 // decay on tensors that have a 16-bit copy (GEMM weights), then
 //   v = momentum * v + g,  p -= lr * (momentum * v + g)   (Nesterov form),  w16 = round(p).
-// One thread per element; the tensor is found by binary search over the offsets.  Thread 0
-// advances the step seed of the stochastic ops.
-__global__ __launch_bounds__(256) void k_sgd(const TkmSgdTensor* __restrict__ t, int nt, long long total,
+// One block updates TKM_SGD_CHUNK consecutive elements of one tensor, 8 per thread with
+// 16-byte accesses (every tensor starts 256-byte aligned); the block finds its tensor by a
+// binary search over the tensors' first blocks.  Block 0 advances the step seed of the
+// stochastic ops.
+__device__ __forceinline__ void sgd_one(float& p, float& v, float g, float lr, float momentum, float wd, bool decay) {
+    if (decay) g = fmaf(wd, p, g);
+    v = fmaf(momentum, v, g);
+    p = fmaf(-lr, fmaf(momentum, v, g), p);
+}
+
+__global__ __launch_bounds__(256) void k_sgd(const TkmSgdTensor* __restrict__ t, int nt,
                                              const float* __restrict__ d_lr, float momentum, float wd,
                                              uint32_t* __restrict__ d_seed, int dt) {
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx == 0 && d_seed) *d_seed += 0x9E3779B9u;
-    if (idx >= total) return;
+    const long long blk = blockIdx.x;
+    if (blk == 0 && threadIdx.x == 0 && d_seed) *d_seed += 0x9E3779B9u;
     int lo = 0, hi = nt - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (t[mid].offset <= idx) lo = mid; else hi = mid - 1;
+        if (t[mid].block0 <= blk) lo = mid; else hi = mid - 1;
     }
     const TkmSgdTensor tt = t[lo];
-    const long long i = idx - tt.offset;
-    if (i >= tt.size) return;
+    const long long i0 = (blk - tt.block0) * TKM_SGD_CHUNK + (long long)threadIdx.x * 8;
+    if (i0 >= tt.size) return;
     const float lr = *d_lr;
-    float p = tt.master[i];
-    float g = tt.grad[i];
-    if (tt.w16) g = fmaf(wd, p, g);
-    const float v = fmaf(momentum, tt.vel[i], g);
-    p = fmaf(-lr, fmaf(momentum, v, g), p);
-    tt.vel[i] = v;
-    tt.master[i] = p;
-    if (tt.w16) ((uint16_t*)tt.w16)[i] = to16(p, dt);
+    const bool decay = tt.w16 != nullptr;
+    if (i0 + 8 <= tt.size) {
+        float4* mp = (float4*)(tt.master + i0);
+        float4* vp = (float4*)(tt.vel + i0);
+        const float4* gp = (const float4*)(tt.grad + i0);
+        float4 p0 = mp[0], p1 = mp[1], v0 = vp[0], v1 = vp[1];
+        const float4 g0 = gp[0], g1 = gp[1];
+        sgd_one(p0.x, v0.x, g0.x, lr, momentum, wd, decay);
+        sgd_one(p0.y, v0.y, g0.y, lr, momentum, wd, decay);
+        sgd_one(p0.z, v0.z, g0.z, lr, momentum, wd, decay);
+        sgd_one(p0.w, v0.w, g0.w, lr, momentum, wd, decay);
+        sgd_one(p1.x, v1.x, g1.x, lr, momentum, wd, decay);
+        sgd_one(p1.y, v1.y, g1.y, lr, momentum, wd, decay);
+        sgd_one(p1.z, v1.z, g1.z, lr, momentum, wd, decay);
+        sgd_one(p1.w, v1.w, g1.w, lr, momentum, wd, decay);
+        mp[0] = p0;
+        mp[1] = p1;
+        vp[0] = v0;
+        vp[1] = v1;
+        if (decay) {
+            const uint4 w = make_uint4((uint32_t)to16(p0.x, dt) | ((uint32_t)to16(p0.y, dt) << 16),
+                                       (uint32_t)to16(p0.z, dt) | ((uint32_t)to16(p0.w, dt) << 16),
+                                       (uint32_t)to16(p1.x, dt) | ((uint32_t)to16(p1.y, dt) << 16),
+                                       (uint32_t)to16(p1.z, dt) | ((uint32_t)to16(p1.w, dt) << 16));
+            *(uint4*)((uint16_t*)tt.w16 + i0) = w;
+        }
+        return;
+    }
+    for (long long i = i0; i < tt.size; ++i) {
+        float p = tt.master[i], v = tt.vel[i];
+        sgd_one(p, v, tt.grad[i], lr, momentum, wd, decay);
+        tt.vel[i] = v;
+        tt.master[i] = p;
+        if (decay) ((uint16_t*)tt.w16)[i] = to16(p, dt);
+    }
 }
 
 __global__ void k_perturb(uint16_t* __restrict__ p, long long i, float delta, int dt) {
@@ -290,9 +444,20 @@ int tkm_rt_softmax_loss(const void* logits, int dtype, const void* labels, int l
                         int loss_kind, float gamma, float* loss_out, int* correct_out, int acc_loss,
                         int acc_correct, void* stream) {
     if (rows <= 0) return 0;
-    hipLaunchKernelGGL(k_softmax_loss, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream,
-                       (const uint16_t*)logits, dtype, labels, label_i32, (uint16_t*)dlogits, row_loss,
-                       row_correct, rows, cols, is_eval, valid_rows, loss_kind, gamma);
+    const bool vec = cols % 8 == 0 && cols <= 8192 && ((uintptr_t)logits & 15u) == 0 &&
+                     (is_eval || ((uintptr_t)dlogits & 15u) == 0);
+    if (vec && cols <= 2048)
+        hipLaunchKernelGGL(k_softmax_loss_v<4>, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                           (const uint16_t*)logits, dtype, labels, label_i32, (uint16_t*)dlogits, row_loss,
+                           row_correct, rows, cols, is_eval, valid_rows, loss_kind, gamma);
+    else if (vec)
+        hipLaunchKernelGGL(k_softmax_loss_v<16>, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                           (const uint16_t*)logits, dtype, labels, label_i32, (uint16_t*)dlogits, row_loss,
+                           row_correct, rows, cols, is_eval, valid_rows, loss_kind, gamma);
+    else
+        hipLaunchKernelGGL(k_softmax_loss, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                           (const uint16_t*)logits, dtype, labels, label_i32, (uint16_t*)dlogits, row_loss,
+                           row_correct, rows, cols, is_eval, valid_rows, loss_kind, gamma);
     if (status()) return -1;
     hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(1024), 0, (hipStream_t)stream, row_loss, row_correct, rows,
                        loss_out, correct_out, acc_loss, acc_correct);
@@ -313,12 +478,11 @@ int tkm_rt_softmax_bwd(const void* p, const void* dp, void* din, int rows, int c
     return status();
 }
 
-int tkm_rt_sgd(const TkmSgdTensor* tensors, int nt, long long total, const float* d_lr, float momentum, float wd,
+int tkm_rt_sgd(const TkmSgdTensor* tensors, int nt, long long n_blocks, const float* d_lr, float momentum, float wd,
                uint32_t* d_seed, int dtype, void* stream) {
-    if (nt <= 0) return 0;
-    const long long blocks = (total + 255) / 256;
-    hipLaunchKernelGGL(k_sgd, dim3((unsigned)(blocks > 0 ? blocks : 1)), dim3(256), 0, (hipStream_t)stream,
-                       tensors, nt, total, d_lr, momentum, wd, d_seed, dtype);
+    if (nt <= 0 || n_blocks <= 0) return 0;
+    hipLaunchKernelGGL(k_sgd, dim3((unsigned)n_blocks), dim3(256), 0, (hipStream_t)stream, tensors, nt, d_lr,
+                       momentum, wd, d_seed, dtype);
     return status();
 }
 
