@@ -350,3 +350,21 @@ def test_eval_counts_first_maximal_logit(gpu):
     assert rt.eval(x, pred, 3) == 3
     assert rt.eval(x, ((pred + 1) % 4).astype(np.uint8), 4) == 0
     rt.close()
+
+
+def test_two_runtimes_agree_bitwise(gpu):
+    """Two runtimes of one graph with the same initial weights give the same losses and weights,
+    bit for bit, over steps that update the weights: every GEMM algorithm, reduction order and
+    kernel choice is fixed by the graph, not by timing."""
+    from tokamak_amd import runtime as R
+    log("[case] llama_small: two runtimes, bitwise")
+    a = R.Runtime(graph("llama_small"), token_labels=True, init_seed=7)
+    b = R.Runtime(graph("llama_small"), token_labels=True, init_seed=7)
+    x = np.random.default_rng(8).standard_normal(a.input_elements).astype(np.float32)
+    y = _tokens(2, 64, 256, 9)
+    la = [a.step(x, y, 0.02) for _ in range(3)]
+    lb = [b.step(x, y, 0.02) for _ in range(3)]
+    assert la == lb and la[2] < la[0]
+    assert a.save_weights() == b.save_weights()
+    a.close()
+    b.close()

@@ -20,13 +20,7 @@ void tkm_gemm_handle_destroy(void *handle);
  * (n x k if trans_b); A and B of type ab_type, C of c_type. */
 int tkm_gemm_create(tkm_gemm **out, void *handle, int trans_a, int trans_b, int m, int n, int k, int lda, int ldb,
                     int ldc, int ab_type, int c_type, float beta, size_t max_workspace);
-/* Workspace bytes any of the plan's candidate algorithms may need. */
 size_t tkm_gemm_workspace(const tkm_gemm *g);
-/* Times the candidates on these operands (C is written, with the plan's beta) and keeps the
- * fastest; a problem already tuned in this process takes the earlier choice.  Synchronizes
- * the stream; not for use under graph capture. */
-int tkm_gemm_tune(tkm_gemm *g, const void *A, const void *B, void *C, void *workspace, size_t ws_bytes,
-                  void *stream);
 int tkm_gemm_run(const tkm_gemm *g, const void *A, const void *B, void *C, void *workspace, size_t ws_bytes,
                  void *stream);
 void tkm_gemm_destroy(tkm_gemm *g);

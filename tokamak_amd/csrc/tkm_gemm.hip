@@ -6,19 +6,15 @@
 //   forward   out[N x rows]  = W[N x K] . in[K x rows]                       (N, N), beta 0
 //   dW        dW[N x K] fp32 = dout[N x rows] . in^T                         (N, T), beta 0
 //   dX        din[K x rows] += W^T . dout                                    (T, N), beta 1
-// The algorithm is chosen once, at ignite: hipblasLtMatmulAlgoGetHeuristic proposes up to
-// TKM_GEMM_CANDIDATES, and tkm_gemm_tune times them on the runtime's own buffers and keeps the
-// fastest (once per distinct problem in a process).  A launch then enqueues one
-// hipblasLtMatmul on the runtime's stream with a caller-owned workspace, so a captured step
-// replays it without allocation.
+// The algorithm is chosen once, at ignite (hipblasLtMatmulAlgoGetHeuristic); a launch then
+// enqueues one hipblasLtMatmul on the runtime's stream with a caller-owned workspace, so a
+// captured step replays it without allocation.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 #include <stdio.h>
 #include <stdlib.h>
 
 #include "tkm_gemm.h"
-
-#define TKM_GEMM_CANDIDATES 8
 
 struct tkm_gemm {
     hipblasLtHandle_t lt;
@@ -27,10 +23,6 @@ struct tkm_gemm {
     hipblasLtMatmulAlgo_t algo;
     float alpha, beta;
     size_t ws_needed;
-    hipblasLtMatmulAlgo_t cand[TKM_GEMM_CANDIDATES];
-    size_t cand_ws[TKM_GEMM_CANDIDATES];
-    int n_cand;
-    int key[10];              // the problem: transposes, sizes, leading dimensions, types, beta
 };
 
 namespace {
@@ -42,23 +34,6 @@ int fail(const char* what, int st) {
 }
 
 hipDataType dtype_of(int t) { return t == TKM_GEMM_BF16 ? HIP_R_16BF : (t == TKM_GEMM_F32 ? HIP_R_32F : HIP_R_16F); }
-
-// problems already tuned in this process: key -> candidate index
-struct tuned_entry {
-    int key[10];
-    int pick;
-};
-tuned_entry g_tuned[256];
-int g_n_tuned = 0;
-
-int find_tuned(const int* key) {
-    for (int i = 0; i < g_n_tuned; ++i) {
-        bool same = true;
-        for (int j = 0; j < 10; ++j) same = same && g_tuned[i].key[j] == key[j];
-        if (same) return g_tuned[i].pick;
-    }
-    return -1;
-}
 }  // namespace
 
 extern "C" {
@@ -99,10 +74,9 @@ int tkm_gemm_create(tkm_gemm** out, void* handle, int trans_a, int trans_b, int 
     hipblasLtMatmulPreferenceCreate(&pref);
     uint64_t ws = max_workspace;
     hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
-    hipblasLtMatmulHeuristicResult_t res[TKM_GEMM_CANDIDATES];
+    hipblasLtMatmulHeuristicResult_t res[1];
     int found = 0;
-    st = hipblasLtMatmulAlgoGetHeuristic(g->lt, g->desc, g->a, g->b, g->c, g->c, pref, TKM_GEMM_CANDIDATES, res,
-                                         &found);
+    st = hipblasLtMatmulAlgoGetHeuristic(g->lt, g->desc, g->a, g->b, g->c, g->c, pref, 1, res, &found);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (st != HIPBLAS_STATUS_SUCCESS || found < 1) {
         snprintf(g_err, sizeof g_err,
@@ -111,72 +85,13 @@ int tkm_gemm_create(tkm_gemm** out, void* handle, int trans_a, int trans_b, int 
         tkm_gemm_destroy(g);
         return -1;
     }
-    g->n_cand = found < TKM_GEMM_CANDIDATES ? found : TKM_GEMM_CANDIDATES;
-    for (int i = 0; i < g->n_cand; ++i) {
-        g->cand[i] = res[i].algo;
-        g->cand_ws[i] = res[i].workspaceSize;
-    }
     g->algo = res[0].algo;
     g->ws_needed = res[0].workspaceSize;
-    const int key[10] = {trans_a, trans_b, m, n, k, lda, ldb, ldc, ab_type * 4 + c_type, beta != 0.0f};
-    for (int j = 0; j < 10; ++j) g->key[j] = key[j];
     *out = g;
     return 0;
 }
 
-size_t tkm_gemm_workspace(const tkm_gemm* g) {
-    if (!g) return 0;
-    size_t w = g->ws_needed;
-    for (int i = 0; i < g->n_cand; ++i)
-        if (g->cand_ws[i] > w) w = g->cand_ws[i];
-    return w;
-}
-
-int tkm_gemm_tune(tkm_gemm* g, const void* A, const void* B, void* C, void* workspace, size_t ws_bytes,
-                  void* stream) {
-    if (!g || g->n_cand <= 1) return 0;
-    int pick = find_tuned(g->key);
-    if (pick < 0) {
-        hipStream_t st = (hipStream_t)stream;
-        hipEvent_t e0, e1;
-        if (hipEventCreate(&e0) != hipSuccess) return fail("hipEventCreate", -1);
-        if (hipEventCreate(&e1) != hipSuccess) {
-            hipEventDestroy(e0);
-            return fail("hipEventCreate", -1);
-        }
-        float best = 0.0f;
-        for (int i = 0; i < g->n_cand; ++i) {
-            if (g->cand_ws[i] > ws_bytes) continue;
-            // one untimed run (also rejects a candidate the library cannot launch), then 5 timed
-            if (hipblasLtMatmul(g->lt, g->desc, &g->alpha, A, g->a, B, g->b, &g->beta, C, g->c, C, g->c, &g->cand[i],
-                                workspace, ws_bytes, st) != HIPBLAS_STATUS_SUCCESS)
-                continue;
-            hipEventRecord(e0, st);
-            bool ok = true;
-            for (int r = 0; r < 5 && ok; ++r)
-                ok = hipblasLtMatmul(g->lt, g->desc, &g->alpha, A, g->a, B, g->b, &g->beta, C, g->c, C, g->c,
-                                     &g->cand[i], workspace, ws_bytes, st) == HIPBLAS_STATUS_SUCCESS;
-            hipEventRecord(e1, st);
-            float ms = 0.0f;
-            if (!ok || hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) continue;
-            if (pick < 0 || ms < best) {
-                best = ms;
-                pick = i;
-            }
-        }
-        hipEventDestroy(e0);
-        hipEventDestroy(e1);
-        if (pick < 0) pick = 0;
-        if (g_n_tuned < (int)(sizeof g_tuned / sizeof g_tuned[0])) {
-            for (int j = 0; j < 10; ++j) g_tuned[g_n_tuned].key[j] = g->key[j];
-            g_tuned[g_n_tuned++].pick = pick;
-        }
-    }
-    if (pick >= g->n_cand) pick = 0;
-    g->algo = g->cand[pick];
-    g->ws_needed = g->cand_ws[pick];
-    return 0;
-}
+size_t tkm_gemm_workspace(const tkm_gemm* g) { return g ? g->ws_needed : 0; }
 
 int tkm_gemm_run(const tkm_gemm* g, const void* A, const void* B, void* C, void* workspace, size_t ws_bytes,
                  void* stream) {

@@ -85,7 +85,8 @@ typedef struct {
     unsigned gx, gy_fwd, bands, band, gx_red;
     int n_par;                          /* reduce targets (plasma: geometry order; prep: dbias, dgamma) */
     int par_kind[3 * 3 * TKM_PLASMA_MAX_NODES], par_node[3 * 3 * TKM_PLASMA_MAX_NODES];
-    size_t part_bytes;
+    size_t part_bytes, part_off;        /* this group's band partials in the partials block */
+    int pw, chan;                       /* partial row width; channels (prep: C, then QK) */
 } rt_group;
 
 struct TkmRuntime {
@@ -123,6 +124,8 @@ struct TkmRuntime {
     size_t attn_ws_bytes;
     void *part_ws;
     size_t part_ws_bytes;
+    TkmReduceChunk *d_red;              /* parameter-gradient reductions, one launch per step */
+    int n_red;
     float *h_pin_lr, *h_pin_loss;
     hipGraph_t step_graph[2];        /* [0] clears the loss, [1] accumulates it (epochs) */
     hipGraphExec_t step_exec[2];
@@ -596,6 +599,8 @@ static int plan_groups(TkmRuntime *rt) {
             G->bands = (unsigned)tkm_bwd_bands(G->rows, (int)G->gx);
             G->gx_red = (unsigned)((geo.part_width + 63) / 64);
             G->part_bytes = TKM_ALIGN((size_t)G->bands * geo.part_width * sizeof(float));
+            G->pw = geo.part_width;
+            G->chan = geo.C;
             G->n_par = 1 + (d.has_qknorm ? 1 : 0);
             G->par_kind[0] = TKM_ARG_DBIAS;
             G->par_kind[1] = TKM_ARG_DWEIGHT;
@@ -612,6 +617,8 @@ static int plan_groups(TkmRuntime *rt) {
             G->bands = (unsigned)tkm_bwd_bands(G->rows, geo.XB);
             G->gx_red = (unsigned)((geo.part_width + 63) / 64);
             G->part_bytes = geo.n_par ? TKM_ALIGN((size_t)G->bands * geo.part_width * sizeof(float)) : 0;
+            G->pw = geo.part_width;
+            G->chan = geo.C;
             G->n_par = geo.n_par;
             for (int p = 0; p < geo.n_par; ++p) {
                 G->par_kind[p] = geo.par[p].kind;
@@ -623,7 +630,8 @@ static int plan_groups(TkmRuntime *rt) {
             snprintf(name, sizeof name, "tkm_plasma_bwd_g%d_reduce", gid);
             if (tkm_rtc_function(rt->module, name, &G->reduce)) return 0;
         }
-        if (part < G->part_bytes) part = G->part_bytes;
+        G->part_off = part;                 /* each group's partials stay until the step's reduction */
+        part += G->part_bytes;
     }
     rt->part_ws_bytes = part;
     if (part && !HIP_OK(hipMalloc(&rt->part_ws, part))) return 0;
@@ -631,7 +639,7 @@ static int plan_groups(TkmRuntime *rt) {
 }
 
 static void free_runtime(TkmRuntime *rt);
-static int tune_gemms(TkmRuntime *rt);
+static int plan_reductions(TkmRuntime *rt);
 
 TkmRuntime *tkm_runtime_ignite_ex(const TkmGraph *g, const char *src, const tkm_runtime_opts *o) {
     if (!g) return NULL;
@@ -738,7 +746,7 @@ TkmRuntime *tkm_runtime_ignite_ex(const TkmGraph *g, const char *src, const tkm_
         *rt->h_pin_lr = 1e-3f;
     }
     if (!alloc_params(rt) || !alloc_saves(rt) || !plan_groups(rt) || !plan_grad_writes(rt) || !plan_gemms(rt) ||
-        !tune_gemms(rt))
+        (rt->training && !plan_reductions(rt)))
         goto fail;
     free(own_src);
     if (opts.verbose)
@@ -773,26 +781,6 @@ static uint8_t *grd(TkmRuntime *rt, int nid) { return rt->grad_arena + rt->graph
 static float *tensor_master(TkmRuntime *rt, int t) { return t >= 0 ? rt->tensors[t].master : NULL; }
 static float *tensor_grad(TkmRuntime *rt, int t) { return t >= 0 ? rt->tensors[t].grad : NULL; }
 
-/* Times each GEMM plan's candidate algorithms on the runtime's own buffers and keeps the
- * fastest (tkm_gemm_tune; outputs are scratch at this point: activations, gradients and the
- * gradient arena are rewritten by every step). */
-static int tune_gemms(TkmRuntime *rt) {
-    const TkmGraph *g = &rt->graph;
-    for (int i = 1; i < g->num_nodes; ++i) {
-        const TkmNode *n = &g->nodes[i];
-        if (n->dead || !is_gemm(n->op) || n->plasma_grp >= 0) continue;
-        rt_node *st = &rt->nodes[i];
-        rt_tensor *t = &rt->tensors[st->t_w];
-        if (tkm_gemm_tune(st->g_fwd, t->w16, act(rt, n->in0), act(rt, i), rt->gemm_ws, rt->gemm_ws_bytes, rt->stream))
-            return 0;
-        if (!rt->training) continue;
-        if (tkm_gemm_tune(st->g_dw, grd(rt, i), act(rt, n->in0), t->grad, rt->gemm_ws, rt->gemm_ws_bytes, rt->stream) ||
-            tkm_gemm_tune(st->g_dx, t->w16, grd(rt, i), grd(rt, n->in0), rt->gemm_ws, rt->gemm_ws_bytes, rt->stream))
-            return 0;
-    }
-    return HIP_OK(hipStreamSynchronize(rt->stream));
-}
-
 /* Resolves a plan parameter (the reference's resolve_arg_ptr, src/tkm_gpu.cu:1142-1164). */
 static void resolve(TkmRuntime *rt, const rt_group *G, const PlasmaGroup *pg, const tkm_kparam *p, int bwd,
                     void **val, int *ival) {
@@ -814,7 +802,7 @@ static void resolve(TkmRuntime *rt, const rt_group *G, const PlasmaGroup *pg, co
         case TKM_ARG_SEED: *val = rt->d_seed; break;
         case TKM_ARG_BRANCH_IN: *val = act(rt, g->nodes[nid].in1); break;
         case TKM_ARG_DBRANCH: *val = grd(rt, g->nodes[nid].in1); break;
-        case TKM_KP_PART: *val = rt->part_ws; break;
+        case TKM_KP_PART: *val = (uint8_t *)rt->part_ws + G->part_off; break;
         case TKM_KP_ROWS: *ival = G->rows; break;
         case TKM_KP_BAND: *ival = (int)G->band; break;
         case TKM_KP_ACC:
@@ -846,34 +834,53 @@ static void launch_group(TkmRuntime *rt, int gid, int bwd) {
     snprintf(what, sizeof what, "group %d %s", gid, bwd ? "backward" : "forward");
     note(rt, tkm_rtc_launch(bwd ? G->bwd : G->fwd, G->gx, bwd ? G->bands : G->gy_fwd, 256, kargs, rt->stream, what),
          what);
-    if (!bwd || G->n_par == 0) return;
-    /* parameter gradients: partial rows of the bands, summed in order */
-    void *part = rt->part_ws;
-    int bands = (int)G->bands, acc = 1;
-    void *dst[3 * 3 * TKM_PLASMA_MAX_NODES];
-    void *rargs[3 + 3 * 3 * TKM_PLASMA_MAX_NODES];
-    for (int p = 0; p < G->n_par; ++p) {
-        const rt_node *st = &rt->nodes[G->chain[G->par_node[p]]];
-        const int t = G->par_kind[p] == TKM_ARG_DWEIGHT ? st->t_wvec : G->par_kind[p] == TKM_ARG_DBETA ? st->t_beta
-                                                                                                         : st->t_bias;
-        dst[p] = tensor_grad(rt, t);
+}
+
+/* The table of parameter-gradient reductions: each group's band partials (its own slice of the
+ * partials block) into its parameters' gradients, 64 columns per entry.  Plasma groups lay
+ * parameter p out at columns [p*C, (p+1)*C); the qkv-prep d(bias) at [0, C), d(gamma) after. */
+static int plan_reductions(TkmRuntime *rt) {
+    const TkmGraph *g = &rt->graph;
+    int n = 0, cap = 0;
+    TkmReduceChunk *h = NULL;
+    for (int pass = 0; pass < 2; ++pass) {
+        for (int gid = 0; gid < g->num_groups; ++gid) {
+            const rt_group *G = &rt->groups[gid];
+            if (G->kind < 0 || G->n_par == 0) continue;
+            for (int p = 0; p < G->n_par; ++p) {
+                const rt_node *st = &rt->nodes[G->chain[G->par_node[p]]];
+                const int t = G->par_kind[p] == TKM_ARG_DWEIGHT ? st->t_wvec
+                              : G->par_kind[p] == TKM_ARG_DBETA ? st->t_beta : st->t_bias;
+                const int col0 = G->kind == TKM_HIP_GROUP_PREP ? (p == 0 ? 0 : G->chan) : p * G->chan;
+                const int ncols = G->kind == TKM_HIP_GROUP_PREP ? (p == 0 ? G->chan : G->pw - G->chan) : G->chan;
+                float *dst = tensor_grad(rt, t);
+                if (!dst) continue;
+                for (int c = 0; c < ncols; c += 64, ++n) {
+                    if (pass == 0) continue;
+                    h[n].part = (const float *)((uint8_t *)rt->part_ws + G->part_off);
+                    h[n].dst = dst + c;
+                    h[n].pw = G->pw;
+                    h[n].bands = (int)G->bands;
+                    h[n].col0 = col0 + c;
+                    h[n].ncols = ncols - c < 64 ? ncols - c : 64;
+                }
+            }
+        }
+        if (pass == 0) {
+            cap = n;
+            n = 0;
+            if (cap == 0) break;
+            h = (TkmReduceChunk *)calloc((size_t)cap, sizeof *h);
+            if (!h) return 0;
+        }
     }
-    int n = 0;
-    if (G->kind == TKM_HIP_GROUP_PREP) {   /* (part, dbias, dgamma, bands, accumulate) */
-        void *dg = G->n_par > 1 ? dst[1] : dst[0];
-        rargs[n++] = &part;
-        rargs[n++] = &dst[0];
-        rargs[n++] = &dg;
-        rargs[n++] = &bands;
-        rargs[n++] = &acc;
-        note(rt, tkm_rtc_launch(G->reduce, G->gx_red, 1, 1024, rargs, rt->stream, "qkv-prep reduce"), "reduce");
-    } else {                                /* (part, bands, acc_params, dst...) */
-        rargs[n++] = &part;
-        rargs[n++] = &bands;
-        rargs[n++] = &acc;
-        for (int p = 0; p < G->n_par; ++p) rargs[n++] = &dst[p];
-        note(rt, tkm_rtc_launch(G->reduce, G->gx_red, 1, 1024, rargs, rt->stream, "plasma reduce"), "reduce");
-    }
+    rt->n_red = n;
+    int ok = 1;
+    if (n > 0)
+        ok = HIP_OK(hipMalloc((void **)&rt->d_red, (size_t)n * sizeof *h)) &&
+             HIP_OK(hipMemcpy(rt->d_red, h, (size_t)n * sizeof *h, hipMemcpyHostToDevice));
+    free(h);
+    return ok;
 }
 
 static float attn_scale(int D) { return 1.0f / sqrtf((float)D); }
@@ -927,7 +934,6 @@ static void record_step(TkmRuntime *rt, int clear_loss) {
     for (int c = 0; c < rt->n_clear; ++c)
         note(rt, tkm_rt_fill_u32(rt->grad_arena + rt->clear[c][0], rt->clear[c][1], 0, rt->stream),
              "gradient slot clear");
-    if (rt->pgrad_bytes) note(rt, tkm_rt_fill_u32(rt->pgrad_block, rt->pgrad_bytes, 0, rt->stream), "gradient clear");
     forward_pass(rt, 0, B);
     unsigned char done[TKM_MAX_GROUPS] = {0};
     for (int i = g->num_nodes - 1; i >= 1; --i) {
@@ -960,6 +966,9 @@ static void record_step(TkmRuntime *rt, int clear_loss) {
                  "softmax backward");
         }
     }
+    /* parameter gradients: every group's band partials, summed in one launch (each gradient
+     * has one producer and is overwritten; gradients nothing writes stay zero) */
+    note(rt, tkm_rt_reduce_parts(rt->d_red, rt->n_red, rt->stream), "parameter-gradient reductions");
     if (rt->total_elems > 0)
         note(rt, tkm_rt_sgd(rt->d_sgd, rt->n_tensors, rt->sgd_blocks, rt->d_lr, 0.9f, 1e-4f, rt->d_seed, rt->dt,
                             rt->stream), "SGD");
@@ -1568,6 +1577,7 @@ static void free_runtime(TkmRuntime *rt) {
     hipFree(rt->row_correct);
     hipFree(rt->attn_ws);
     hipFree(rt->part_ws);
+    hipFree(rt->d_red);
     hipFree(rt->gemm_ws);
     hipFree(rt->param_block);
     hipFree(rt->pgrad_block);

@@ -25,6 +25,14 @@ typedef struct {
 /* Elements one SGD block updates (256 threads x 8). */
 #define TKM_SGD_CHUNK 2048
 
+/* Up to 64 columns of one group's band partials of parameter gradients: dst[c] = sum over
+ * bands b of part[b * pw + col0 + c], c < ncols (overwritten). */
+typedef struct {
+    const float *part;
+    float *dst;
+    int pw, bands, col0, ncols;
+} TkmReduceChunk;
+
 int tkm_rt_f32_to_16(const float *src, void *dst, size_t n, int dtype, void *stream);
 int tkm_rt_16_to_f32(const void *src, float *dst, size_t n, int dtype, void *stream);
 int tkm_rt_fill_u32(void *dst, size_t bytes, uint32_t value, void *stream);
@@ -41,6 +49,9 @@ int tkm_rt_softmax_bwd(const void *p, const void *dp, void *din, int rows, int c
  * block0 the prefix sums. */
 int tkm_rt_sgd(const TkmSgdTensor *tensors, int nt, long long n_blocks, const float *d_lr, float momentum, float wd,
                uint32_t *d_seed, int dtype, void *stream);
+/* Every chunk of the table, one block each (the band sums in the order of the generated
+ * per-group reduce kernels). */
+int tkm_rt_reduce_parts(const TkmReduceChunk *chunks, int n, void *stream);
 int tkm_rt_perturb(void *p, long long i, float delta, int dtype, void *stream);
 int tkm_rt_add_f32(float *acc, const float *v, void *stream);
 int tkm_rt_gather(const void *images, const uint8_t *labels, const uint32_t *order, long long first, int B,

@@ -384,6 +384,26 @@ __global__ __launch_bounds__(256) void k_sgd(const TkmSgdTensor* __restrict__ t,
     }
 }
 
+// Parameter gradients of every group from their band partials, in one launch at the end of
+// the backward: per 64 columns, 16 waves sum bands w, w+16, ... and wave 0 adds the 16 sums in
+// order, as the generated per-group reduce kernels do.
+__global__ __launch_bounds__(1024) void k_reduce_parts(const TkmReduceChunk* __restrict__ t) {
+    const TkmReduceChunk e = t[blockIdx.x];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float acc = 0.f;
+    if (lane < e.ncols) {
+#pragma unroll 4
+        for (int b = wave; b < e.bands; b += 16) acc += e.part[(size_t)b * e.pw + e.col0 + lane];
+    }
+    __shared__ float red[16][64];
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0 || lane >= e.ncols) return;
+    float sum = red[0][lane];
+    for (int q = 1; q < 16; ++q) sum += red[q][lane];
+    e.dst[lane] = sum;
+}
+
 __global__ void k_perturb(uint16_t* __restrict__ p, long long i, float delta, int dt) {
     p[i] = to16(ld16(p, (size_t)i, dt) + delta, dt);
 }
@@ -483,6 +503,12 @@ int tkm_rt_sgd(const TkmSgdTensor* tensors, int nt, long long n_blocks, const fl
     if (nt <= 0 || n_blocks <= 0) return 0;
     hipLaunchKernelGGL(k_sgd, dim3((unsigned)n_blocks), dim3(256), 0, (hipStream_t)stream, tensors, nt, d_lr,
                        momentum, wd, d_seed, dtype);
+    return status();
+}
+
+int tkm_rt_reduce_parts(const TkmReduceChunk* chunks, int n, void* stream) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_reduce_parts, dim3((unsigned)n), dim3(1024), 0, (hipStream_t)stream, chunks);
     return status();
 }
 
