@@ -53,6 +53,17 @@ TKM_API char *tkm_codegen_hip_source(const TkmGraph *g, int dtype);
  * them (src/tkm_registry.c:43-456); the runtime allocates parameters and saved state by them. */
 TKM_API uint32_t tkm_hip_res_flags(const TkmNode *n);
 
+/* Pointwise ops' code.  With the front end linked, the generator pastes each pointwise op's
+ * code as the registry holds it (TkmOpSpec fwd_cuda / bwd_cuda, or the user formulas
+ * fwd_expr / bwd_expr), as the reference's generator does, and takes ops it has no formula of
+ * its own for (TKM_OP_FORMULA*); without the front end it uses this build's own formulas of
+ * the ops it knows.  mode 1 (default): as described; 0: this build's formulas for every op it
+ * knows; 2: every pointwise op as an op unknown to this build (the TKM_OP_FORMULA* path a new
+ * registry op takes).  Process-wide; read when a source is generated (tkm_codegen_*, ignite). */
+TKM_API void tkm_hip_use_registry_code(int mode);
+/* 1 when the registry is linked (tkm_find_spec_by_node resolves). */
+TKM_API int tkm_hip_registry_linked(void);
+
 /* ---- run-time options ------------------------------------------------------------------- */
 
 typedef struct {

@@ -60,6 +60,13 @@ enum {
     TKM_OP_DROP,            /* Drop: keep with probability 1 - fval, scaled by 1 / (1 - fval); the
                                mask is drawn per channel pair from the node's generator, seeded by
                                the step seed (registry src/tkm_registry.c:426-434)  (mask, seed) */
+    TKM_OP_FORMULA,         /* a pointwise op of the reference registry that this build has no
+                               formula of its own for: its TkmOpSpec code (fwd_cuda / bwd_cuda,
+                               or fwd_expr / bwd_expr) is emitted as the registry holds it.  Only
+                               the whole-graph generator (tkm_codegen_hip.c, front end linked)
+                               can give it; the descriptor API rejects it                    */
+    TKM_OP_FORMULA_W,       /* the same with a weight vector                          (param w) */
+    TKM_OP_FORMULA_B,       /* the same with a bias vector                            (param b) */
     TKM_OP_COUNT
 };
 

@@ -3,7 +3,8 @@ compiled against the reference's own header and linked with the reference's unch
 (src/tkm_core.c, src/tkm_registry.c) and libtkm_hip.so (oracle/Makefile, target `driver`, built
 in the build container; the binary travels under oracle/_ref/).  On the GPU it runs the
 reference CLI's gradient-check protocol through tkm_load_string, and trains a model file
-loaded with tkm_load_file, saving and reloading its TKM1 weights."""
+loaded with tkm_load_file, saving and reloading its TKM1 weights, and checks the registry-code
+paths of the generator (pointwise ops pasted from the registry) against its own formulas."""
 import os
 import subprocess
 
@@ -40,4 +41,16 @@ def test_c_driver_numcheck(gpu, tmp_path):
 def test_c_driver_trains_model_file(gpu, tmp_path):
     model = os.path.join(HERE, "golden", "models", "llama_small.tkm")
     r = _run(["train", model, "2", "6", "0.01", str(tmp_path / "w.bin")], tmp_path)
+    assert r.returncode == 0 and "PASS" in r.stdout
+
+
+@needs_driver
+def test_c_driver_registry_code_agrees(gpu, tmp_path):
+    """One training step of pointwise_mix.tkm (every pointwise op of the registry that has code
+    there, in FC-anchored chains) with the registry's pasted code, with this build's formulas,
+    and through the path of an op unknown to this build: the last two code paths are the same
+    code and agree bit for bit; this build's formulas agree with the registry's code to
+    rounding (loss 1e-3, input gradient 2e-2 of its largest value, updated weights 1e-4)."""
+    model = os.path.join(HERE, "golden", "models", "pointwise_mix.tkm")
+    r = _run(["registry", model, "2", str(tmp_path)], tmp_path)
     assert r.returncode == 0 and "PASS" in r.stdout

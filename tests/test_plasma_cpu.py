@@ -27,19 +27,21 @@ from tokamak_amd import plasma, prep
 
 RNG = np.random.default_rng(77)
 OPS = plasma.OPS
-POINTWISE = [n for n in plasma.OP_NAMES if n not in ("RMSNorm", "LN", "BN", "L2Norm", "Add", "Drop")]
+POINTWISE = [n for n in plasma.OP_NAMES
+             if n not in ("RMSNorm", "LN", "BN", "L2Norm", "Add", "Drop") + plasma.FORMULA_OPS]
 
 
 # ---- op table ----------------------------------------------------------------------------
 
 def test_op_numbering_and_flags_agree():
-    assert len(plasma.OP_NAMES) == 30
+    assert len(plasma.OP_NAMES) == 33
     want = {"Bias": oracle.PR_BIAS, "RMSNorm": oracle.PR_W | oracle.PR_NORM,
             "LN": oracle.PR_W | oracle.PR_BETA | oracle.PR_NORM, "BN": oracle.PR_W | oracle.PR_BETA | oracle.PR_NORM,
             "L2Norm": oracle.PR_NORM, "LayerScale": oracle.PR_W, "DyT": oracle.PR_W, "PReLU": oracle.PR_W,
             "xATLU": oracle.PR_W, "Add": oracle.PR_BRANCH, "Drop": oracle.PR_MASK}
     for name, code in OPS.items():
-        assert oracle.plasma_flags(code) == want.get(name, 0), name
+        if name not in plasma.FORMULA_OPS:
+            assert oracle.plasma_flags(code) == want.get(name, 0), name
     # defaults of the registry (src/tkm_registry.c)
     L = plasma.lib()
     defaults = {"BN": 1e-2, "LN": 1e-5, "RMSNorm": 1e-5, "L2Norm": 1e-5, "LeakyReLU": 0.01, "ELU": 1.0,
@@ -359,3 +361,13 @@ def test_null_handles_rejected():
     assert L.tkm_plasma_bwd(None, None, 4, 0, None, 0, None) == -1
     assert L.tkm_plasma_bwd_workspace_bytes(None, 4) == 0
     L.tkm_plasma_destroy(None)
+
+
+@pytest.mark.parametrize("name", plasma.FORMULA_OPS)
+def test_descriptor_api_rejects_registry_only_ops(name):
+    """Formula, FormulaW and FormulaB carry no formula of this build: only the whole-graph
+    generator, given the registry's code, can emit them."""
+    d = plasma.make_desc(64, ["Bias", name])
+    with pytest.raises(plasma.AttnError) as e:
+        plasma.source(d)
+    assert "registry" in str(e.value)

@@ -80,7 +80,7 @@ def test_op_mapping_matches_registry():
             mapped.add(e["name"])
         else:
             assert code == -1, e["name"]
-    assert mapped == set(plasma.OP_NAMES)
+    assert mapped == set(plasma.OP_NAMES) - set(plasma.FORMULA_OPS)
     assert REGISTRY[62]["name"] == "Softplus" and REGISTRY[63]["name"] == "Snake"
 
 

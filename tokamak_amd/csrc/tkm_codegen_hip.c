@@ -35,7 +35,43 @@
  * src/tkm_registry.c:445-455); pinned against the registry by tests/test_tkm_runtime_cpu.py. */
 enum { SPEC_SOFTPLUS = 62, SPEC_SNAKE = 63 };
 
+/* The registry (the reference's tkm_registry.c) is part of the front end, which the
+ * application links; without it the generator uses this build's own op formulas. */
+#pragma weak tkm_find_spec_by_node
+
+static int g_registry_code = 1;
+
+void tkm_hip_use_registry_code(int mode) { g_registry_code = mode < 0 ? 0 : (mode > 2 ? 2 : mode); }
+
+int tkm_hip_registry_linked(void) { return tkm_find_spec_by_node != NULL; }
+
+static const TkmOpSpec *registry_spec(const TkmNode *n) {
+    return tkm_find_spec_by_node ? tkm_find_spec_by_node(n) : NULL;
+}
+
+/* A pointwise op of the registry with code the generator can paste (CUDA snippets or a user
+ * formula, both directions). */
+static int has_pointwise_code(const TkmOpSpec *sp) {
+    return sp && sp->cat == CAT_FLUID && ((sp->fwd_cuda && sp->bwd_cuda) || (sp->fwd_expr && sp->bwd_expr));
+}
+
+/* An op this build has no formula of its own for: the registry's code, by its parameters. */
+static int formula_op(const TkmNode *n) {
+    const TkmOpSpec *sp = registry_spec(n);
+    if (!has_pointwise_code(sp)) return -1;
+    switch (sp->res_flags) {
+        case RES_NONE: return TKM_OP_FORMULA;
+        case RES_PARAM_WEIGHT: return TKM_OP_FORMULA_W;
+        case RES_PARAM_BIAS: return TKM_OP_FORMULA_B;
+        default: return -1;
+    }
+}
+
 int tkm_hip_plasma_op(const TkmNode *n) {
+    if (g_registry_code == 2) {         /* every pointwise op as an op unknown to this build */
+        const int f = formula_op(n);
+        if (f >= 0) return f;
+    }
     switch (n->op) {
         case OP_BIAS: return TKM_OP_BIAS;
         case OP_RMSNORM: return TKM_OP_RMSNORM;
@@ -68,8 +104,27 @@ int tkm_hip_plasma_op(const TkmNode *n) {
         case OP_USER_FLUID:
             if (n->spec_id == SPEC_SOFTPLUS) return TKM_OP_SOFTPLUS;
             if (n->spec_id == SPEC_SNAKE) return TKM_OP_SNAKE;
-            return -1;
-        default: return -1;
+            return formula_op(n);
+        default: return formula_op(n);
+    }
+}
+
+/* The registry's code of each chain position's op (g_registry_code and the front end linked),
+ * for the pointwise ops that have it; all-NULL otherwise. */
+static void group_formulas(const TkmGraph *g, const tkm_plasma_desc *d, const int *map, int nm,
+                           tkm_plasma_formula *out) {
+    memset(out, 0, sizeof(tkm_plasma_formula) * 3 * TKM_PLASMA_MAX_NODES);
+    for (int k = 0; k < nm; ++k) {
+        const TkmNode *n = &g->nodes[map[k]];
+        const int op = k < (d->twin ? d->n_left : 0) ? d->left_ops[k].op
+                       : k < (d->twin ? d->n_left + d->n_right : 0) ? d->right_ops[k - d->n_left].op
+                       : d->main_ops[k - (d->twin ? d->n_left + d->n_right : 0)].op;
+        const TkmOpSpec *sp = registry_spec(n);
+        const int forced = op == TKM_OP_FORMULA || op == TKM_OP_FORMULA_W || op == TKM_OP_FORMULA_B;
+        if (!has_pointwise_code(sp) || !tkm_plasma_op_pointwise(op) || (!g_registry_code && !forced)) continue;
+        out[k].expr = sp->fwd_cuda ? 0 : 1;
+        out[k].fwd = sp->fwd_cuda ? sp->fwd_cuda : sp->fwd_expr;
+        out[k].bwd = sp->bwd_cuda ? sp->bwd_cuda : sp->bwd_expr;
     }
 }
 
@@ -167,7 +222,9 @@ int tkm_hip_plasma_desc(const TkmGraph *g, int gid, int dtype, tkm_plasma_desc *
     if (rc) return rc;
     if (chain_nodes)
         for (int i = 0; i < nm; ++i) chain_nodes[i] = map[i];
-    return tkm_plasma_check_desc(d);
+    tkm_plasma_formula f[3 * TKM_PLASMA_MAX_NODES];
+    group_formulas(g, d, map, nm, f);
+    return tkm_plasma_check_desc_f(d, f);
 }
 
 /* Internal (kind, chain index) of a signature argument, or TKM_KP_UNUSED.  map: chain index ->
@@ -299,8 +356,13 @@ char *tkm_codegen_hip_source(const TkmGraph *g, int dtype) {
                 if (!rc) rc = tkm_prep_emit(&s, &d, &fp, &bp, 1);
             } else {
                 tkm_plasma_desc d;
-                rc = tkm_hip_plasma_desc(g, gid, dtype, &d, NULL);
-                if (!rc) rc = tkm_plasma_emit(&s, &d, &fp, &bp, 1);
+                int map[3 * TKM_PLASMA_MAX_NODES];
+                tkm_plasma_formula f[3 * TKM_PLASMA_MAX_NODES];
+                rc = tkm_hip_plasma_desc(g, gid, dtype, &d, map);
+                if (!rc) {
+                    group_formulas(g, &d, map, d.twin ? d.n_left + d.n_right + d.n_main : d.n_main, f);
+                    rc = tkm_plasma_emit(&s, &d, &fp, &bp, 1, f);
+                }
             }
         }
         if (rc) {

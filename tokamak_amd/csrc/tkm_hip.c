@@ -51,6 +51,7 @@
 #pragma weak tkm_parse_dsl
 #pragma weak tkm_optimize_and_bind
 #pragma weak tkm_plan_memory
+#pragma weak tkm_find_spec_by_node
 
 #define TKM_GEMM_MAX_WS (64u << 20)
 #define TKM_ALIGN(x) (((x) + 255) & ~(size_t)255)
@@ -172,6 +173,10 @@ static void note(TkmRuntime *rt, int rc, const char *what) {
 /* ---- op resources (the registry's resource flags, src/tkm_registry.c:43-456) -------------- */
 
 uint32_t tkm_hip_res_flags(const TkmNode *n) {
+    /* with the front end linked, the registry's own flags (equal for every op this table
+     * knows: tests/test_tkm_runtime_cpu.py; also those of ops it does not) */
+    const TkmOpSpec *sp = tkm_find_spec_by_node ? tkm_find_spec_by_node(n) : NULL;
+    if (sp) return sp->res_flags;
     switch (n->op) {
         case OP_BN: case OP_LN: return RES_PARAM_WEIGHT | RES_PARAM_BETA | RES_SAVE_ISTD | RES_SAVE_XHAT;
         case OP_RMSNORM: return RES_PARAM_WEIGHT | RES_SAVE_ISTD | RES_SAVE_XHAT;

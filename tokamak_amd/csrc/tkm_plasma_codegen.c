@@ -15,6 +15,7 @@
  *     through LDS in a fixed order into one partial row per band, and a reduce kernel (16
  *     waves per column group) adds the bands in order (no atomics).
  */
+#include <ctype.h>
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -92,7 +93,16 @@ static const op_info OPS[TKM_OP_COUNT] = {
                       "g *= 1.0f + sinf(2.0f * fv * p);"},
     [TKM_OP_ADD] = {"Add", F_BRANCH, 0.0f, NULL, NULL},
     [TKM_OP_DROP] = {"Drop", F_MASK | F_SEED, 0.1f, NULL, NULL},
+    [TKM_OP_FORMULA] = {"Formula", 0, 0.0f, NULL, NULL},
+    [TKM_OP_FORMULA_W] = {"FormulaW", F_W, 0.0f, NULL, NULL},
+    [TKM_OP_FORMULA_B] = {"FormulaB", F_BIAS, 0.0f, NULL, NULL},
 };
+
+int tkm_plasma_op_pointwise(int op) {
+    return op >= 0 && op < TKM_OP_COUNT && !(OPS[op].flags & (F_NORM | F_MASK | F_BRANCH | F_BETA));
+}
+
+static int is_formula_op(int op) { return op == TKM_OP_FORMULA || op == TKM_OP_FORMULA_W || op == TKM_OP_FORMULA_B; }
 
 float tkm_plasma_default_fval(int op) { return (op >= 0 && op < TKM_OP_COUNT) ? OPS[op].fval : 0.0f; }
 
@@ -116,7 +126,9 @@ static const tkm_plasma_node *node_at(const tkm_plasma_desc *d, int k) {
 
 static int n_nodes(const tkm_plasma_desc *d) { return d->twin ? d->n_left + d->n_right + d->n_main : d->n_main; }
 
-int tkm_plasma_check_desc(const tkm_plasma_desc *d) {
+int tkm_plasma_check_desc(const tkm_plasma_desc *d) { return tkm_plasma_check_desc_f(d, NULL); }
+
+int tkm_plasma_check_desc_f(const tkm_plasma_desc *d, const tkm_plasma_formula *formulas) {
     if (!d) return tkm_set_error(TKM_ATTN_EINVAL, "descriptor is NULL");
     if (d->channels <= 0 || d->channels % 2 != 0 || d->channels > (1 << 20))
         return tkm_set_error(TKM_ATTN_EUNSUPPORTED, "channels %d: must be positive, even and at most 2^20",
@@ -131,6 +143,11 @@ int tkm_plasma_check_desc(const tkm_plasma_desc *d) {
     for (int k = 0; k < n_nodes(d); ++k) {
         const tkm_plasma_node *n = node_at(d, k);
         if (n->op < 0 || n->op >= TKM_OP_COUNT) return tkm_set_error(TKM_ATTN_EINVAL, "node %d: unknown op %d", k, n->op);
+        if (is_formula_op(n->op) && !(formulas && formulas[k].fwd && formulas[k].bwd))
+            return tkm_set_error(TKM_ATTN_EUNSUPPORTED, "node %d: %s needs the registry's code of its op (whole-graph "
+                                 "generator with the front end linked)", k, OPS[n->op].name);
+        if (formulas && formulas[k].fwd && !tkm_plasma_op_pointwise(n->op))
+            return tkm_set_error(TKM_ATTN_EINVAL, "node %d: %s does not take registry code", k, OPS[n->op].name);
         if (!isfinite(n->fval)) return tkm_set_error(TKM_ATTN_EINVAL, "node %d: fval must be finite", k);
         const int f = OPS[n->op].flags;
         const int in_gate = d->twin && k < d->n_left + d->n_right;
@@ -329,6 +346,98 @@ static void emit_param_loads(sbuf *s, const tkm_plasma_desc *d, const tkm_plasma
     }
 }
 
+/* ---- registry code of pointwise ops ---------------------------------------------------------
+ * The reference's generator pastes a pointwise op's TkmOpSpec code into its per-channel-pair
+ * kernels (src/tkm_codegen.c:296-357, 404-460).  Here each pair of a lane's chunk runs the same
+ * code in a block of its own that declares what the code reads: v (forward) or dy and pre
+ * (backward) as float2, fval, w_vec / b_vec with the pair at tid = 0, and acc_dw / acc_db for
+ * the parameter gradients, which then join this kernel's band sums. */
+
+/* A user formula in x and fval (TkmOpSpec fwd_expr / bwd_expr) with x replaced by `xname`,
+ * pi by its value and the math functions by their float versions, as the reference's
+ * generator translates them (src/tkm_codegen.c:72-103); everything else unchanged. */
+static void emit_expr(sbuf *s, const char *expr, const char *xname) {
+    static const char *const map[][2] = {{"exp", "expf"}, {"log", "logf"}, {"ln", "logf"}, {"sqrt", "sqrtf"},
+                                         {"sin", "sinf"}, {"cos", "cosf"}, {"tanh", "tanhf"}, {"abs", "fabsf"},
+                                         {"max", "fmaxf"}, {"min", "fminf"}, {"pow", "powf"}};
+    for (const char *p = expr; *p;) {
+        if (isalpha((unsigned char)*p) || *p == '_') {
+            char name[32];
+            int len = 0;
+            while ((isalnum((unsigned char)*p) || *p == '_')) {
+                if (len < (int)sizeof name - 1) name[len++] = *p;
+                ++p;
+            }
+            name[len] = '\0';
+            const char *out = name;
+            if (!strcmp(name, "x")) out = xname;
+            else if (!strcmp(name, "pi")) out = "3.14159265358979323846f";
+            for (size_t i = 0; i < sizeof map / sizeof map[0]; ++i)
+                if (!strcmp(name, map[i][0])) out = map[i][1];
+            sb_add(s, "%s", out);
+        } else {
+            sb_add(s, "%c", *p++);
+        }
+    }
+}
+
+static void emit_pair_params(sbuf *s, int flags, int k, const char *pad) {
+    if (flags & F_W) sb_add(s, "%sconst float2 wv_[1] = {make_float2(w%d[j], w%d[j + 1])};\n", pad, k, k);
+    if (flags & F_BIAS) sb_add(s, "%sconst float2 bv_[1] = {make_float2(bias%d[j], bias%d[j + 1])};\n", pad, k, k);
+}
+
+static void emit_registry_forward(sbuf *s, const tkm_plasma_formula *f, int flags, int k, const char *v) {
+    sb_add(s, "            /* the registry's code of this op */\n");
+    sb_add(s, "#pragma unroll\n            for (int j = 0; j < TKM_CW; j += 2) {\n");
+    sb_add(s, "                const float2 in_ = make_float2(%s[j], %s[j + 1]);\n", v, v);
+    emit_pair_params(s, flags, k, "                ");
+    sb_add(s, "                float2 out_;\n                {\n");
+    sb_add(s, "                    float2 v = in_; const float fval = fv; const int tid = 0; (void)fval; (void)tid;\n");
+    if (flags & F_W) sb_add(s, "                    const float2 *w_vec = wv_; (void)w_vec;\n");
+    if (flags & F_BIAS) sb_add(s, "                    const float2 *b_vec = bv_; (void)b_vec;\n");
+    if (f->expr) {
+        sb_add(s, "                    v.x = ");
+        emit_expr(s, f->fwd, "v.x");
+        sb_add(s, ";\n                    v.y = ");
+        emit_expr(s, f->fwd, "v.y");
+        sb_add(s, ";\n");
+    } else {
+        sb_add(s, "                    %s\n", f->fwd);
+    }
+    sb_add(s, "                    out_ = v;\n                }\n");
+    sb_add(s, "                %s[j] = out_.x;\n                %s[j + 1] = out_.y;\n            }\n", v, v);
+}
+
+static void emit_registry_backward(sbuf *s, const tkm_plasma_formula *f, int flags, int k, const char *gv,
+                                   const char *pv) {
+    sb_add(s, "            /* the registry's code of this op */\n");
+    sb_add(s, "#pragma unroll\n            for (int j = 0; j < TKM_CW; j += 2) {\n");
+    sb_add(s, "                const float2 gin_ = make_float2(%s[j], %s[j + 1]);\n", gv, gv);
+    sb_add(s, "                const float2 pin_ = make_float2(%s[j], %s[j + 1]);\n", pv, pv);
+    emit_pair_params(s, flags, k, "                ");
+    sb_add(s, "                float2 gout_, aw_ = make_float2(0.f, 0.f), ab_ = make_float2(0.f, 0.f);\n");
+    sb_add(s, "                (void)aw_; (void)ab_;\n                {\n");
+    sb_add(s, "                    float2 dy = gin_; const float2 pre = pin_; const float fval = fv; const int tid = 0;\n");
+    sb_add(s, "                    (void)pre; (void)fval; (void)tid;\n");
+    sb_add(s, "                    float2 acc_dw = make_float2(0.f, 0.f), acc_db = make_float2(0.f, 0.f);\n");
+    if (flags & F_W) sb_add(s, "                    const float2 *w_vec = wv_; (void)w_vec;\n");
+    if (flags & F_BIAS) sb_add(s, "                    const float2 *b_vec = bv_; (void)b_vec;\n");
+    if (f->expr) {
+        sb_add(s, "                    dy.x *= ");
+        emit_expr(s, f->bwd, "pre.x");
+        sb_add(s, ";\n                    dy.y *= ");
+        emit_expr(s, f->bwd, "pre.y");
+        sb_add(s, ";\n");
+    } else {
+        sb_add(s, "                    %s\n", f->bwd);
+    }
+    sb_add(s, "                    gout_ = dy; aw_ = acc_dw; ab_ = acc_db;\n                }\n");
+    sb_add(s, "                %s[j] = gout_.x;\n                %s[j + 1] = gout_.y;\n", gv, gv);
+    if (flags & F_W) sb_add(s, "                if (live) { a_w%d[j] += aw_.x; a_w%d[j + 1] += aw_.y; }\n", k, k);
+    if (flags & F_BIAS) sb_add(s, "                if (live) { a_bias%d[j] += ab_.x; a_bias%d[j + 1] += ab_.y; }\n", k, k);
+    sb_add(s, "            }\n");
+}
+
 /* Forward of node k on v[TKM_CW]; `save` emits the stores of the norm state (forward pass only;
  * the backward replays norms from their saved xhat, emit_replay_norm). */
 static void emit_node_forward(sbuf *s, const tkm_plasma_desc *d, const tkm_plasma_geom *g, int k, const char *v,
@@ -408,6 +517,8 @@ static void emit_node_forward(sbuf *s, const tkm_plasma_desc *d, const tkm_plasm
         sb_add(s, "            tkm_unpack_%s(live ? branch_%d[(size_t)r * TKM_CH + ch] : TKM_ZERO(), bi);\n",
                kind16(d), k);
         sb_add(s, "#pragma unroll\n            for (int j = 0; j < TKM_CW; ++j) %s[j] += bi[j];\n", v);
+    } else if (g->formulas && g->formulas[k].fwd) {
+        emit_registry_forward(s, &g->formulas[k], o->flags, k, v);
     } else {
         sb_add(s, "#pragma unroll\n            for (int j = 0; j < TKM_CW; ++j) {\n");
         sb_add(s, "                float x = %s[j];\n", v);
@@ -485,6 +596,8 @@ static void emit_node_backward(sbuf *s, const tkm_plasma_desc *d, const tkm_plas
         sb_add(s, "#pragma unroll\n                for (int j = 0; j < TKM_CW; ++j) pb[j] += %s[j];\n", gv);
         sb_add(s, "                dbranch_%d[(size_t)r * TKM_CH + ch] = tkm_pack_%s(pb);\n", k, kind16(d));
         sb_add(s, "            }\n");
+    } else if (g->formulas && g->formulas[k].bwd) {
+        emit_registry_backward(s, &g->formulas[k], o->flags, k, gv, pv);
     } else {
         sb_add(s, "#pragma unroll\n            for (int j = 0; j < TKM_CW; ++j) {\n");
         sb_add(s, "                float g = %s[j];\n", gv);
@@ -713,11 +826,12 @@ static int emit_bwd(sbuf *s, const tkm_plasma_desc *d, const tkm_plasma_geom *g,
 }
 
 int tkm_plasma_emit(tkm_sbuf *s, const tkm_plasma_desc *d, const tkm_kplan *fwd_plan, const tkm_kplan *bwd_plan,
-                    int scoped) {
-    int rc = tkm_plasma_check_desc(d);
+                    int scoped, const tkm_plasma_formula *formulas) {
+    int rc = tkm_plasma_check_desc_f(d, formulas);
     if (rc) return rc;
     tkm_plasma_geom g;
     tkm_plasma_geometry(d, &g);
+    g.formulas = formulas;
     if (scoped) sb_add(s, "namespace tkm_g%d {\n", d->group_id);
     emit_constants(s, d, &g);
     if (emit_fwd(s, d, &g, fwd_plan) || emit_bwd(s, d, &g, bwd_plan))
@@ -734,7 +848,7 @@ int tkm_plasma_emit(tkm_sbuf *s, const tkm_plasma_desc *d, const tkm_kplan *fwd_
 char *tkm_plasma_source(const tkm_plasma_desc *d) {
     sbuf s = {0};
     sb_add(&s, "%s", tkm_hip_prelude());
-    if (tkm_plasma_emit(&s, d, NULL, NULL, 0) != TKM_ATTN_OK) {
+    if (tkm_plasma_emit(&s, d, NULL, NULL, 0, NULL) != TKM_ATTN_OK) {
         free(s.buf);
         return NULL;
     }

@@ -19,7 +19,11 @@ HEADER = os.path.join(attn.ROOT, "include", "tkm_plasma.h")
 
 OP_NAMES = ["Bias", "RMSNorm", "LN", "BN", "L2Norm", "SiLU", "ReLU", "ReLU2", "LeakyReLU", "ELU", "GELU",
             "Mish", "HardSwish", "HardSigmoid", "Tanh", "Sigmoid", "SwishBeta", "Sin", "CosGate", "SoftCap",
-            "Clamp", "Scale", "LayerScale", "DyT", "PReLU", "xATLU", "Softplus", "Snake", "Add", "Drop"]
+            "Clamp", "Scale", "LayerScale", "DyT", "PReLU", "xATLU", "Softplus", "Snake", "Add", "Drop",
+            # ops whose code only the registry holds (whole-graph generator with the front end
+            # linked); the descriptor API rejects them
+            "Formula", "FormulaW", "FormulaB"]
+FORMULA_OPS = ("Formula", "FormulaW", "FormulaB")
 OPS = {n: i for i, n in enumerate(OP_NAMES)}
 ARG_KINDS = ["in", "out", "dout", "din", "w", "beta", "bias", "xhat", "istd", "branch", "dbranch",
              "dw", "dbeta", "dbias", "mask", "seed"]
