@@ -567,32 +567,36 @@ def main():
             fn()
     torch.cuda.synchronize()
 
+    # The timed region holds the K steps and two events, nothing between the kernels: an
+    # event recorded between two kernels leaves the GPU idle for 6-10 us (kernel trace).
     K = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(K)]
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     t_start.record(stream)
     for k in range(K):
-        ev[k][0].record(stream)
-        for i, (_, fn) in enumerate(stages):
+        for _, fn in stages:
             fn()
-            ev[k][i + 1].record(stream)
     t_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = t_start.elapsed_time(t_end)
-    kernel_path = {}  # the kernels each stage launches (one more step, after the timed region)
-    for name, fn in stages:
-        fn()
-        kernel_path[name] = attn.last_kernels()
-    torch.cuda.synchronize()
     ms_step = total_ms / K
-
-    per = {name: np.array([ev[k][i].elapsed_time(ev[k][i + 1]) for k in range(K)])
-           for i, (name, _) in enumerate(stages)}
-    step_ms = np.array([ev[k][0].elapsed_time(ev[k][len(stages)]) for k in range(K)])
+    # Per kernel, right after: K launches of each kernel back to back between two events
+    # (each launch recomputes the same outputs from the same inputs).
+    kernel_path = {}
+    per = {}
+    for name, fn in stages:
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(K):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        kernel_path[name] = attn.last_kernels()
+        per[name] = e0.elapsed_time(e1) / K
 
     f_fwd = attn.attention_flops(B, S, Hq, D, causal, kv_len, "fwd")
     f_total = f_fwd * (3.5 if backward else 1.0)
@@ -602,18 +606,16 @@ def main():
     credit = {"attn_fwd": f_fwd, "bwd_dkdv": 2.0 * f_fwd, "bwd_dq": 0.5 * f_fwd}
     delta_bytes = 2.0 * B * S * Hq * D * 2 + 4.0 * B * Hq * S
     kernels = {}
-    for name, t in per.items():
-        avg = float(t.mean())
-        k = {"avg_ms": round(avg, 5), "p10_ms": round(float(np.percentile(t, 10)), 5),
-             "p90_ms": round(float(np.percentile(t, 90)), 5)}
+    for name, avg in per.items():
+        k = {"avg_ms": round(avg, 5)}
         if name in credit:
             k["tflops"] = round(credit[name] / (avg * 1e-3) / 1e12, 2)
             k["frac_peak"] = round(k["tflops"] / PEAK_FP16_TFLOPS, 4)
         else:
             k["gbps"] = round(delta_bytes / (avg * 1e-3) / 1e9, 1)
         kernels[name] = k
-    dom = max(per, key=lambda n: per[n].mean())
-    dom_avg = float(per[dom].mean())
+    dom = max(per, key=lambda n: per[n])
+    dom_avg = per[dom]
     if dom in credit:
         ach = credit[dom] / (dom_avg * 1e-3) / 1e12
         roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS,
@@ -628,7 +630,7 @@ def main():
                 "avg_ms": round(dom_avg, 5)}
 
     value = f_total / (ms_step * 1e-3) / 1e12
-    fwd_ms = float(per["attn_fwd"].mean())
+    fwd_ms = per["attn_fwd"]
     res = {
         "metric": METRIC if args.config == "cfg3" else f"FlashAttn TFLOP/s ({args.config})",
         "value": round(value, 2),
@@ -648,8 +650,8 @@ def main():
         "frac_peak": round(value / PEAK_FP16_TFLOPS, 4),
         "fwd": {"ms": round(fwd_ms, 5), "tflops": kernels["attn_fwd"]["tflops"],
                 "frac_peak": kernels["attn_fwd"]["frac_peak"]},
-        "step_ms_p10_p50_p90": [round(float(np.percentile(step_ms, p)), 5) for p in (10, 50, 90)],
         "kernels": kernels,
+        "kernel_timing": "after the timed region: K launches of each kernel back to back between two events",
         "kernel_path": kernel_path,
         "roofline": roof,
         "wall_s": round(wall, 3),
