@@ -52,7 +52,7 @@ def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, overflow=()):
     kv = None if kv_len is None else [int(x) for x in kv_len]
     args = struct.pack("<QQQQIIIfIIIIIIIIIIII", QKV, OUT, LSE, KVLEN if kv else 0, S, Hq, Hkv,
                        0.127, int(causal), n_qblk, ldb, ldo, G, n_wg, n_items, bhq,
-                       reciprocal(bhq, n_items), reciprocal(Hq, bhq), reciprocal(G, Hq), 0)
+                       reciprocal(n_qblk, n_items), reciprocal(Hq, bhq), reciprocal(G, Hq), 0)
     assert len(args) == attn_fwd.KERNARG_BYTES
     mem = {"qkv": (QKV, B * S * ldb, ldb, 256), "out": (OUT, B * S * ldo, ldo, ldo),
            "lse": (LSE, B * Hq * S * 4, 4, 4), "kv_len": (KVLEN, 4 * B, 4, 4)}
@@ -144,6 +144,7 @@ def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, overflow=()):
     (2, 2048, 4, 4, True, None, 7),
     (1, 512, 4, 2, True, None, 8),          # one item per workgroup: the DMA stream runs past the last item
     (1, 300, 3, 1, True, [129], 256),
+    (2, 2048, 4, 2, True, None, 20),        # 20 places over the 8 XCDs: 3, 3, 3, 3, 2, 2, 2, 2
 ])
 def test_fwd_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg):
     run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg)
@@ -198,7 +199,7 @@ def run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg):
     kv = None if kv_len is None else [int(x) for x in kv_len]
     args = struct.pack("<QQQQQIIIfIIIIfIIIIIII", QKV, DOUT, QUADS, DQKV, KVLEN if kv else 0, S, Hq, Hkv,
                        0.127, int(causal), ldb, ldo, Hq // Hkv, 0.088, n_kblk, (S + 31) // 32 * 32, n_wg,
-                       n_items, bh, reciprocal(bh, n_items), reciprocal(Hkv, bh))
+                       n_items, bh, reciprocal(n_kblk, n_items), reciprocal(Hkv, bh))
     assert len(args) == attn_dkdv.KERNARG_BYTES
     stored = {}
     next_kv = {}
@@ -249,7 +250,7 @@ def run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d):
     kv = None if kv_len is None else [int(x) for x in kv_len]
     args = struct.pack("<QQQQQQQQIIIfIIIIfIIIIIIIII", QKV, O_, DOUT, LSE, DELTA, QUADS, DQKV,
                        KVLEN if kv else 0, S, Hq, Hkv, 0.127, int(causal), ldb, ldo, G, 0.088, n_qblk,
-                       (S + 31) // 32 * 32, n_wg, n_items, bhq, reciprocal(bhq, n_items),
+                       (S + 31) // 32 * 32, n_wg, n_items, bhq, reciprocal(n_qblk, n_items),
                        reciprocal(Hq, bhq), reciprocal(G, Hq), int(compute_d))
     assert len(args) == attn_dq.KERNARG_BYTES
     stored = {}
@@ -290,7 +291,8 @@ def run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d):
 BWD_CASES = [(1, 512, 2, 1, True, None, 3), (2, 700, 4, 2, True, None, 5), (2, 700, 4, 2, False, None, 4),
              (2, 1024, 8, 8, True, None, 16),
              (2, 1000, 2, 2, False, [1000, 333], 3), (3, 600, 2, 1, True, [0, 65, 600], 2),
-             (1, 64, 1, 1, True, None, 1), (1, 1, 1, 1, False, None, 1), (1, 300, 3, 1, True, [129], 256)]
+             (1, 64, 1, 1, True, None, 1), (1, 1, 1, 1, False, None, 1), (1, 300, 3, 1, True, [129], 256),
+             (2, 1024, 4, 2, True, None, 12)]
 
 
 @pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", BWD_CASES)

@@ -11,8 +11,8 @@ Instead of LSE and D it reads the workspace's row values -LSE*log2(e) and -D, st
 (batch, head) in tiles of 32 rows (the 32 values -LSE*log2e, then the 32 values -D; rows
 padded to a multiple of 32 with zeros), which the pass that computes D writes.
 
-Work decomposition: grid (Hkv, B, n_kblk), one workgroup = 4 waves = one (batch, kv head,
-block of 128 keys); one wave per SIMD.  A wave owns 32 keys: K (prescaled by
+Work decomposition: persistent, one workgroup (4 waves, one per SIMD) per compute unit walks
+items (batch, kv head, block of 128 keys), the key blocks of a head together on one XCD.  A wave owns 32 keys: K (prescaled by
 scale*log2(e)) and V of those keys sit in AGPRs as the B operands of S = Q K^T and
 dP = dO V^T, and the accumulators dV^T, dK^T (C[m = head dim][n = key]) in AGPRs.  The
 workgroup walks the query tiles (32 rows) of every q-head of the group from the last one down
@@ -38,7 +38,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .common import Lanes, lane_basics, row_read_offsets, swz, tr_read_offsets
+from .common import Lanes, lane_basics, row_read_offsets, swz, tr_read_offsets, xcd_slot
 from .gfx950 import A, BRANCH, Prog, S, V, ar, kernel_text, sr, vr
 
 NAME = "tkm_fa_bwd_dkdv_d128_f16"
@@ -65,14 +65,14 @@ ARGS = [(0, 8, "ptr"), (8, 8, "ptr"), (16, 8, "ptr"), (24, 8, "ptr"), (32, 8, "p
 KERNARG_BYTES = 104
 
 # ---- SGPRs
-S_WG = 2                               # workgroup index (one-dimensional grid)
+S_WG = 2                               # workgroup index, then its place in a round (xcd_slot)
 S_KA, S_KD = 3, 4                      # round of the current item / of the DMA stream's item
 S_QKV, S_DOUT, S_PAIRS, S_DQKV, S_KVLEN = 8, 10, 12, 14, 16
 S_SEQ, S_HQ, S_HKV, S_SL2, S_CAUSAL, S_LDB = 18, 19, 20, 21, 22, 23
 S_LDO, S_G, S_SCALE, S_NKBLK, S_SP, S_NWG, S_NI, S_BH = 24, 25, 26, 27, 28, 29, 30, 31
 S_TQ, S_TO, S_TL = 5, 6, 7             # offsets of the requested tile (Q, dO, row values)
 S_LDB32, S_LDO32 = 88, 89              # 32 rows of qkv / dO in bytes
-S_MAGBH, S_MAGHKV = 90, 91             # ceil(2^32 / (B*Hkv)), ceil(2^32 / Hkv) (0 for 1)
+S_MAGNK, S_MAGHKV = 90, 91             # ceil(2^32 / n_kblk), ceil(2^32 / Hkv) (0 for 1)
 S_BA, S_KVHA, S_ITERSD, S_QTBD = 92, 93, 94, 95   # current item's batch, kv head; DMA item's tiles
 S_WAVE, S_KVL, S_KB0, S_KW0, S_QTB, S_QTL, S_ITERS, S_IT = 32, 33, 34, 35, 36, 37, 38, 39
 S_BQKV, S_BDO, S_BLD = 40, 42, 44      # 64-bit bases of the DMA stream's item
@@ -376,9 +376,11 @@ class Body:
         s(f"s_or_b32 {sr(S_CODE)}, {sr(S_CODE)}, {sr(T)}", S(S_CODE) + S(T), S(S_CODE))
 
     # ---------------------------------------------------------------- items
-    # A workgroup walks items i = z*(B*Hkv) + b*Hkv + kvh (z = key block, heaviest first for
-    # causal) in rounds of NWG: round k takes item k*NWG + wg, or k*NWG + NWG-1-wg for odd k,
-    # so the long and short items of consecutive rounds pair up.  An item has
+    # A workgroup walks items i = (b*Hkv + kvh)*n_kblk + z (z = key block, fastest) in rounds
+    # of NWG: round k takes item k*NWG + v, or k*NWG + NWG-1-v for odd k, v the workgroup's
+    # place (xcd_slot: consecutive places share an XCD).  The key blocks of a head then run
+    # together on one XCD and share its L2 for the head's Q / dO rows, and for causal the
+    # long and short blocks of consecutive rounds pair up (z with n_kblk-1-z).  An item has
     # g*(QTE - QTB) query tiles, or one tile that no wave uses when its keys all lie past
     # kv_len.  Two roles follow the item sequence: the current item (tile it: its keys, masks,
     # accumulators) and the DMA stream (tile it+3), which runs ahead across item boundaries.
@@ -392,14 +394,14 @@ class Body:
         s(f"s_add_u32 {sr(dst)}, {sr(dst)}, {sr(T)}", S(dst) + S(T), S(dst))
 
     def decode(self, i, z, b, kvh):
-        """z = i / (B*Hkv), b = (i % (B*Hkv)) / Hkv, kvh = i % Hkv (multiply-high by the host's
-        reciprocals, checked exact on the host for every index that occurs)."""
+        """R = i / n_kblk, z = i % n_kblk, b = R / Hkv, kvh = R % Hkv (multiply-high by the
+        host's reciprocals, checked exact on the host for every index that occurs)."""
         s, R = self.s, S_TMP + 13
-        s(f"s_mul_hi_u32 {sr(z)}, {sr(i)}, {sr(S_MAGBH)}", S(i) + S(S_MAGBH), S(z))
-        s(f"s_cmp_eq_u32 {sr(S_BH)}, 1", S(S_BH), [("scc", 0)])
-        s(f"s_cselect_b32 {sr(z)}, {sr(i)}, {sr(z)}", S(i) + S(z) + [("scc", 0)], S(z))
-        s(f"s_mul_i32 {sr(R)}, {sr(z)}, {sr(S_BH)}", S(z) + S(S_BH), S(R))
-        s(f"s_sub_u32 {sr(R)}, {sr(i)}, {sr(R)}", S(i) + S(R), S(R))
+        s(f"s_mul_hi_u32 {sr(R)}, {sr(i)}, {sr(S_MAGNK)}", S(i) + S(S_MAGNK), S(R))
+        s(f"s_cmp_eq_u32 {sr(S_NKBLK)}, 1", S(S_NKBLK), [("scc", 0)])
+        s(f"s_cselect_b32 {sr(R)}, {sr(i)}, {sr(R)}", S(i) + S(R) + [("scc", 0)], S(R))
+        s(f"s_mul_i32 {sr(z)}, {sr(R)}, {sr(S_NKBLK)}", S(R) + S(S_NKBLK), S(z))
+        s(f"s_sub_u32 {sr(z)}, {sr(i)}, {sr(z)}", S(i) + S(z), S(z))
         s(f"s_mul_hi_u32 {sr(b)}, {sr(R)}, {sr(S_MAGHKV)}", S(R) + S(S_MAGHKV), S(b))
         s(f"s_cmp_eq_u32 {sr(S_HKV)}, 1", S(S_HKV), [("scc", 0)])
         s(f"s_cselect_b32 {sr(b)}, {sr(R)}, {sr(b)}", S(R) + S(b) + [("scc", 0)], S(b))
@@ -790,11 +792,12 @@ def build(check_ldb: int = 12288, check_ldo: int = 4096) -> str:
     # ---------------------------------------------------------------- scalars
     p.smem(f"s_load_dwordx16 {sr(8, 16)}, {sr(0, 2)}, 0x0", S(8, 16), S(0, 2))
     p.smem(f"s_load_dwordx8 {sr(24, 8)}, {sr(0, 2)}, 0x40", S(24, 8), S(0, 2))
-    p.smem(f"s_load_dwordx2 {sr(S_MAGBH, 2)}, {sr(0, 2)}, 0x60", S(S_MAGBH, 2), S(0, 2))
+    p.smem(f"s_load_dwordx2 {sr(S_MAGNK, 2)}, {sr(0, 2)}, 0x60", S(S_MAGNK, 2), S(0, 2))
     L = Lanes(p, check_ldb)
     L.shr(V_PT + 0, L.k(6), 0)
     p.readlane(f"v_readfirstlane_b32 {sr(S_WAVE)}, {vr(V_PT + 0)}", V(V_PT + 0), S(S_WAVE))
     p.waitcnt(lgkm=0)
+    xcd_slot(p, S_WG, S_NWG, S_TMP, S_TMP + 1)
     T0, T3 = S_TMP, S_TMP + 3
     sal(f"s_add_u32 {sr(T0)}, {sr(S_SEQ)}, 31", S(S_SEQ), S(T0))
     sal(f"s_lshr_b32 {sr(S_QTL)}, {sr(T0)}, 5", S(T0), S(S_QTL))

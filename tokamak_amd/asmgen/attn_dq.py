@@ -10,8 +10,9 @@ tile: the 32 values -LSE*log2e, then the 32 values -D; rows past S zero) that th
 kernel reads; otherwise it reads D from delta.
 
 Work decomposition: persistent, one workgroup (4 waves, one per SIMD) per compute unit walks
-items (block of 256 query rows, batch, q-head), heaviest first for causal, in snake order
-over rounds of NWG items.  A wave owns 64 query rows (two blocks of 32): Q (prescaled by
+items (batch, q-head, block of 256 query rows; block fastest) in snake order over rounds of
+NWG items, consecutive items of a round on one XCD (xcd_slot), so that the blocks of a head
+share K/V tiles in its L2 and, for causal, long and short blocks of consecutive rounds pair up.  A wave owns 64 query rows (two blocks of 32): Q (prescaled by
 scale*log2(e)) and dO of its rows sit in AGPRs as the B operands of S^T = K Q^T and
 dP^T = V dO^T, dQ^T (C[m = head dim][n = query]) accumulates in AGPRs.  K and V tiles of 32
 keys go HBM -> LDS by buffer DMA into four buffers, requested three tiles ahead; the DMA
@@ -34,7 +35,7 @@ from __future__ import annotations
 import numpy as np
 
 from .attn_dkdv import split_scalar
-from .common import Lanes, lane_basics, row_read_offsets, swz, tr_read_offsets
+from .common import Lanes, lane_basics, row_read_offsets, swz, tr_read_offsets, xcd_slot
 from .gfx950 import A, BRANCH, PERMLANE, Prog, S, V, ar, kernel_text, sr, vr
 
 NAME = "tkm_fa_bwd_dq_d128_f16"
@@ -61,7 +62,7 @@ KERNARG_BYTES = 136
 S_WG, S_KA, S_KD, S_TK, S_CODE, S_IT = 2, 3, 4, 5, 6, 7
 S_QKV, S_O, S_DOUT, S_LSE, S_DELTA, S_QUADS, S_DQKV, S_KVLEN = 8, 10, 12, 14, 16, 18, 20, 22
 S_SEQ, S_HQ, S_HKV, S_SL2, S_CAUSAL, S_LDB, S_LDO, S_G = 24, 25, 26, 27, 28, 29, 30, 31
-S_SCALE, S_NQBLK, S_SP, S_NWG, S_NI, S_BHQ, S_MAGBHQ, S_MAGHQ = 32, 33, 34, 35, 36, 37, 38, 39
+S_SCALE, S_NQBLK, S_SP, S_NWG, S_NI, S_BHQ, S_MAGNQ, S_MAGHQ = 32, 33, 34, 35, 36, 37, 38, 39
 S_MAGG, S_WD = 40, 41
 S_WAVE, S_KVL, S_Q0, S_NT, S_ACTEND, S_MASKB = 42, 43, 44, 45, 46, 47
 S_RK, S_RV = 48, 52                    # DMA descriptors of the DMA stream's item
@@ -162,8 +163,9 @@ class Body:
             s(f"s_sub_u32 {sr(rem)}, {sr(x)}, {sr(rem)}", S(x) + S(rem), S(rem))
 
     def decode(self, i, z, b, h, kvh):
+        """item i -> (b, h, kv head, query block z): z fastest."""
         R = S_TMP + 13
-        self.divide(i, S_BHQ, S_MAGBHQ, z, R)
+        self.divide(i, S_NQBLK, S_MAGNQ, R, z)
         self.divide(R, S_HQ, S_MAGHQ, b, h)
         self.divide(h, S_G, S_MAGG, kvh, None)
 
@@ -732,6 +734,7 @@ def build(check_ldb: int = 12288) -> str:
     L.shr(V_PT + 0, L.k(6), 0)
     p.readlane(f"v_readfirstlane_b32 {sr(S_WAVE)}, {vr(V_PT + 0)}", V(V_PT + 0), S(S_WAVE))
     p.waitcnt(lgkm=0)
+    xcd_slot(p, S_WG, S_NWG, S_TMP, S_TMP + 1)
     T3 = S_TMP + 3
     sal(f"s_lshl_b32 {sr(S_LDB32)}, {sr(S_LDB)}, 5", S(S_LDB), S(S_LDB32))
     sal(f"s_lshl_b32 {sr(S_LDSW)}, {sr(S_WAVE)}, 11", S(S_WAVE), S(S_LDSW))

@@ -8,8 +8,10 @@ log of the scaled scores) out; q-head h reads kv-head h/(Hq/Hkv); key j is visib
 query i iff j < kv_len[b] and (!causal || j <= i).
 
 Work decomposition: persistent, one workgroup (4 waves, one per SIMD) per compute unit walks
-items (block of 256 query rows, batch, q-head), heaviest first for causal, in snake order over
-rounds of NWG items.  A wave owns 64 query rows: Q (prescaled by scale*log2(e), rounded to
+items (batch, q-head, block of 256 query rows; block fastest) in snake order over rounds of NWG
+items, consecutive items of a round on one XCD (xcd_slot): the query blocks of a head, and the
+q-heads of a kv group, read the same K/V tiles through that XCD's L2, and for causal the long
+and short blocks of consecutive rounds pair up.  A wave owns 64 query rows: Q (prescaled by scale*log2(e), rounded to
 fp16) sits in AGPRs as two 32-row blocks, so every K or V operand read from LDS feeds two
 MFMAs, and its O^T accumulators sit in AGPRs.  K/V tiles of 64 keys go HBM -> LDS by buffer
 DMA into two K and two V buffers (rows past the valid range read as zero), row-major with the
@@ -42,7 +44,7 @@ from __future__ import annotations
 import numpy as np
 
 from .attn_dkdv import split_scalar
-from .common import Lanes, lane_basics, row_read_offsets, swz, tr_read_offsets
+from .common import Lanes, lane_basics, row_read_offsets, swz, tr_read_offsets, xcd_slot
 from .gfx950 import A, BRANCH, PERMLANE, Prog, S, V, ar, kernel_text, sr, vr
 
 NAME = "tkm_fa_fwd_d128_f16"
@@ -75,7 +77,7 @@ KERNARG_BYTES = 96
 S_KARG, S_WG = 0, 2
 S_QKV, S_OUT, S_LSE, S_KVLEN = 8, 10, 12, 14
 S_SEQ, S_HQ, S_HKV, S_SL2, S_CAUSAL, S_NQBLK, S_LDB, S_LDO = 16, 17, 18, 19, 20, 21, 22, 23
-S_G, S_NWG, S_NI, S_BHQ, S_MAGBHQ, S_MAGHQ, S_MAGG = 24, 25, 26, 27, 28, 29, 30
+S_G, S_NWG, S_NI, S_BHQ, S_MAGNQ, S_MAGHQ, S_MAGG = 24, 25, 26, 27, 28, 29, 30
 # the current item
 S_KA, S_IT, S_NT, S_ACTEND, S_MASKB, S_Q0, S_KVL, S_BA = 32, 33, 34, 35, 36, 37, 38, 39
 S_HA, S_CODE, S_WAVE, S_PASS, S_LDSW, S_KVEND, S_KVHA = 40, 41, 42, 43, 44, 45, 46
@@ -166,7 +168,7 @@ class Body:
         s(f"s_mov_b32 {sr(dst + 3)}, 0x20000", [], S(dst + 3))
 
     def item_index(self, k_sgpr, dst, tmp):
-        """dst = item of round k: k*NWG + (k odd ? NWG-1-wg : wg)."""
+        """dst = item of round k: k*NWG + (k odd ? NWG-1-v : v), v the workgroup's place."""
         s = self.s
         s(f"s_mul_i32 {sr(dst)}, {sr(k_sgpr)}, {sr(S_NWG)}", S(k_sgpr) + S(S_NWG), S(dst))
         s(f"s_sub_u32 {sr(tmp)}, {sr(S_NWG)}, 1", S(S_NWG), S(tmp))
@@ -187,8 +189,8 @@ class Body:
             s(f"s_sub_u32 {sr(rem)}, {sr(x)}, {sr(rem)}", S(x) + S(rem), S(rem))
 
     def decode(self, i, z, b, h, kvh, r):
-        """item i -> (z = i / (B*Hq), b, h, kv head): h fastest."""
-        self.divide(i, S_BHQ, S_MAGBHQ, z, r)
+        """item i -> (b, h, kv head, query block z): z fastest."""
+        self.divide(i, S_NQBLK, S_MAGNQ, r, z)
         self.divide(r, S_HQ, S_MAGHQ, b, h)
         self.divide(h, S_G, S_MAGG, kvh, None)
 
@@ -843,6 +845,7 @@ def build(check_ldb: int = 12288) -> str:
     L.shr(V_PT + 0, L.k(6), 0)
     p.readlane(f"v_readfirstlane_b32 {sr(S_WAVE)}, {vr(V_PT + 0)}", V(V_PT + 0), S(S_WAVE))
     p.waitcnt(lgkm=0)
+    xcd_slot(p, S_WG, S_NWG, S_TMP, S_TMP + 1)
     # DMA row offset of this wave inside a tile: wave * 4 instructions * 4 rows * 256 B
     sal(f"s_lshl_b32 {sr(S_LDSW)}, {sr(S_WAVE)}, 12", S(S_WAVE), S(S_LDSW))
     # ------------------------------------------------------------------ prologue: lane values

@@ -156,3 +156,28 @@ def lane_basics(L: Lanes, regs):
     L.and_(LANE, L.k(63), 0)
     L.and_(L32, L.k(31), 0)
     L.shr(HI, L.k(5), LANE)
+
+
+def xcd_slot(p: Prog, wg: int, nwg: int, t0: int, t1: int):
+    """s[wg] := the workgroup's place among the NWG places of a round, dealt XCD by XCD.
+
+    The dispatcher hands workgroups to the 8 XCDs in turn (workgroup w to XCD w % 8), so XCD
+    x runs workgroups x, x+8, x+16, ...; they take the places x*q + min(x, r) + 0, 1, ...
+    (q = NWG / 8, r = NWG % 8).  Consecutive places then run on one XCD and share its L2: the
+    items of a round that read the same rows (the blocks of one head) fetch them from HBM
+    once.  The map is a permutation of 0 .. NWG-1 for every NWG."""
+    sal = p.salu
+    sal(f"s_and_b32 {sr(t0)}, {sr(wg)}, 7", S(wg), S(t0))
+    sal(f"s_lshr_b32 {sr(t1)}, {sr(nwg)}, 3", S(nwg), S(t1))
+    sal(f"s_mul_i32 {sr(t1)}, {sr(t1)}, {sr(t0)}", S(t1) + S(t0), S(t1))
+    sal(f"s_lshr_b32 {sr(wg)}, {sr(wg)}, 3", S(wg), S(wg))
+    sal(f"s_add_u32 {sr(wg)}, {sr(wg)}, {sr(t1)}", S(wg) + S(t1), S(wg))
+    sal(f"s_and_b32 {sr(t1)}, {sr(nwg)}, 7", S(nwg), S(t1))
+    sal(f"s_min_u32 {sr(t1)}, {sr(t1)}, {sr(t0)}", S(t1) + S(t0), S(t1))
+    sal(f"s_add_u32 {sr(wg)}, {sr(wg)}, {sr(t1)}", S(wg) + S(t1), S(wg))
+
+
+def xcd_slots(nwg: int) -> list:
+    """The places xcd_slot gives workgroups 0 .. nwg-1."""
+    q, r = nwg // 8, nwg % 8
+    return [(w % 8) * q + min(w % 8, r) + w // 8 for w in range(nwg)]
