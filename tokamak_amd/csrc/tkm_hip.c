@@ -95,8 +95,12 @@ struct TkmRuntime {
     tkm_runtime_opts opts;
     int dt, training;
     hipStream_t stream;
+    /* Training: the weight-gradient GEMMs run on `side` with their own workspace, forked from
+     * `stream` at each GEMM node of the backward walk and joined before the reductions. */
+    hipStream_t side;
+    hipEvent_t ev_fork, ev_join;
     void *lt;
-    void *gemm_ws;
+    void *gemm_ws, *gemm_ws_side;
     size_t gemm_ws_bytes;
     hipModule_t module;
     rt_group *groups;
@@ -168,6 +172,11 @@ static void note(TkmRuntime *rt, int rc, const char *what) {
         rt->failed = 1;
     }
     if (rt->counting) rt->kernel_count++;
+}
+
+/* Work enqueued on `waiter` from now on runs after everything enqueued on `on` so far. */
+static void depend(TkmRuntime *rt, hipStream_t waiter, hipStream_t on, hipEvent_t ev) {
+    if (!HIP_OK(hipEventRecord(ev, on)) || !HIP_OK(hipStreamWaitEvent(waiter, ev, 0))) rt->failed = 1;
 }
 
 /* ---- op resources (the registry's resource flags, src/tkm_registry.c:43-456) -------------- */
@@ -572,6 +581,7 @@ static int plan_gemms(TkmRuntime *rt) {
     }
     rt->gemm_ws_bytes = ws;
     if (ws && !HIP_OK(hipMalloc(&rt->gemm_ws, ws))) return 0;
+    if (ws && rt->training && !HIP_OK(hipMalloc(&rt->gemm_ws_side, ws))) return 0;
     return 1;
 }
 
@@ -683,6 +693,9 @@ TkmRuntime *tkm_runtime_ignite_ex(const TkmGraph *g, const char *src, const tkm_
         goto fail;
     }
     if (!HIP_OK(hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking))) goto fail;
+    if (!HIP_OK(hipStreamCreateWithFlags(&rt->side, hipStreamNonBlocking))) goto fail;
+    if (!HIP_OK(hipEventCreateWithFlags(&rt->ev_fork, hipEventDisableTiming))) goto fail;
+    if (!HIP_OK(hipEventCreateWithFlags(&rt->ev_join, hipEventDisableTiming))) goto fail;
     if (tkm_gemm_handle_create(&rt->lt)) goto fail;
     /* generated kernels: prelude + source, hipRTC for gfx950 (src/tkm_gpu.cu:1047-1078) */
     if (!src) src = own_src = tkm_codegen_hip_source(G, rt->dt);
@@ -954,8 +967,12 @@ static void record_step(TkmRuntime *rt, int clear_loss) {
         rt_node *st = &rt->nodes[i];
         void *in_act = act(rt, n->in0), *out_act = act(rt, i), *dout = grd(rt, i), *din = grd(rt, n->in0);
         if (is_gemm(n->op)) {
+            /* dW on the side stream: its inputs (this node's gradient, complete once every
+             * consumer's backward ran, and the saved input activation) are never written again
+             * in the step, and only SGD reads its output */
             rt_tensor *t = &rt->tensors[st->t_w];
-            note(rt, tkm_gemm_run(st->g_dw, dout, in_act, t->grad, rt->gemm_ws, rt->gemm_ws_bytes, rt->stream),
+            depend(rt, rt->side, rt->stream, rt->ev_fork);
+            note(rt, tkm_gemm_run(st->g_dw, dout, in_act, t->grad, rt->gemm_ws_side, rt->gemm_ws_bytes, rt->side),
                  "GEMM dW");
             note(rt, tkm_gemm_run(st->g_dx, t->w16, dout, din, rt->gemm_ws, rt->gemm_ws_bytes, rt->stream), "GEMM dX");
         } else if (n->op == OP_GQA_ATTN) {
@@ -971,6 +988,7 @@ static void record_step(TkmRuntime *rt, int clear_loss) {
                  "softmax backward");
         }
     }
+    depend(rt, rt->stream, rt->side, rt->ev_join);
     /* parameter gradients: every group's band partials, summed in one launch (each gradient
      * has one producer and is overwritten; gradients nothing writes stay zero) */
     note(rt, tkm_rt_reduce_parts(rt->d_red, rt->n_red, rt->stream), "parameter-gradient reductions");
@@ -1584,12 +1602,16 @@ static void free_runtime(TkmRuntime *rt) {
     hipFree(rt->part_ws);
     hipFree(rt->d_red);
     hipFree(rt->gemm_ws);
+    hipFree(rt->gemm_ws_side);
     hipFree(rt->param_block);
     hipFree(rt->pgrad_block);
     hipFree(rt->save_block);
     hipFree(rt->d_sgd);
     free(rt->clear);
     if (rt->h_pin_lr) hipHostFree(rt->h_pin_lr);
+    if (rt->ev_fork) hipEventDestroy(rt->ev_fork);
+    if (rt->ev_join) hipEventDestroy(rt->ev_join);
+    if (rt->side) hipStreamDestroy(rt->side);
     if (rt->stream) hipStreamDestroy(rt->stream);
     free(rt->tensors);
     free(rt->nodes);
