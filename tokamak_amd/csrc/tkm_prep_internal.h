@@ -21,7 +21,9 @@ enum {
     TKM_PREP_FWD_RPW = 4,          /* forward: rows per wave per block */
     TKM_PREP_BWD_BATCH = 4,        /* backward: rows per wave loaded before the arithmetic */
     TKM_BWD_TARGET_BLOCKS = 2048,  /* backward: bands are chosen to give about this many blocks */
-    TKM_BWD_MIN_BAND = 16,         /* backward: rows per band, at least */
+    TKM_BWD_MIN_BAND = 4,          /* backward: rows per band, at least (one row per wave:
+                                    * at 4096 x 512 the rows a wave walks one after the other
+                                    * cost more than the 4x larger partial rows' reduction) */
     TKM_REDUCE_WAVES = 16          /* partial-row reduction: waves per block (1024 threads) */
 };
 
