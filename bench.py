@@ -58,6 +58,9 @@ def parse():
     ap.add_argument("--config", default="cfg3",
                     choices=sorted(CONFIGS) + sorted(PREP_CONFIGS) + sorted(PLASMA_CONFIGS) + ["cfg4"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="time the K steps as one replay of a captured hipGraph (at cfg2 and cfg4-attn "
+                         "this measured the same as eager launches)")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="threads for the CPU baseline (default: min(16, online CPUs); the GPU "
                          "boxes allot 16 host CPUs to each GPU)")
@@ -569,34 +572,45 @@ def main():
 
     # The timed region holds the K steps and two events, nothing between the kernels: an
     # event recorded between two kernels leaves the GPU idle for 6-10 us (kernel trace).
+    # With --graph the K steps are captured first (nothing runs during a capture) and the
+    # timed region is one replay of that graph.
     K = args.steps
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    t_start.record(stream)
-    for k in range(K):
-        for _, fn in stages:
-            fn()
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    total_ms = t_start.elapsed_time(t_end)
+    use_graph = args.graph
+
+    def timed(fns, reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        graph = None
+        if use_graph:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(reps):
+                    for fn in fns:
+                        fn()
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        e0.record(stream)
+        if graph is not None:
+            graph.replay()
+        else:
+            for _ in range(reps):
+                for fn in fns:
+                    fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1), time.perf_counter() - w0
+
+    total_ms, wall = timed([fn for _, fn in stages], K)
     ms_step = total_ms / K
     # Per kernel, right after: K launches of each kernel back to back between two events
     # (each launch recomputes the same outputs from the same inputs).
     kernel_path = {}
     per = {}
     for name, fn in stages:
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(K):
-            fn()
-        e1.record(stream)
+        per[name] = timed([fn], K)[0] / K
+        fn()
         torch.cuda.synchronize()
         kernel_path[name] = attn.last_kernels()
-        per[name] = e0.elapsed_time(e1) / K
 
     f_fwd = attn.attention_flops(B, S, Hq, D, causal, kv_len, "fwd")
     f_total = f_fwd * (3.5 if backward else 1.0)
@@ -652,6 +666,7 @@ def main():
                 "frac_peak": kernels["attn_fwd"]["frac_peak"]},
         "kernels": kernels,
         "kernel_timing": "after the timed region: K launches of each kernel back to back between two events",
+        "timed_as": "one replay of a captured hipGraph of the K steps" if use_graph else "eager launches",
         "kernel_path": kernel_path,
         "roofline": roof,
         "wall_s": round(wall, 3),
