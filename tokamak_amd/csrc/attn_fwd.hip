@@ -41,14 +41,19 @@
 
 namespace tkm {
 
-template <int D, int DT, int QB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// KSPLIT = 2 (grids of at most one workgroup per CU): 8 waves in two groups of 4 over the same
+// query rows; group g walks its own half of the block's key tiles through its own buffers, with
+// its own fixed m (and its own exact redo), and group 1 hands (m, l, O) to group 0 through LDS
+// at the end, which merges them (rescaling each side by 2^(m_side - m)) and writes O and LSE.
+// The heaviest causal block then walks half its tiles, at two waves per SIMD.
+template <int D, int DT, int QB, int KSPLIT>
+__global__ __launch_bounds__(256 * KSPLIT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
                    float* __restrict__ lse, const int32_t* __restrict__ kv_len, int B, int S,
                    int Hq, int Hkv, float sl2, int causal, int n_qblk) {
     constexpr bool PRE = (DT == DT_F16);  // scale folded into Q, -m into the accumulator
     constexpr bool SPL = Split<DT>::on;   // bf16: P as hi + lo
-    constexpr int NW = 4;                 // waves per workgroup (two workgroups per CU)
+    constexpr int NW = 4;                 // waves per group (two workgroups, or one of two groups, per CU)
     constexpr int WR = 32 * QB;           // query rows per wave
     constexpr int BM = NW * WR, BN = 64;
     constexpr int KS = D / 16;    // k-steps over the head dim (S^T)
@@ -61,11 +66,12 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
     constexpr int RPI = 64 / CPR;     // rows per DMA instruction (64 lanes x 16 bytes)
     constexpr int NI = BN / RPI / NW;  // DMA instructions per wave, per tile and tensor
     constexpr int NL = SPL ? PKS : 1;
-    __shared__ __attribute__((aligned(1024))) char smem[2][2][TILEB];  // [K, V][buffer]
+    __shared__ __attribute__((aligned(1024))) char smem[KSPLIT][2][2][TILEB];  // [group][K, V][buffer]
     __shared__ int redo;  // set when a P overflowed: recompute with the exact row max
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+    const int grp = wave >> 2, gw = wave & 3;                    // key-split group, wave in it
     const int l32 = lane & 31, hi = lane >> 5;
     const int nh = B * Hq;
     const int bid = blockIdx.x;
@@ -83,7 +89,7 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
         kvl = kvl < 0 ? 0 : (kvl > S ? S : kvl);
     }
 
-    const int q0 = qblk * BM + wave * WR;  // first query row of this wave
+    const int q0 = qblk * BM + gw * WR;  // first query row of this wave
     u32x4 qf[QB][KS];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -112,6 +118,9 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
     const int n_plain = min(kvl / BN, causal ? (q0 + 1) / BN : ntiles);
     // tiles [0, n_act) hold at least one key visible to this wave
     const int n_act = causal ? min(ntiles, (q0 + WR - 1) / BN + 1) : ntiles;
+    // this group's tiles [tb, te); every group runs nit iterations (barriers stay matched)
+    const int nit = KSPLIT == 2 ? (ntiles + 1) / 2 : ntiles;
+    const int tb = grp == 0 ? 0 : nit, te = grp == 0 ? nit : ntiles;
 
     // DMA of one tile (tensor 0 = K, 1 = V) into buffer buf: wave w moves rows
     // [w*NI*RPI, (w+1)*NI*RPI) of the BN-row tile.
@@ -122,8 +131,8 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
                                  (uint32_t)min(BN, kv_end - k0) * ldb);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const int r0 = (wave * NI + i) * RPI, row = r0 + dma_r;
-            dma16(r, &smem[tensor][buf][r0 * ROWB],
+            const int r0 = (gw * NI + i) * RPI, row = r0 + dma_r;
+            dma16(r, &smem[grp][tensor][buf][r0 * ROWB],
                   (uint32_t)row * ldb + (uint32_t)((dma_p ^ swz<D>(row)) << 4));
         }
     };
@@ -303,34 +312,35 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
     // into the other buffers (K(j), V(j) live in buffers j&1).  The loop is unrolled by two
     // so buffer indices are constants.  The two waves sharing a SIMD (different workgroups)
     // overlap each other's phases.
-    auto iteration = [&](auto Pc, int t, bool fixed) __attribute__((always_inline)) {
-        constexpr int P = decltype(Pc)::value;  // = t & 1
-        if (t + 1 < ntiles) {
+    auto iteration = [&](auto Pc, int i, bool fixed) __attribute__((always_inline)) {
+        constexpr int P = decltype(Pc)::value;  // = i & 1
+        const int t = tb + i;
+        if (t + 1 < te) {
             issue(t + 1, 0, P ^ 1);
             issue(t + 1, 1, P ^ 1);
         }
-        if (t < n_act) {
-            stage_s(smem[0][P], I0{});
+        if (t < te && t < n_act) {
+            stage_s(smem[grp][0][P], I0{});
             if (t >= n_plain) stage_mask(t, I0{});
             bool bad = false;
-            if (t == 0 && !fixed) softmax_first(I0{});
+            if (t == tb && !fixed) softmax_first(I0{});
             else bad = softmax_next(I0{});
             if (__any(bad) && lane == 0) redo = 1;
-            stage_pv(smem[1][P], I0{});
+            stage_pv(smem[grp][1][P], I0{});
         }
         wait_dma();
         __syncthreads();
     };
     auto main_loop = [&](bool fixed) __attribute__((always_inline)) {
-        if (ntiles > 0) {
-            issue(0, 0, 0);
-            issue(0, 1, 0);
+        if (tb < te) {
+            issue(tb, 0, 0);
+            issue(tb, 1, 0);
         }
         wait_dma();
         __syncthreads();
-        for (int t = 0; t < ntiles; t += 2) {
-            iteration(I0{}, t, fixed);
-            if (t + 1 < ntiles) iteration(I1{}, t + 1, fixed);
+        for (int i = 0; i < nit; i += 2) {
+            iteration(I0{}, i, fixed);
+            if (i + 1 < nit) iteration(I1{}, i + 1, fixed);
         }
     };
 
@@ -345,12 +355,13 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
             mx[qb] = -INFINITY;
             cinit[qb] = f32x16{};
         }
-        for (int t = 0; t < ntiles; ++t) {
-            issue(t, 0, 0);
+        for (int i = 0; i < nit; ++i) {
+            const int t = tb + i;
+            if (t < te) issue(t, 0, 0);
             wait_dma();
             __syncthreads();
-            if (t < n_act) {
-                stage_s(smem[0][0], I0{});
+            if (t < te && t < n_act) {
+                stage_s(smem[grp][0][0], I0{});
                 if (t >= n_plain) stage_mask(t, I0{});
                 float tm[QB];
                 row_max(I0{}, tm);
@@ -368,6 +379,48 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
         }
         set_cinit();
         main_loop(true);
+    }
+
+    if constexpr (KSPLIT == 2) {
+        // Group 1's m, partial row sums and O^T accumulators to group 0 (the buffers are free:
+        // the last iteration ended with every DMA done and a barrier).  Element j of the
+        // state of wave gw's lane sits at float (j*4 + gw)*64 + lane.
+        constexpr int NV = QB * (2 + NDB * 16);
+        float* xs = reinterpret_cast<float*>(&smem[0][0][0][0]);
+        static_assert(NV * 4 * 64 * 4 <= (int)sizeof(smem), "merge state fits the tile buffers");
+        auto at = [&](int j) -> float& { return xs[(j * 4 + gw) * 64 + lane]; };
+        if (grp == 1) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                at(qb * (2 + NDB * 16)) = m[qb];
+                at(qb * (2 + NDB * 16) + 1) = lsum[qb];
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) at(qb * (2 + NDB * 16) + 2 + db * 16 + r) = o[db][qb][r];
+            }
+        }
+        __syncthreads();
+        if (grp == 1) return;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            const int base = qb * (2 + NDB * 16);
+            const float m1 = at(base), l1 = at(base + 1);
+            // a side without a visible key of the row (its row sum 0) takes no part
+            const float L0 = half_sum(lsum[qb]), L1 = half_sum(l1);
+            if (L1 > 0.f) {
+                const float mn = L0 > 0.f ? fmaxf(m[qb], m1) : m1;
+                const float a0 = L0 > 0.f ? fast_exp2(m[qb] - mn) : 0.f;
+                const float a1 = fast_exp2(m1 - mn);
+                lsum[qb] = lsum[qb] * a0 + l1 * a1;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        o[db][qb][r] = o[db][qb][r] * a0 + at(base + 2 + db * 16 + r) * a1;
+                m[qb] = mn;
+            }
+        }
     }
 
 #pragma unroll
@@ -392,15 +445,37 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
     }
 }
 
+// Compute units of the current device (cached per device; 0 if it cannot be read).
+static int compute_units() {
+    static int cached[64];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cached[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 template <int D, int DT>
 static int launch_fwd_t(const FwdArgs& a) {
     constexpr int QB = 1;  // 32-row blocks per wave
     constexpr int BM = 128 * QB;
     const int n_qblk = (a.S + BM - 1) / BM;
-    dim3 grid((unsigned)(a.B * a.Hq * n_qblk)), block(256);
-    hipLaunchKernelGGL((fa_fwd_kernel<D, DT, QB>), grid, block, 0, (hipStream_t)a.stream,
-                       (const uint16_t*)a.qkv, (uint16_t*)a.o, a.lse, a.kv_len, a.B, a.S, a.Hq,
-                       a.Hkv, a.scale * 1.4426950408889634f, a.causal, n_qblk);
+    const long long n_wg = (long long)a.B * a.Hq * n_qblk;
+    dim3 grid((unsigned)n_wg);
+    // At most one workgroup per CU: split each block's keys over two groups of waves (the
+    // critical causal block walks half its tiles, and every SIMD holds two waves).
+    if (n_wg <= compute_units()) {
+        hipLaunchKernelGGL((fa_fwd_kernel<D, DT, QB, 2>), grid, dim3(512), 0, (hipStream_t)a.stream,
+                           (const uint16_t*)a.qkv, (uint16_t*)a.o, a.lse, a.kv_len, a.B, a.S, a.Hq,
+                           a.Hkv, a.scale * 1.4426950408889634f, a.causal, n_qblk);
+    } else {
+        hipLaunchKernelGGL((fa_fwd_kernel<D, DT, QB, 1>), grid, dim3(256), 0, (hipStream_t)a.stream,
+                           (const uint16_t*)a.qkv, (uint16_t*)a.o, a.lse, a.kv_len, a.B, a.S, a.Hq,
+                           a.Hkv, a.scale * 1.4426950408889634f, a.causal, n_qblk);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
