@@ -45,7 +45,9 @@ static int op_flags(int op) {
 
 int pr_op_flags(int op) { return op >= 0 && op < PR_OP_COUNT ? op_flags(op) : -1; }
 
-/* ---- the prelude's generators (reference src/tkm_gpu.cu:751-800), restated ---------- */
+/* ---- the prelude's generators (reference src/tkm_gpu.cu:751-800), restated ----------
+ * Pinned bit for bit to the reference's own generator code (tests/golden/rng_vectors.npz,
+ * written by running src/tkm_gpu.cu:751-794 through oracle/ref_rng_harness.hip). */
 typedef struct {
     int type;
     uint32_t s;                 /* xorshift32 state */

@@ -394,8 +394,9 @@ def test_drop_xorshift32_known_answer():
 
 
 def test_drop_pcg32_is_pcg32_srandom():
-    """Generator 3 (the front end's default) is pcg32_srandom(seed ^ 0x853C49E6748FEA9B, idx); the
-    oracle's PCG32 stream is pinned to O'Neill's demo vector above."""
+    """Generator 3 (what the shipped models select with `prng: pcg32`) is
+    pcg32_srandom(seed ^ 0x853C49E6748FEA9B, idx); the oracle's PCG32 stream is pinned to
+    O'Neill's demo vector above."""
     for seed, idx in ((0, 0), (1234, 77), (0x13579BDF, 123456)):
         got = oracle.rng_u32(3, seed, idx, 8)
         want = oracle.pcg32_sequence(seed ^ 0x853C49E6748FEA9B, idx, 8)
@@ -403,10 +404,26 @@ def test_drop_pcg32_is_pcg32_srandom():
 
 
 @pytest.mark.parametrize("rng_type", [1, 2, 3, 4])
+def test_drop_generators_match_the_reference(rng_type):
+    """All four generators, bit for bit, against the reference's own generator code
+    (src/tkm_gpu.cu:751-794, run on the GPU by oracle/ref_rng_harness.hip; vectors written by
+    tests/golden/make_rng_vectors.py): 80 streams (seeds 0, 1, 2^32-1, the runtime's Drop
+    seeds and others; stream indices up to 2^32-1) x 16 draws of rng_u32, and rng_uniform's
+    24-bit float of each draw.  Generator 2 (Wang hash + xorshift32) is the front end's
+    default when a model names no `prng` (src/tkm_core.c:252)."""
+    v = np.load(os.path.join(HERE, "golden", "rng_vectors.npz"))
+    u32 = v[f"u32_{rng_type}"]
+    for k in range(v["seeds"].size):
+        got = oracle.rng_u32(rng_type, int(v["seeds"][k]), int(v["idxs"][k]), u32.shape[1])
+        assert np.array_equal(np.asarray(got, np.uint32), u32[k]), (rng_type, k)
+    uni = (u32 >> 8).astype(np.float32) * np.float32(1.0 / 16777216.0)
+    assert np.array_equal(uni, v[f"uni_{rng_type}"])
+
+
+@pytest.mark.parametrize("rng_type", [1, 2, 3, 4])
 def test_drop_keep_rate_and_pairs(rng_type):
-    """The keep fraction is 1 - p within 5 sigma for every generator (the Wang-hash and
-    counter generators have no published vectors: their bits are parity unpinned beyond this),
-    and the two channels of a pair come from consecutive draws of one stream."""
+    """The keep fraction is 1 - p within 5 sigma for every generator, and the two channels of a
+    pair come from consecutive draws of one stream."""
     rows, C, p = 256, 64, 0.3
     keep = oracle.drop_keep(rows, C, 0x13579BDF, 17, rng_type, p)
     n = keep.size
