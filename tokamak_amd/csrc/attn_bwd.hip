@@ -91,8 +91,12 @@ __global__ __launch_bounds__(256) void fa_bwd_delta_kernel(const uint16_t* __res
 //   dV^T += dO^T P,  dK^T += Q^T dS the P / dS accumulators are the B operands in place,
 //                                  dO^T and Q^T come from transposed LDS reads
 // dK (times scale) and dV are written once; no atomics.
-template <int D, int DT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// KSPLIT = 2 (grids of at most one workgroup per CU): 8 waves in two groups of 4 over the same
+// keys; group g walks every other query tile of the key block's list through its own buffers
+// (its waves load the same K; group 0 moves the V rows both read), and group 1 adds its dK and
+// dV accumulators into group 0's through LDS before group 0 writes them.
+template <int D, int DT, int KSPLIT>
+__global__ __launch_bounds__(256 * KSPLIT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ dout,
                         const float* __restrict__ lse, const float* __restrict__ delta,
                         uint16_t* __restrict__ dqkv, const int32_t* __restrict__ kv_len, int B,
@@ -104,12 +108,13 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
     constexpr int ROWB = D * 2, CPR = D / 8, TILEB = BM * ROWB;
     constexpr int RPI = 64 / CPR;     // rows per DMA instruction
     constexpr int NI = BM / RPI / 4;  // DMA instructions per wave, per tile and tensor
-    __shared__ __attribute__((aligned(1024))) char smem[2][2][TILEB];  // [buffer][Q, dO]
+    __shared__ __attribute__((aligned(1024))) char smem[KSPLIT][2][2][TILEB];  // [group][buffer][Q, dO]
     __shared__ __attribute__((aligned(1024))) char sV[4][32 * ROWB];   // V rows of each wave
-    __shared__ __attribute__((aligned(16))) float sLD[2][2][64];       // [buffer][LSE, D]
+    __shared__ __attribute__((aligned(16))) float sLD[KSPLIT][2][2][64];       // [group][buffer][LSE, D]
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+    const int grp = wv >> 2, wave = wv & 3;                    // key-split group, wave in it
     const int l32 = lane & 31, hi = lane >> 5;
     const int nh = B * Hkv;
     const int kblk = blockIdx.x / nh;  // ascending key block = most query tiles first (causal)
@@ -143,16 +148,20 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
             const int vrows = max(0, min(32, kvl - kw0));
             const auto rv = make_rsrc(bqkv + (size_t)kw0 * ld + (size_t)(Hq + Hkv + kvh) * D,
                                       (uint32_t)vrows * ldb);
+            if (grp == 0) {
 #pragma unroll
-            for (int i = 0; i < 32 / RPI; ++i) {
-                const int r = i * RPI + lane / CPR;
-                dma16(rv, &sV[wave][i * RPI * ROWB],
-                      (uint32_t)r * ldb + (uint32_t)(((lane % CPR) ^ swz<D>(r)) << 4));
+                for (int i = 0; i < 32 / RPI; ++i) {
+                    const int r = i * RPI + lane / CPR;
+                    dma16(rv, &sV[wave][i * RPI * ROWB],
+                          (uint32_t)r * ldb + (uint32_t)(((lane % CPR) ^ swz<D>(r)) << 4));
+                }
             }
         }
         const int qt_begin = causal ? kb0 / BM : 0;
         const int nq = (S + BM - 1) / BM - qt_begin;
         const int iters = g * nq;
+        // group g takes iterations g, g + KSPLIT, ...; every group runs nit (barriers matched)
+        const int nit = (iters + KSPLIT - 1) / KSPLIT;
 
         const int dma_r = lane / CPR, dma_p = lane % CPR;
         auto issue = [&](int it, int buf) __attribute__((always_inline)) {
@@ -164,13 +173,13 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
             for (int i = 0; i < NI; ++i) {
                 const int r0 = (wave * NI + i) * RPI, r = r0 + dma_r;
                 const uint32_t sw = (uint32_t)((dma_p ^ swz<D>(r)) << 4);
-                dma16(rq, &smem[buf][0][r0 * ROWB], (uint32_t)r * ldb + sw);
-                dma16(ro, &smem[buf][1][r0 * ROWB], (uint32_t)r * ldob + sw);
+                dma16(rq, &smem[grp][buf][0][r0 * ROWB], (uint32_t)r * ldb + sw);
+                dma16(ro, &smem[grp][buf][1][r0 * ROWB], (uint32_t)r * ldob + sw);
             }
             if (wave == 0) {
                 const size_t li = ((size_t)b * Hq + h) * S + qr0;
-                dma4(make_rsrc(lse + li, rows * 4), &sLD[buf][0][0], (uint32_t)l32 * 4);
-                dma4(make_rsrc(delta + li, rows * 4), &sLD[buf][1][0], (uint32_t)l32 * 4);
+                dma4(make_rsrc(lse + li, rows * 4), &sLD[grp][buf][0][0], (uint32_t)l32 * 4);
+                dma4(make_rsrc(delta + li, rows * 4), &sLD[grp][buf][1][0], (uint32_t)l32 * 4);
             }
         };
 
@@ -178,18 +187,19 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
         const int trow = (lane & 15) >> 2;
         const int tcol = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
 
-        issue(0, 0);
+        if (grp < iters) issue(grp, 0);
         wait_dma();
         __syncthreads();
 
-        for (int it = 0; it < iters; ++it) {
-            const int buf = it & 1;
+        for (int j = 0; j < nit; ++j) {
+            const int it = grp + j * KSPLIT;
+            const int buf = j & 1;
             const int qr0 = (qt_begin + it % nq) * BM;
-            if (it + 1 < iters) issue(it + 1, buf ^ 1);
-            const bool active = !causal || (qr0 + BM - 1 >= kw0);
+            if (it + KSPLIT < iters) issue(it + KSPLIT, buf ^ 1);
+            const bool active = it < iters && (!causal || (qr0 + BM - 1 >= kw0));
             if (active) {
-                const char* qt = smem[buf][0];
-                const char* ot = smem[buf][1];
+                const char* qt = smem[grp][buf][0];
+                const char* ot = smem[grp][buf][1];
                 f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
@@ -208,8 +218,8 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
                 u32x4 pl[Split<DT>::on ? PKS : 1], sl[Split<DT>::on ? PKS : 1];
 #pragma unroll
                 for (int g4 = 0; g4 < 4; ++g4) {
-                    const f32x4 L = *reinterpret_cast<const f32x4*>(&sLD[buf][0][g4 * 8 + hi * 4]);
-                    const f32x4 Dl = *reinterpret_cast<const f32x4*>(&sLD[buf][1][g4 * 8 + hi * 4]);
+                    const f32x4 L = *reinterpret_cast<const f32x4*>(&sLD[grp][buf][0][g4 * 8 + hi * 4]);
+                    const f32x4 Dl = *reinterpret_cast<const f32x4*>(&sLD[grp][buf][1][g4 * 8 + hi * 4]);
                     float p[4], ds[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -266,6 +276,34 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
             wait_dma();
             __syncthreads();
         }
+    }
+
+    if constexpr (KSPLIT == 2) {
+        // Group 1's dK^T then dV^T accumulators into group 0's, through the Q/dO buffers (free
+        // once the last iteration ended with every DMA done and a barrier): element r of block
+        // db of wave w's lane at float ((db*16 + r)*4 + w)*64 + lane.
+        float* xs = reinterpret_cast<float*>(&smem[0][0][0][0]);
+        static_assert(NDB * 16 * 4 * 64 * 4 <= (int)sizeof(smem), "one accumulator set fits the buffers");
+        auto at = [&](int db, int r) -> float& { return xs[((db * 16 + r) * 4 + wave) * 64 + lane]; };
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+            f32x16(&acc)[NDB] = pass ? dv : dk;
+            if (grp == 1) {
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) at(db, r) = acc[db][r];
+            }
+            __syncthreads();
+            if (grp == 0) {
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[db][r] += at(db, r);
+            }
+            __syncthreads();
+        }
+        if (grp == 1) return;
     }
 
     // dK^T (scaled), dV^T: lane holds key = kw0 + l32, d = db*32 + g4*8 + hi*4 + 0..3.
@@ -505,15 +543,35 @@ static int launch_delta_t(const BwdArgs& a) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+static int compute_units_bwd() {
+    static int cached[64];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cached[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 template <int D, int DT>
 static int launch_dkdv_t(const BwdArgs& a) {
     constexpr int BN = 128;
     const int n_kblk = (a.S + BN - 1) / BN;
-    dim3 grid((unsigned)(a.B * a.Hkv * n_kblk)), block(256);
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, DT>), grid, block, 0, (hipStream_t)a.stream,
-                       (const uint16_t*)a.qkv, (const uint16_t*)a.dout, a.lse, (const float*)a.delta,
-                       (uint16_t*)a.dqkv, a.kv_len, a.B, a.S, a.Hq, a.Hkv, a.scale,
-                       a.scale * 1.4426950408889634f, a.causal);
+    const long long n_wg = (long long)a.B * a.Hkv * n_kblk;
+    dim3 grid((unsigned)n_wg);
+    // At most one workgroup per CU: split each key block's query tiles over two groups of waves.
+    if (n_wg <= compute_units_bwd())
+        hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, DT, 2>), grid, dim3(512), 0, (hipStream_t)a.stream,
+                           (const uint16_t*)a.qkv, (const uint16_t*)a.dout, a.lse, (const float*)a.delta,
+                           (uint16_t*)a.dqkv, a.kv_len, a.B, a.S, a.Hq, a.Hkv, a.scale,
+                           a.scale * 1.4426950408889634f, a.causal);
+    else
+        hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, DT, 1>), grid, dim3(256), 0, (hipStream_t)a.stream,
+                           (const uint16_t*)a.qkv, (const uint16_t*)a.dout, a.lse, (const float*)a.delta,
+                           (uint16_t*)a.dqkv, a.kv_len, a.B, a.S, a.Hq, a.Hkv, a.scale,
+                           a.scale * 1.4426950408889634f, a.causal);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
