@@ -295,7 +295,13 @@ BWD_CASES = [(1, 512, 2, 1, True, None, 3), (2, 700, 4, 2, True, None, 5), (2, 7
              (2, 1024, 4, 2, True, None, 12)]
 
 
-@pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", BWD_CASES)
+# GQA shapes whose last items have one visible query tile per head: past its last item the
+# unfixed dK/dV stream advanced one head per request, past the group's last, and read 256
+# bytes past the end of dO
+DKDV_PAST_END = [(1, 6, 4, 2, True, [2], 1), (2, 800, 4, 2, True, None, 8), (3, 131, 4, 2, True, None, 3)]
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", BWD_CASES + DKDV_PAST_END)
 def test_dkdv_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg):
     """Every workgroup ends, waves meet at every barrier, DMA and stores stay in their tensors,
     and each (key block, batch, kv head) item's dK and dV rows are stored."""
@@ -326,3 +332,41 @@ def test_dq_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d):
     ldb = (Hq + 2 * Hkv) * 256
     heads = {(base - DQKV) % ldb // 256 for _, _, m, base, _ in sim.stores if m == "dqkv"}
     assert heads == set(range(Hq))
+
+
+# ---------------------------------------------------------------- seeded random shapes
+def _random_shapes(seed, n):
+    """Shapes the fixed cases above do not pin down: GQA ratios up to 8, ragged S, per-batch
+    key lengths (0 and S included), and workgroup counts from 1 to a full MI355X."""
+    import random
+    rng = random.Random(seed)
+    out = []
+    while len(out) < n:
+        B = rng.randint(1, 3)
+        Hkv = rng.randint(1, 2)
+        Hq = Hkv * rng.choice((1, 2, 3, 4, 8))
+        if B * Hq > 12:
+            continue
+        S = rng.choice((rng.randint(1, 300), rng.randint(300, 1200)))
+        causal = rng.random() < 0.6
+        kv_len = None
+        if rng.random() < 0.4:
+            kv_len = [rng.choice((0, S, rng.randint(0, S))) for _ in range(B)]
+        n_wg = rng.choice((1, 2, 3, 5, 8, 9, 13, 256))
+        out.append((B, S, Hq, Hkv, causal, kv_len, n_wg))
+    return out
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", _random_shapes(1, 8))
+def test_fwd_scalar_flow_random(B, S, Hq, Hkv, causal, kv_len, n_wg):
+    run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg)
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", _random_shapes(2, 8))
+def test_dkdv_scalar_flow_random(B, S, Hq, Hkv, causal, kv_len, n_wg):
+    run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg)
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", _random_shapes(3, 8))
+def test_dq_scalar_flow_random(B, S, Hq, Hkv, causal, kv_len, n_wg):
+    run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d=(S % 2 == 0))

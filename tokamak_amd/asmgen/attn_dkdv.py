@@ -435,16 +435,19 @@ class Body:
 
     def decode_d(self, sfx):
         """DMA stream: item of round S_KD -> bases, descriptors, QTBD, ITERSD; tile (0, QTL).
-        Past the last item the stream keeps re-reading its item from head 0's last tile (in
-        bounds, never used): left at the head past the group's last, it would read the rows
-        after the item's (past the end of dO for the last batch and kv head)."""
+        Past the last item the stream re-reads its last item's tile (0, QTL) at every request
+        (in bounds, never used): one tile per decode, so that the next request decodes again
+        instead of advancing.  Advancing, it would walk on past the group's last head (one head
+        per request where a head has one visible query tile) and, for the last batch and kv
+        head, read past the end of dO."""
         p, s = self.p, self.s
         I, Z, B, KVH, KVL, KB0 = (S_TMP + k for k in range(6))
         T0, T1, T2 = S_TMP + 6, S_TMP + 7, S_TMP + 8
         self.item_index(S_KD, I)
         s(f"s_cmp_ge_u32 {sr(I)}, {sr(S_NI)}", S(I) + S(S_NI), [("scc", 0)])
         p.branch(f"s_cbranch_scc0 .Ldd_{sfx}", [("scc", 0)], skip_xdl=ACC)
-        s(f"s_mov_b32 {sr(S_ITERSD)}, 0x7fffffff", [], S(S_ITERSD))
+        s(f"s_mov_b32 {sr(S_ITERSD)}, 1", [], S(S_ITERSD))
+        s(f"s_mov_b32 {sr(S_ITD)}, 0", [], S(S_ITD))
         s(f"s_mov_b32 {sr(S_H3)}, 0", [], S(S_H3))
         s(f"s_mov_b32 {sr(S_QT3)}, {sr(S_QTL)}", S(S_QTL), S(S_QT3))
         p.branch(f"s_branch .Lde_{sfx}", skip_xdl=ACC)
