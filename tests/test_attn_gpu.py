@@ -296,6 +296,33 @@ def test_growing_scores_redo_path(gpu, causal, dtype):
     _assert_ok(res)
 
 
+def _random_cases(seed, n):
+    """Seeded shapes beyond the fixed cases: GQA ratios up to 8, ragged S, per-batch key
+    lengths (0 and S included), both head dims and element types, causal or not."""
+    import random
+    rng = random.Random(seed)
+    out = []
+    while len(out) < n:
+        B, Hkv = rng.randint(1, 3), rng.randint(1, 2)
+        Hq = Hkv * rng.choice((1, 2, 3, 4, 8))
+        if B * Hq > 12:
+            continue
+        S = rng.choice((rng.randint(1, 128), rng.randint(129, 600)))
+        kv_len = None
+        if rng.random() < 0.4:
+            kv_len = [rng.choice((0, S, rng.randint(0, S))) for _ in range(B)]
+        D, dtype = rng.choice(((128, "f16"), (128, "f16"), (128, "bf16"), (64, "f16"), (64, "bf16")))
+        out.append((B, S, Hq, Hkv, D, dtype, rng.random() < 0.6, kv_len, rng.randint(0, 1000)))
+    return out
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,D,dtype,causal,kv_len,seed", _random_cases(11, 20))
+def test_random_shapes(gpu, B, S, Hq, Hkv, D, dtype, causal, kv_len, seed):
+    """Forward and backward of seeded random shapes against the oracle (the assembly kernels
+    for fp16 D=128, the HIP kernels otherwise)."""
+    _assert_ok(run_gpu_case(gpu, B, S, Hq, Hkv, D, dtype=dtype, causal=causal, kv_len=kv_len, seed=seed))
+
+
 def test_kernel_paths(gpu):
     """Which kernels each configuration runs (tkm_attn_last_kernels): fp16 D=128 -- the
     config-3 hot path -- takes the three gfx950 assembly kernels, and only it; bf16 and D=64
