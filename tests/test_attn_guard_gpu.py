@@ -9,30 +9,11 @@ After the forward and the backward:
     and did not, would show as NaN).
 Shapes cover both kernel families (the assembly kernels for fp16 D=128, the HIP kernels
 otherwise), GQA, ragged S, per-batch key lengths with 0, and the causal diagonal."""
-import numpy as np
 import pytest
 
 import oracle
 from attn_cases import TOL_BWD, TOL_FWD, compare, from_device, log, split_dqkv
-
-GUARD = 4096   # bytes on each side
-
-
-class Guarded:
-    """A tensor of numel elements of dtype at byte offset GUARD inside an all-ones buffer."""
-
-    def __init__(self, numel, dtype, device):
-        import torch
-        esz = torch.empty(0, dtype=dtype).element_size()
-        self.nbytes = numel * esz
-        self.raw = torch.full((GUARD * 2 + self.nbytes,), 255, dtype=torch.uint8, device=device)
-        self.t = self.raw[GUARD:GUARD + self.nbytes].view(dtype)
-
-    def intact(self):
-        import torch
-        g = torch.cat([self.raw[:GUARD], self.raw[GUARD + self.nbytes:]])
-        return bool((g == 255).all())
-
+from guarded import GUARD, Guarded, from_numpy16
 
 CASES = [  # B, S, Hq, Hkv, D, dtype, causal, kv_len
     (2, 300, 4, 2, 128, "f16", True, None),
@@ -81,8 +62,8 @@ def test_guarded_buffers(gpu, B, S, Hq, Hkv, D, dtype, causal, kv_len):
         kvl = Guarded(B, torch.int32, gpu)
         kvl.t.copy_(torch.tensor(kv_len, dtype=torch.int32))
         bufs.append(kvl)
-    qkv.t.copy_(torch.from_numpy(np.ascontiguousarray(inp["qkv_bits"]).view(np.int16).reshape(-1)).view(tdt))
-    dout.t.copy_(torch.from_numpy(np.ascontiguousarray(inp["dout_bits"]).view(np.int16).reshape(-1)).view(tdt))
+    qkv.t.copy_(from_numpy16(inp["qkv_bits"], dtype))
+    dout.t.copy_(from_numpy16(inp["dout_bits"], dtype))
     attn.gqa_fwd(qkv.t, B, S, Hq, Hkv, D, causal=causal, kv_len=None if kvl is None else kvl.t,
                  out=o.t, lse=lse.t)
     attn.gqa_bwd(qkv.t, o.t, dout.t, lse.t, B, S, Hq, Hkv, D, causal=causal,
