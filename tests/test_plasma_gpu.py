@@ -60,7 +60,10 @@ def _nodes(c):
             for n, fv in items]
 
 
-def run_chain(dev, c, rows, dtype, seed):
+def run_chain(dev, c, rows, dtype, seed, guard=False):
+    """One chain's forward and backward against the oracle.  guard: every tensor is moved into
+    an all-ones (NaN) guarded buffer, the forward's outputs and the backward workspace start
+    as NaN, and the guards must be intact after each call."""
     import torch
     from tokamak_amd import plasma
     C, twin = c["C"], bool(c.get("twin"))
@@ -109,8 +112,21 @@ def run_chain(dev, c, rows, dtype, seed):
     dp_r, dp_b = oracle.round_to(rng.standard_normal((rows, W)).astype(np.float32), dtype)
     tens["din"] = to_device(dp_b, dtype, dev)
 
+    guards, ws = [], None
+    if guard:
+        from guarded import Guarded
+        fwd_outs = {k for k in tens if k == "out" or (isinstance(k, tuple) and k[0] in ("xhat", "istd", "mask"))}
+        for k, v in list(tens.items()):
+            g = Guarded(v.numel(), v.dtype, dev)
+            if k not in fwd_outs:
+                g.t.copy_(v.reshape(-1))
+            tens[k] = g.t.view(v.shape)
+            guards.append(g)
+        ws = Guarded(max(P.bwd_workspace_bytes(rows), 1), torch.uint8, dev)
+        guards.append(ws)
     P.fwd(tens, rows)
     torch.cuda.synchronize()
+    assert all(g.intact() for g in guards)
     plain = {k: v for k, v in params.items() if k[0] in ("w", "beta", "bias", "branch", "keep")}
     ro, rxh, ris = oracle.plasma_fwd(x_r, rows, C, nodes, plain, twin, nl, nr, dtype)
     check16("out", from_device(tens["out"]), ro, dtype)
@@ -121,8 +137,9 @@ def run_chain(dev, c, rows, dtype, seed):
         np.testing.assert_allclose(gis[k], ris[k], rtol=1e-5)
         gxh[k] = from_device(tens[("xhat", k)])
 
-    P.bwd(tens, rows, acc)
+    P.bwd(tens, rows, acc, workspace=None if ws is None else ws.t)
     torch.cuda.synchronize()
+    assert all(g.intact() for g in guards)
     din, dbr, grads = oracle.plasma_bwd(
         g_r, x_r, rows, C, nodes, plain, gxh, gis, twin, nl, nr, dtype, acc_flags=acc, din_prev=dp_r,
         dbranch_prev={k[1]: v for k, v in params.items() if k[0] == "dbranch_prev"},
@@ -144,6 +161,13 @@ def run_chain(dev, c, rows, dtype, seed):
 def test_plasma_chain_parity(gpu, ci, dtype):
     rows = {512: 300, 1536: 130}.get(CHAINS[ci]["C"], 777)
     run_chain(gpu, CHAINS[ci], rows, dtype, seed=ci + 1)
+
+
+@pytest.mark.parametrize("ci", [0, 3, 6, 9, 10], ids=lambda i: f"chain{i}_C{CHAINS[i]['C']}")
+def test_plasma_guarded_buffers(gpu, ci):
+    """The chains' kernels write nothing outside their tensors and every forward output and
+    workspace byte they own (tests/guarded.py); results as in test_plasma_chain_parity."""
+    run_chain(gpu, CHAINS[ci], 131, "f16" if ci % 2 else "bf16", 100 + ci, guard=True)
 
 
 def test_plasma_config4_pre_attention(gpu):
