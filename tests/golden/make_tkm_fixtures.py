@@ -21,7 +21,7 @@ two-layer decoder for the chained-oracle parity test (llama_small.tkm, batch 2),
 reference's models/exotic_llama.tkm (batch 2) and models/llama3_style.tkm (batch 1; its
 structure only), and the inputs of the reference's GPU gradient check (src/main.c:202-306):
 one "input: 1x1x32 / test: <op> -> SoftmaxCE" graph per checked op (batch 2) and its fused
-twin-FC graph (batch 4).  The model texts of the reference are read in place, not copied.
+twin-FC graph (batch 4); and eight seeded random small decoders (random_decoder).  The model texts of the reference are read in place, not copied.
 """
 from __future__ import annotations
 
@@ -50,6 +50,44 @@ FUSED_CHECK = ("input: 1x1x8\nflow:\n  trunk: FC(8) -> Softplus -> FC(8) -> Tanh
                "  } -> Mul -> Softplus -> FC(4) -> SoftmaxCE\n")
 
 
+def random_decoder(seed):
+    """A seeded small decoder in the .tkm DSL: width, heads and GQA ratio, head dim (QKNorm only
+    with 64, as the reference requires), RoPE, causal or not, SwiGLU or GELU feed-forward,
+    one or two layers, vocabulary and batch all drawn.  Returns (text, batch)."""
+    import random
+    r = random.Random(seed)
+    D = r.choice((64, 128))
+    hkv = r.choice((1, 2))
+    hq = hkv * r.choice((1, 2, 4))
+    C, S, V = r.choice((64, 128, 192)), r.choice((16, 32, 48, 64)), r.choice((64, 256))
+    hidden = r.choice((96, 128, 192))
+    qknorm = D == 64 and r.random() < 0.5
+    rope = r.random() < 0.7
+    causal = ", causal=true" if r.random() < 0.7 else ""
+    post = (" -> QKNorm" if qknorm else "") + (" -> RoPE(theta=10000)" if rope else "")
+    if r.random() < 0.6:
+        ffn = ["  branch: RMSNorm -> {", f"    gate: FC({hidden}) -> SiLU", f"    up: FC({hidden})",
+               f"  }} -> Mul -> FC({C})"]
+    else:
+        ffn = [f"  branch: RMSNorm -> FC({hidden}) -> GELU -> FC({C})"]
+    layer = (["attention: {", "  branch: RMSNorm -> {", f"    q: FC({hq * D}){post}",
+              f"    k: FC({hkv * D}){post}", f"    v: FC({hkv * D})",
+              f"  }} -> GQA(q={hq}, kv={hkv}, d={D}{causal}) -> FC({C})", "  skip: Identity", "} -> Add", "",
+              "ffn: {"] + ffn + ["  skip: Identity", "} -> Add"])
+    if r.random() < 0.5:   # two layers (the DSL repeats a block only for counts of 2 and more)
+        body = ["layer x 2: {"] + ["  " + ln if ln else "" for ln in layer] + ["}"]
+    else:
+        body = layer
+    lines = ["input: 1x%dx%d" % (S, C), "prng: pcg32", "", "flow:"] + ["  " + ln if ln else "" for ln in body]
+    lines += ["", f"  head: RMSNorm -> FC({V}) -> SoftmaxCE"]
+    return "\n".join(lines) + "\n", r.choice((1, 2))
+
+
+# seeds picked to cover both head dims, GQA ratios 1 to 4, QKNorm with and without RoPE, causal
+# and not, SwiGLU and GELU, one and two layers
+RANDOM_DECODER_SEEDS = (1000, 1005, 1008, 1010, 1015, 1021, 1029, 1037)
+
+
 def models():
     out = [("cfg4", os.path.join(HERE, "models", "cfg4_llama.tkm"), 8, None),
            ("llama_small", os.path.join(HERE, "models", "llama_small.tkm"), 2, None),
@@ -59,6 +97,9 @@ def models():
     for op in NUMCHECK_OPS:
         name = "numcheck_" + op.split("(")[0]
         out.append((name, None, 2, f"input: 1x1x32\ntest: {op} -> SoftmaxCE"))
+    for seed in RANDOM_DECODER_SEEDS:
+        text, batch = random_decoder(seed)
+        out.append((f"rand_decoder_{seed}", None, batch, text))
     return out
 
 

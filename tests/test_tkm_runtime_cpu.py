@@ -31,6 +31,10 @@ NAMES = sorted({k.split("/")[0] for k in GRAPHS.files})
 REGISTRY = json.load(open(os.path.join(HERE, "golden", "tkm_registry.json")))
 
 
+# seeded random small decoders (tests/golden/make_tkm_fixtures.py: random_decoder)
+RANDOM_DECODERS = sorted({k.split("/")[0] for k in GRAPHS.files if k.startswith("rand_decoder_")})
+
+
 def gjson(name):
     return json.loads(bytes(GRAPHS[name + "/json"]).decode())
 
@@ -97,7 +101,7 @@ def _kernel_params(src, name):
 
 
 @pytest.mark.parametrize("name", ["cfg4", "llama_small", "exotic_llama", "fused_check", "numcheck_LayerScale",
-                                  "llama3_style"])
+                                  "llama3_style"] + RANDOM_DECODERS)
 def test_kernels_take_the_signature_parameters(name):
     """tkm_plasma_{fwd,bwd}_g<N> of every group: the TkmKernelSig's arguments first, in order,
     with its C types and names (src/tkm_core.c:289-382), then only this build's extras."""
@@ -118,7 +122,7 @@ def test_prep_descriptor_mapping():
     """The qkv_prep node's fields (written by the reference's 3-way rule,
     src/tkm_registry.c:750-768) become tkm_prep_desc fields; S = H*W of the group."""
     L = R.lib()
-    for name in ("cfg4", "llama_small", "exotic_llama", "llama3_style"):
+    for name in ["cfg4", "llama_small", "exotic_llama", "llama3_style"] + RANDOM_DECODERS:
         js = gjson(name)
         g = gbuf(name)
         seen = 0
@@ -185,7 +189,8 @@ def test_plasma_descriptor_mapping():
             assert d.channels == grp["C"]
 
 
-@pytest.mark.parametrize("name,dtype", [("exotic_llama", 0), ("fused_check", 1), ("numcheck_Snake", 0)])
+@pytest.mark.parametrize("name,dtype", [("exotic_llama", 0), ("fused_check", 1), ("numcheck_Snake", 0),
+                                        ("rand_decoder_1010", 0), ("rand_decoder_1037", 1)])
 def test_generated_source_compiles(name, dtype):
     """prelude + tkm_codegen_hip_source compiles with hipRTC for gfx950 (no GPU needed)."""
     src = prep.prelude() + "\n" + R.codegen(gbuf(name), dtype)

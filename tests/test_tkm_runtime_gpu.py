@@ -243,7 +243,14 @@ def _chained_case(name, dtype):
     return rt, gs, w0, x, y, rows, C0
 
 
-@pytest.mark.parametrize("name,dtype", [("llama_small", "f16"), ("llama_small", "bf16"), ("exotic_llama", "f16")])
+# seeded random small decoders (tests/golden/make_tkm_fixtures.py: random_decoder): both head
+# dims, GQA ratios 1 to 4, QKNorm with and without RoPE, causal and not, SwiGLU and GELU
+_RANDOM = sorted({k.split("/")[0] for k in np.load(os.path.join(HERE, "golden", "tkm_graphs.npz")).files
+                  if k.startswith("rand_decoder_")})
+
+
+@pytest.mark.parametrize("name,dtype", [("llama_small", "f16"), ("llama_small", "bf16"), ("exotic_llama", "f16")]
+                         + [(n, "f16") for n in _RANDOM] + [(n, "bf16") for n in _RANDOM[::3]])
 def test_step_matches_chained_oracle(gpu, name, dtype):
     """One step at lr 0.05 from the same weights on both sides: the loss within 1e-4 (relative),
     the input gradient within 2e-2 of its largest magnitude, and every learnable tensor's
