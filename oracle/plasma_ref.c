@@ -174,7 +174,9 @@ double pr_op_fwd(int op, double fv, double x, double w, double b) {
         case PR_DYT: return tanh(fv * x) * w;
         case PR_PRELU: return x > 0 ? x : x * w * fv;
         case PR_XATLU: return x * (w * sigm(x) + 1.0 - w);
-        case PR_SOFTPLUS: return log1p(exp(x));
+        /* the reference's user formula log(1.0 + exp(x)) (tkm_registry.c:446-448) runs in
+           float: expf overflows above ln(FLT_MAX) and the result is +inf */
+        case PR_SOFTPLUS: { const double e = exp(x); return isinf((float)e) ? INFINITY : log1p(e); }
         case PR_SNAKE: { const double s = sin(fv * x); return x + s * s / fv; }
         default: return x;
     }

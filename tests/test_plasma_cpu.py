@@ -371,3 +371,19 @@ def test_descriptor_api_rejects_registry_only_ops(name):
     with pytest.raises(plasma.AttnError) as e:
         plasma.source(d)
     assert "registry" in str(e.value)
+
+
+def test_softplus_overflows_as_the_reference_formula():
+    """Softplus is the registry's user formula log(1.0 + exp(x)) (tkm_registry.c:446-448), which
+    the reference's generated code evaluates in float: finite up to ln(FLT_MAX) ~ 88.72, +inf
+    above (expf overflows).  The oracle follows the float evaluation there, not the exact
+    function; checked against numpy's float32 evaluation of the same formula."""
+    op = OPS["Softplus"]
+    with np.errstate(over="ignore"):
+        for x in (-30.0, 0.0, 20.0, 80.0, 88.0, 88.72, 88.73, 100.0, 1000.0):
+            f32 = float(np.log(np.float32(1.0) + np.exp(np.float32(x))))
+            got = oracle.plasma_op(op, 0.0, x)
+            if np.isinf(f32):
+                assert np.isinf(got) and got > 0, (x, got)
+            else:
+                assert got == pytest.approx(f32, rel=1e-6, abs=1e-7), (x, got, f32)

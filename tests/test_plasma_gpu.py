@@ -44,6 +44,8 @@ CHAINS = [
     # a Drop between a gate and a residual add that a norm closes (exotic_llama's group shape)
     dict(C=512, chain=["Bias", ("DyT", 0.5), ("Drop", 0.1, 3, 131), "Add", "RMSNorm"], acc=7),
     dict(C=64, twin=True, left=["Bias", ("Drop", 0.2, 1, 7)], right=["SiLU"], chain=[("Drop", 0.3, 4, 9), "LN"], acc=3),
+    # Softplus past ln(FLT_MAX): the reference's float formula gives +inf there, as this build does
+    dict(C=64, chain=[("Scale", 100.0), "Softplus"], acc=0),
 ]
 
 
