@@ -21,7 +21,7 @@ two-layer decoder for the chained-oracle parity test (llama_small.tkm, batch 2),
 reference's models/exotic_llama.tkm (batch 2) and models/llama3_style.tkm (batch 1; its
 structure only), and the inputs of the reference's GPU gradient check (src/main.c:202-306):
 one "input: 1x1x32 / test: <op> -> SoftmaxCE" graph per checked op (batch 2) and its fused
-twin-FC graph (batch 4); and eight seeded random small decoders (random_decoder).  The model texts of the reference are read in place, not copied.
+twin-FC graph (batch 4); and nine seeded random small decoders (random_decoder).  The model texts of the reference are read in place, not copied.
 """
 from __future__ import annotations
 
@@ -84,8 +84,8 @@ def random_decoder(seed):
 
 
 # seeds picked to cover both head dims, GQA ratios 1 to 4, QKNorm with and without RoPE, causal
-# and not, SwiGLU and GELU, one and two layers
-RANDOM_DECODER_SEEDS = (1000, 1005, 1008, 1010, 1015, 1021, 1029, 1037)
+# and not, SwiGLU and GELU, one and two layers; 2021 (one batch of 16 rows) from a sweep of 30
+RANDOM_DECODER_SEEDS = (1000, 1005, 1008, 1010, 1015, 1021, 1029, 1037, 2021)
 
 
 def models():
