@@ -17,11 +17,10 @@ scale*log2(e)) and dO of its rows sit in AGPRs as the B operands of S^T = K Q^T 
 dP^T = V dO^T, dQ^T (C[m = head dim][n = query]) accumulates in AGPRs.  K and V tiles of 32
 keys go HBM -> LDS by buffer DMA into four buffers, requested three tiles ahead; the DMA
 stream runs on across item boundaries.  Per tile and wave (lane = query row):
-    S^T  = K Q'^T + (-LSE*log2e)     16 MFMAs (the offset is the accumulators' start value,
-                                     constant for the item)
-    dP^T = V dO^T                    16 MFMAs
-    dS^T = exp2(S^T) (dP^T - D)      masked to 0 where the key is hidden, packed to fp16 in
-                                     place as the B operand of
+    S^T  = K Q'^T + (-LSE*log2e)     16 MFMAs (the offsets are the accumulators' start values,
+    dP^T = V dO^T + (-D)             16 MFMAs  constant for the item)
+    dS^T = exp2(S^T) dP^T            masked to 0 where the key is hidden, packed to fp16 in
+                                     dP^T's registers as the B operand of
     dQ^T += K^T dS^T                 16 MFMAs, K^T read transposed (ds_read_b64_tr_b16)
 Every K or V operand read from LDS feeds two MFMAs (both 32-row blocks).  A loop body runs 48
 MFMA slots: S^T/dP^T of the next tile with this tile's elementwise work between them, one
@@ -71,23 +70,25 @@ S_TMP = 64                             # s64..s95
 NEXT_FREE_SGPR = 96
 
 # ---- VGPRs
-V_SET = (0, 64)         # set J: S^T qb at +16qb, dP^T qb at +32+16qb
-V_DS = 128              # packed dS^T: (qb*2 + ks)*4 + w
-V_CS = 144              # -LSE*log2e of the lane's row, 16 copies per qb
-V_RB = 180              # row-read buffers
+V_SET = (0, 64)         # set J: S^T qb at +16qb, dP^T qb at +32+16qb; after the elementwise
+                        # step, the packed dS^T (qb, ks) in dP^T qb's registers 4ks .. 4ks+3
+V_CD = (128, 176)       # -D of the lane's row, 16 copies per qb (dP^T's start values)
+V_CS = 144              # -LSE*log2e of the lane's row, 16 copies per qb (S^T's start values)
+V_RB = 192              # row-read buffers
 V_TB = V_RB + 4 * NRB   # transposed-read buffers
 V_KOFF = V_TB + 4 * NTB
 V_VOFF = V_KOFF + 8
 V_DOFF = V_VOFF + 8     # DMA rows (2)
-V_DA = V_DOFF + 2       # DMA addresses (4)
-V_ND = V_DA + 4         # -D of the lane's row, per qb (2)
-V_L32 = V_ND + 2
+V_DA = V_DOFF + 2       # DMA addresses (2: each is read when its request issues)
+V_L32 = V_DA + 2
 V_HI4 = V_L32 + 1
 V_TK = V_HI4 + 1        # mask thresholds per qb (2)
-V_T = V_TK + 2          # temporaries (8)
+V_T = V_TK + 2          # temporaries (8); D of the lane's row per qb in V_T+1, V_T+2 at an item start
+V_ND = V_T + 1
 assert V_T + 8 <= 256
 V_PT = 100              # prologue lane scratch (score set 1, free until the first body)
-EPI_BASE = V_DS         # epilogue temporaries at an item boundary: clear of the prefetched rows
+EPI_BASE = V_CD[0]      # epilogue temporaries at an item boundary (the start values are rebuilt
+                        # after it): clear of the prefetched rows
 
 # ---- AGPRs
 A_DQ, A_Q, A_O = 0, 128, 192
@@ -302,12 +303,12 @@ class Body:
         k = (0 if which == "k" else 2) + i
         off = jb * BUFB + (TILE if which == "v" else 0) + i * 1024
         self.s(f"s_add_u32 m0, {sr(S_LDSW)}, {off}", S(S_LDSW), [("m0", 0)])
-        self.p.valu(f"v_add_u32_e32 {vr(V_DA + k)}, {sr(S_TK)}, {vr(V_DOFF + i)}", S(S_TK) + V(V_DOFF + i), V(V_DA + k))
+        self.p.valu(f"v_add_u32_e32 {vr(V_DA + k % 2)}, {sr(S_TK)}, {vr(V_DOFF + i)}", S(S_TK) + V(V_DOFF + i), V(V_DA + k % 2))
 
     def dma_ld(self, which, i):
         k = (0 if which == "k" else 2) + i
         rs = S_RK if which == "k" else S_RV
-        self.p.dma(f"buffer_load_dwordx4 {vr(V_DA + k)}, {sr(rs, 4)}, 0 offen lds", V(V_DA + k) + S(rs, 4))
+        self.p.dma(f"buffer_load_dwordx4 {vr(V_DA + k % 2)}, {sr(rs, 4)}, 0 offen lds", V(V_DA + k % 2) + S(rs, 4))
 
     def dma_all(self, jb):
         for which, i in self.DMA_ORDER:
@@ -341,18 +342,23 @@ class Body:
         which, qb = k4 // 2, k4 % 2
         dst = sblk(J, which, qb)
         if ks == 0:
-            c = V_CS + 16 * qb if which == 0 else None
+            c = V_CS + 16 * qb if which == 0 else V_CD[qb]
         else:
             c = dst
         b = (A_Q if which == 0 else A_O) + (qb * 8 + ks) * 4
         self.p.mfma(MFMA, dst, V_RB + ((2 * ks + which) % NRB) * 4, b, c, b_acc=True)
 
-    def dq_mfma(self, j):
-        """Slot j of dQ^T: vi = j // 2 (ks = vi // 4, db = vi % 4), qb = j % 2."""
+    @staticmethod
+    def ds_reg(J, qb, ks):
+        """First of the four registers of packed dS^T (qb, ks) of set J (in dP^T qb's registers)."""
+        return sblk(J, 1, qb) + 4 * ks
+
+    def dq_mfma(self, j, J):
+        """Slot j of dQ^T from set J: vi = j // 2 (ks = vi // 4, db = vi % 4), qb = j % 2."""
         vi, qb = j // 2, j % 2
         ks, db = vi // 4, vi % 4
         acc = A_DQ + (db * 2 + qb) * 16
-        self.p.mfma(MFMA, acc, V_TB + (vi % NTB) * 4, V_DS + (qb * 2 + ks) * 4, acc, dst_acc=True)
+        self.p.mfma(MFMA, acc, V_TB + (vi % NTB) * 4, self.ds_reg(J, qb, ks), acc, dst_acc=True)
 
     # ---------------------------------------------------------------- elementwise (set J)
     @staticmethod
@@ -373,10 +379,10 @@ class Body:
             if masked:   # hidden iff kc > tq
                 p.valu(f"v_cmp_gt_i32_e32 vcc, {kc(r0 + k)}, {vr(V_TK + qb)}", V(V_TK + qb), [("vcc", 0)])
                 p.valu(f"v_cndmask_b32_e64 {vr(x + k)}, {vr(x + k)}, 0, vcc", V(x + k) + [("vcc", 0)], V(x + k))
-            p.valu(f"v_add_f32_e32 {vr(dp + k)}, {vr(V_ND + qb)}, {vr(dp + k)}", V(V_ND + qb) + V(dp + k), V(dp + k))
             p.valu(f"v_mul_f32_e32 {vr(dp + k)}, {vr(x + k)}, {vr(dp + k)}", V(x + k) + V(dp + k), V(dp + k))
-        p.valu(f"v_cvt_pk_f16_f32 {vr(V_DS + (qb * 2 + ks) * 4 + w)}, {vr(dp)}, {vr(dp + 1)}", V(dp, 2),
-               V(V_DS + (qb * 2 + ks) * 4 + w))
+        # dS^T word (qb, ks, w) goes to register 4ks + w of dP^T qb: read by this step or an earlier one
+        ds = self.ds_reg(J, qb, ks) + w
+        p.valu(f"v_cvt_pk_f16_f32 {vr(ds)}, {vr(dp)}, {vr(dp + 1)}", V(dp, 2), V(ds))
 
     def mask_threshold(self):
         """Per qb: tq = min(causal ? q - k0 - 4hi : big, kvl - 1 - k0 - 4hi), k0 = 32*IT, q =
@@ -450,7 +456,7 @@ class Body:
                 which, i = self.DMA_ORDER[dma_at[s_]]
                 self.dma_m0(which, jb3, i)
             if ew:
-                self.dq_mfma(s_ - 32)
+                self.dq_mfma(s_ - 32, J0)
             if s_ in dma_at:
                 which, i = self.DMA_ORDER[dma_at[s_]]
                 self.dma_ld(which, i)
@@ -651,7 +657,10 @@ class Body:
             p.valu(f"v_mul_f32_e32 {vr(c)}, 0xbfb8aa3b, {vr(V_T + 5 + qb)}", V(V_T + 5 + qb), V(c))
             for r in range(1, 16):
                 p.valu(f"v_mov_b32_e32 {vr(c + r)}, {vr(c)}", V(c), V(c + r))
-            p.valu(f"v_sub_f32_e32 {vr(V_ND + qb)}, 0, {vr(V_ND + qb)}", V(V_ND + qb), V(V_ND + qb))
+            d = V_CD[qb]
+            p.valu(f"v_sub_f32_e32 {vr(d)}, 0, {vr(V_ND + qb)}", V(V_ND + qb), V(d))
+            for r in range(1, 16):
+                p.valu(f"v_mov_b32_e32 {vr(d + r)}, {vr(d)}", V(d), V(d + r))
 
     def epilogue(self, base=8):
         """dQ^T * scale of the current item: lane holds row q0 + 32qb + l32, d = db*32 + g4*8 +
