@@ -120,16 +120,18 @@ def test_gqa_equals_repeated_heads_full_size(gpu):
         assert not st["n_bad"], st
 
 
-def test_config5_fwdbwd_all_heads(gpu):
-    """BASELINE config 5: fp16 non-causal B2 H32 S8192 D128 with per-batch kv_len {8192, 5000}
-    (3192 padded keys, a partial last tile), forward + backward at full size.  Every head is
-    checked: heads are independent (Hq = Hkv), so the oracle runs on groups of 8 heads as the
-    8-head problem made of their Q, K, V and dO columns, covering O, LSE, dQ, dK and dV of
-    every row of both batches."""
+CFG5 = dict(B=2, S=8192, H=32, D=128, kvl=[8192, 5000])
+
+
+@pytest.fixture(scope="module")
+def cfg5_run(gpu):
+    """BASELINE config 5 run once on the GPU: fp16 non-causal B2 H32 S8192 D128 with per-batch
+    kv_len {8192, 5000} (3192 padded keys, a partial last tile), forward + backward at full
+    size; the inputs and the outputs (host copies) for the per-head-group checks."""
     import torch
     from tokamak_amd import attn
-    B, S, H, D, kvl = 2, 8192, 32, 128, [8192, 5000]
-    log(f"[case] config 5 B{B} S{S} Hq{H} Hkv{H} D{D} f16 causal=0 kv_len={kvl}; oracle on all heads")
+    B, S, H, D, kvl = (CFG5[k] for k in ("B", "S", "H", "D", "kvl"))
+    log(f"[case] config 5 B{B} S{S} Hq{H} Hkv{H} D{D} f16 causal=0 kv_len={kvl}")
     inp = oracle.make_inputs(B, S, H, H, D, "f16", seed_qkv=5, seed_do=6)
     qkv = to_device(inp["qkv_bits"], "f16", gpu)
     dout = to_device(inp["dout_bits"], "f16", gpu)
@@ -137,27 +139,35 @@ def test_config5_fwdbwd_all_heads(gpu):
     o, lse = attn.gqa_fwd(qkv, B, S, H, H, D, causal=False, kv_len=kv)
     dqkv = attn.gqa_bwd(qkv, o, dout, lse, B, S, H, H, D, causal=False, kv_len=kv)
     torch.cuda.synchronize()
-    o_g, lse_g, d_g = from_device(o), from_device(lse), from_device(dqkv)
+    out = dict(inp=inp, o=from_device(o), lse=from_device(lse), d=from_device(dqkv))
     del qkv, dout, o, lse, dqkv
-    res = []
-    for h0 in range(0, H, 8):
-        heads = list(range(h0, h0 + 8))
+    return out
 
-        def cols(first):
-            return np.concatenate([np.arange((first + h) * D, (first + h + 1) * D) for h in heads])
-        n, qkv_cols = len(heads), np.concatenate([cols(0), cols(H), cols(2 * H)])
-        o_ref, lse_ref = oracle.fwd(inp["qkv"][:, :, qkv_cols], B, S, n, n, D, causal=False, kv_len=kvl)
-        part = [compare(f"O[h{h0}+]", o_g[:, :, cols(0)], o_ref, TOL_FWD),
-                compare(f"LSE[h{h0}+]", lse_g[:, heads, :], lse_ref, TOL_FWD)]
-        d_ref = oracle.bwd(inp["qkv"][:, :, qkv_cols], oracle.round_to(o_ref, "f16")[0],
-                           inp["dout"][:, :, cols(0)], lse_ref, B, S, n, n, D, causal=False, kv_len=kvl)
-        for nm, g, r in zip(("dQ", "dK", "dV"), split_dqkv(d_g[:, :, qkv_cols], B, S, n, n, D),
-                            split_dqkv(d_ref, B, S, n, n, D)):
-            part.append(compare(f"{nm}[h{h0}+]", g, r, TOL_BWD))
-        for st in part:
-            log(f"    {st['name']:>9}: max_abs={st['max_abs']:.3e} max_rel={st['max_rel']:.3e} "
-                f"bad={st['n_bad']}/{st['n']}")
-        res += part
+
+@pytest.mark.parametrize("h0", [0, 8, 16, 24], ids=lambda h: f"heads{h}-{h + 7}")
+def test_config5_fwdbwd_all_heads(cfg5_run, h0):
+    """Config 5, every head over the four cases: heads are independent (Hq = Hkv), so the
+    oracle runs on heads h0 .. h0+7 as the 8-head problem made of their Q, K, V and dO
+    columns, covering O, LSE, dQ, dK and dV of every row of both batches."""
+    B, S, H, D, kvl = (CFG5[k] for k in ("B", "S", "H", "D", "kvl"))
+    inp, o_g, lse_g, d_g = cfg5_run["inp"], cfg5_run["o"], cfg5_run["lse"], cfg5_run["d"]
+    heads = list(range(h0, h0 + 8))
+
+    def cols(first):
+        return np.concatenate([np.arange((first + h) * D, (first + h + 1) * D) for h in heads])
+    n, qkv_cols = len(heads), np.concatenate([cols(0), cols(H), cols(2 * H)])
+    log(f"[case] config 5 oracle on heads {h0}..{h0 + 7}")
+    o_ref, lse_ref = oracle.fwd(inp["qkv"][:, :, qkv_cols], B, S, n, n, D, causal=False, kv_len=kvl)
+    res = [compare(f"O[h{h0}+]", o_g[:, :, cols(0)], o_ref, TOL_FWD),
+           compare(f"LSE[h{h0}+]", lse_g[:, heads, :], lse_ref, TOL_FWD)]
+    d_ref = oracle.bwd(inp["qkv"][:, :, qkv_cols], oracle.round_to(o_ref, "f16")[0],
+                       inp["dout"][:, :, cols(0)], lse_ref, B, S, n, n, D, causal=False, kv_len=kvl)
+    for nm, g, r in zip(("dQ", "dK", "dV"), split_dqkv(d_g[:, :, qkv_cols], B, S, n, n, D),
+                        split_dqkv(d_ref, B, S, n, n, D)):
+        res.append(compare(f"{nm}[h{h0}+]", g, r, TOL_BWD))
+    for st in res:
+        log(f"    {st['name']:>9}: max_abs={st['max_abs']:.3e} max_rel={st['max_rel']:.3e} "
+            f"bad={st['n_bad']}/{st['n']}")
     _assert_ok(res)
 
 
