@@ -339,6 +339,8 @@ def test_random_shapes(gpu, B, S, Hq, Hkv, D, dtype, causal, kv_len, seed):
     (1, 98, 8, 1, 128, "f16", True, [6], 448),
     (2, 300, 4, 2, 128, "f16", False, [3, 300], 8),
     (1, 200, 2, 2, 64, "bf16", True, [5], 9),
+    (3, 1265, 32, 8, 64, "f16", True, [0, 464, 6], 7),
+    (4, 1187, 32, 8, 128, "f16", True, [1187, 1187, 14, 1187], 93),
 ])
 def test_backward_on_forward_state(gpu, B, S, Hq, Hkv, D, dtype, causal, kv_len, seed):
     """The backward kernels on their own inputs: the oracle's backward takes the O and LSE that
@@ -348,7 +350,9 @@ def test_backward_on_forward_state(gpu, B, S, Hq, Hkv, D, dtype, causal, kv_len,
     every P is of order 1 and dK, dV sum hundreds of (row, head) terms, so the forward's rounding
     (P to 16 bits before PV, as the reference's, tkm_gpu.cu:402; LSE to fp32) carried through
     D = sum(O dO) and P = exp(s - LSE) puts one element per shape just past the gradient bar.
-    On the forward's state each is within it."""
+    On the forward's state each is within it.  The last two are the same effect in shapes that
+    walk several rounds of work items (a batch with 6 or 14 visible keys per row, 4 q-heads
+    per kv head), one for each kernel family."""
     import torch
     from tokamak_amd import attn
     log(f"[case] backward on the forward's state B{B} S{S} Hq{Hq} Hkv{Hkv} D{D} {dtype} "
