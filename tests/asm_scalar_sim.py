@@ -84,6 +84,7 @@ class Wave:
         self.wg, self.wave = wg, wave
         self.done = False
         self.loads = []         # (destination operand, descriptor base) of plain buffer loads
+        self.load_nrec = {}     # descriptor base -> num_records of the plain buffer loads
         self.vscal = {}         # vgpr -> (scalar offset, largest lane offset) (lane reach)
 
     def get(self, o, w64=False):
@@ -183,13 +184,14 @@ class Sim:
                 return
 
     def _inside(self, base, nrec, what):
-        """The tensor a descriptor lies in.  A descriptor covers whole rows of pitch bytes of
-        which lanes touch only the first row_bytes, so its last row may end past the tensor
-        by pitch - row_bytes."""
+        """The tensor a descriptor lies in: every byte of [base, base + num_records) must be
+        inside it, so that no request through the descriptor, whatever its lane offsets, can
+        reach memory past the tensor's end (the hardware drops only offsets at or past
+        num_records)."""
         if nrec == 0:
             return None
         for name, (b0, size, pitch, row_bytes) in self.mem.items():
-            if b0 <= base and base + nrec - pitch + row_bytes <= b0 + size:
+            if b0 <= base and base + nrec <= b0 + size:
                 return name
         raise Fail(f"{what}: descriptor [{base:#x}, +{nrec}) outside every tensor")
 
@@ -324,6 +326,7 @@ class Sim:
             base, nrec, _ = self._desc(w, a[2])
             self._inside(base, nrec, text)
             w.loads.append((a[0], base))
+            w.load_nrec[base] = nrec
             return
         if op.startswith("buffer_store"):
             base, nrec, _ = self._desc(w, a[2])

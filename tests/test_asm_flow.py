@@ -66,7 +66,7 @@ def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, overflow=()):
     def tile(b, kvh, qblk, t, v):
         col = (Hq + (Hkv if v else 0) + kvh) * 256
         rows = max(0, min(64, kvend(b, qblk) - 64 * t))
-        return QKV + (b * S + 64 * t) * ldb + col, rows * ldb
+        return QKV + (b * S + 64 * t) * ldb + col, (rows - 1) * ldb + 256 if rows else 0
 
     def item_of(w):
         s = w.s
@@ -216,6 +216,11 @@ def run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg):
             w.loads.clear()
         elif words[0] == "item":
             b, kvh, kw0 = w.s[attn_dkdv.S_BA], w.s[attn_dkdv.S_KVHA], w.s[attn_dkdv.S_KW0]
+            # the stream's Q / dO descriptors end at the last row's last head of the kv group
+            G = Hq // Hkv
+            got = (w.s[attn_dkdv.S_RQ + 2], w.s[attn_dkdv.S_RO + 2])
+            if got != ((S - 1) * ldb + G * 256, (S - 1) * ldo + G * 256):
+                raise Fail(f"Q / dO descriptor sizes {got}")
             loads = next_kv.pop((w.wg, w.wave))
             if sorted(o[1] for o, _ in loads) != list(range(attn_dkdv.A_NK, attn_dkdv.A_NV + 32, 4)):
                 raise Fail(f"next-item K/V loads into {sorted(o[1] for o, _ in loads)}")
@@ -274,6 +279,10 @@ def run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d):
             got = sorted(w.loads)
             if got != want:
                 raise Fail(f"next-item row loads {got[:3]}..., expected {want[:3]}...")
+            # each row descriptor ends at the batch's last row of the head
+            for base, ld in ((QKV + row * ldb + col, ldb), (DOUT + row * ldo + col, ldo)):
+                if w.load_nrec[base] != (S - 1) * ld + 256:
+                    raise Fail(f"row descriptor at {base:#x}: {w.load_nrec[base]} bytes")
             w.loads.clear()
             checked[0] += 1
 
@@ -370,3 +379,31 @@ def test_dkdv_scalar_flow_random(B, S, Hq, Hkv, causal, kv_len, n_wg):
 @pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", _random_shapes(3, 8))
 def test_dq_scalar_flow_random(B, S, Hq, Hkv, causal, kv_len, n_wg):
     run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d=(S % 2 == 0))
+
+
+# ---------------------------------------------------------------- descriptor reach
+@pytest.mark.parametrize("gen", ["fwd", "dq", "dkdv"])
+def test_descriptors_end_at_the_tensor_end(monkeypatch, gen):
+    """Every descriptor ends at or before the end of its tensor (Sim._inside): a descriptor
+    over whole rows of the packed pitch (rows * stride bytes, the earlier form) reaches up to
+    stride - 256 bytes past the tensor for the last batch's rows, and the check must catch it
+    for each kernel; the kernels as built pass the same shape."""
+    mod = {"fwd": attn_fwd, "dq": attn_dq, "dkdv": attn_dkdv}[gen]
+    shape = (2, 300, 4, 2, True, None, 5)
+    run = {"fwd": lambda: run_fwd(*shape), "dq": lambda: run_dq(*shape, compute_d=True),
+           "dkdv": lambda: run_dkdv(*shape)}[gen]
+    run()
+
+    def whole_rows(self, dst, rows, stride, *width):
+        self.s(f"s_mul_i32 {gfx950.sr(dst)}, {gfx950.sr(rows)}, {gfx950.sr(stride)}",
+               gfx950.S(rows) + gfx950.S(stride), gfx950.S(dst))
+    monkeypatch.setattr(mod.Body, "nrec_rows", whole_rows)
+    key = "fwd" if gen == "fwd" else mod.NAME
+    good = _lines.pop(key)
+    try:
+        # (the forward's tile check, which compares each K/V tile's descriptor with the
+        # expected one, may see the longer descriptor first)
+        with pytest.raises(Fail, match="outside every tensor" if gen != "fwd" else "outside every tensor|holds"):
+            run()
+    finally:
+        _lines[key] = good

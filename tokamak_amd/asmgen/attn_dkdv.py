@@ -172,19 +172,19 @@ class Body:
             self.p = saved
 
     # ---------------------------------------------------------------- descriptors
-    def rsrc(self, dst, base_lo, off_rows_sgpr, stride_sgpr, rows_sgpr, extra_sgpr=None):
-        """dst = buffer descriptor for base + off_rows*stride (+ extra), rows*stride bytes."""
-        s, T = self.s, S_TMP + 8
-        s(f"s_mul_i32 {sr(T)}, {sr(off_rows_sgpr)}, {sr(stride_sgpr)}", S(off_rows_sgpr) + S(stride_sgpr), S(T))
-        s(f"s_mul_hi_u32 {sr(T + 1)}, {sr(off_rows_sgpr)}, {sr(stride_sgpr)}", S(off_rows_sgpr) + S(stride_sgpr), S(T + 1))
-        if extra_sgpr is not None:
-            s(f"s_add_u32 {sr(T)}, {sr(T)}, {sr(extra_sgpr)}", S(T) + S(extra_sgpr), S(T) + [("scc", 0)])
-            s(f"s_addc_u32 {sr(T + 1)}, {sr(T + 1)}, 0", S(T + 1) + [("scc", 0)], S(T + 1))
-        s(f"s_add_u32 {sr(dst)}, {sr(base_lo)}, {sr(T)}", S(base_lo) + S(T), S(dst) + [("scc", 0)])
-        s(f"s_addc_u32 {sr(dst + 1)}, {sr(base_lo + 1)}, {sr(T + 1)}", S(base_lo + 1) + S(T + 1) + [("scc", 0)], S(dst + 1))
-        s(f"s_and_b32 {sr(dst + 1)}, {sr(dst + 1)}, 0xffff", S(dst + 1), S(dst + 1))
-        s(f"s_mul_i32 {sr(dst + 2)}, {sr(rows_sgpr)}, {sr(stride_sgpr)}", S(rows_sgpr) + S(stride_sgpr), S(dst + 2))
-        s(f"s_mov_b32 {sr(dst + 3)}, 0x20000", [], S(dst + 3))
+    def nrec_rows(self, dst, rows, stride, width_sgpr=None):
+        """dst = bytes of a descriptor over `rows` rows of `stride` bytes whose lanes touch
+        the first `width` bytes of each row (256, or the SGPR width_sgpr): (rows-1)*stride +
+        width, 0 without rows.  It ends at the last row's last touched byte, so no request
+        reaches past the tensor's end."""
+        s = self.s
+        s(f"s_mul_i32 {sr(dst)}, {sr(rows)}, {sr(stride)}", S(rows) + S(stride), S(dst))
+        s(f"s_sub_u32 {sr(dst)}, {sr(dst)}, {sr(stride)}", S(dst) + S(stride), S(dst))
+        if width_sgpr is None:
+            s(f"s_add_u32 {sr(dst)}, {sr(dst)}, 0x100", S(dst), S(dst))
+        else:
+            s(f"s_add_u32 {sr(dst)}, {sr(dst)}, {sr(width_sgpr)}", S(dst) + S(width_sgpr), S(dst))
+        s(f"s_max_i32 {sr(dst)}, {sr(dst)}, 0", S(dst), S(dst))
 
     def tile_offsets(self, h_sgpr, qt_sgpr):
         """Byte offsets of tile (head offset h, q-tile qt) from the fixed descriptors:
@@ -540,7 +540,7 @@ class Body:
                 s(f"s_add_u32 {sr(COL)}, {sr(COL)}, {sr(S_TMP + 3)}", S(COL) + S(S_TMP + 3), S(COL))
             self.add64(rs, S_QKV, T0, S_LDB, COL)
             s(f"s_and_b32 {sr(rs + 1)}, {sr(rs + 1)}, 0xffff", S(rs + 1), S(rs + 1))
-            s(f"s_mul_i32 {sr(rs + 2)}, {sr(ROWS)}, {sr(S_LDB)}", S(ROWS) + S(S_LDB), S(rs + 2))
+            self.nrec_rows(rs + 2, ROWS, S_LDB)
             s(f"s_mov_b32 {sr(rs + 3)}, 0x20000", [], S(rs + 3))
         KO = V_T
         p.valu(f"v_mul_lo_u32 {vr(KO)}, {vr(V_L32)}, {sr(S_LDB)}", V(V_L32) + S(S_LDB), V(KO))
@@ -580,7 +580,7 @@ class Body:
                 s(f"s_add_u32 {sr(COL)}, {sr(COL)}, {sr(B)}", S(COL) + S(B), S(COL))
             self.add64(rs, S_QKV, T0, S_LDB, COL)
             s(f"s_and_b32 {sr(rs + 1)}, {sr(rs + 1)}, 0xffff", S(rs + 1), S(rs + 1))
-            s(f"s_mul_i32 {sr(rs + 2)}, {sr(ROWS)}, {sr(S_LDB)}", S(ROWS) + S(S_LDB), S(rs + 2))
+            self.nrec_rows(rs + 2, ROWS, S_LDB)
             s(f"s_mov_b32 {sr(rs + 3)}, 0x20000", [], S(rs + 3))
         KO = V_T
         p.valu(f"v_mul_lo_u32 {vr(KO)}, {vr(V_L32)}, {sr(S_LDB)}", V(V_L32) + S(S_LDB), V(KO))
@@ -639,7 +639,7 @@ class Body:
                 s(f"s_add_u32 {sr(COL)}, {sr(COL)}, {sr(T2)}", S(COL) + S(T2), S(COL))
             self.add64(rs, S_DQKV, T0, S_LDB, COL)
             s(f"s_and_b32 {sr(rs + 1)}, {sr(rs + 1)}, 0xffff", S(rs + 1), S(rs + 1))
-            s(f"s_mul_i32 {sr(rs + 2)}, {sr(S_SEQ)}, {sr(S_LDB)}", S(S_SEQ) + S(S_LDB), S(rs + 2))
+            self.nrec_rows(rs + 2, S_SEQ, S_LDB)
             s(f"s_mov_b32 {sr(rs + 3)}, 0x20000", [], S(rs + 3))
         s(f"s_mul_i32 {sr(EPW)}, {sr(S_WAVE)}, {EPI_WAVE}", S(S_WAVE), S(EPW))
         s(f"s_add_u32 {sr(EPW)}, {sr(EPW)}, {LDS_EPI}", S(EPW), S(EPW))
@@ -838,9 +838,11 @@ def build(check_ldb: int = 12288, check_ldo: int = 4096) -> str:
     p.valu(f"v_mov_b32_e32 {vr(V_L32)}, {vr(L32)}", V(L32), V(V_L32))
     p.valu(f"v_lshlrev_b32_e32 {vr(V_HI4)}, 2, {vr(HI)}", V(HI), V(V_HI4))
     # ---------------------------------------------------------------- DMA descriptor sizes
-    # (the same for every item: a batch's Q / dO rows, a kv group's row values)
-    sal(f"s_mul_i32 {sr(S_RQ + 2)}, {sr(S_SEQ)}, {sr(S_LDB)}", S(S_SEQ) + S(S_LDB), S(S_RQ + 2))
-    sal(f"s_mul_i32 {sr(S_RO + 2)}, {sr(S_SEQ)}, {sr(S_LDO)}", S(S_SEQ) + S(S_LDO), S(S_RO + 2))
+    # (the same for every item: a batch's Q / dO rows up to the last row's last head of the
+    # kv group, a kv group's row values)
+    sal(f"s_lshl_b32 {sr(T0)}, {sr(S_G)}, 8", S(S_G), S(T0))
+    b.nrec_rows(S_RQ + 2, S_SEQ, S_LDB, T0)
+    b.nrec_rows(S_RO + 2, S_SEQ, S_LDO, T0)
     sal(f"s_mul_i32 {sr(S_RL + 2)}, {sr(S_G)}, {sr(S_SP)}", S(S_G) + S(S_SP), S(S_RL + 2))
     sal(f"s_lshl_b32 {sr(S_RL + 2)}, {sr(S_RL + 2)}, 3", S(S_RL + 2), S(S_RL + 2))
     for dst in (S_RQ, S_RO, S_RL):

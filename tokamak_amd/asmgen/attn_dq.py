@@ -135,6 +135,16 @@ class Body:
         s(f"s_add_u32 {sr(dst)}, {sr(src)}, {sr(lo)}", S(src) + S(lo), S(dst) + [("scc", 0)])
         s(f"s_addc_u32 {sr(dst + 1)}, {sr(src + 1)}, {sr(hi)}", S(src + 1) + S(hi) + [("scc", 0)], S(dst + 1))
 
+    def nrec_rows(self, dst, rows, stride):
+        """dst = bytes of a descriptor over `rows` rows of `stride` bytes whose lanes touch
+        the first 256 bytes of each row (one head): (rows-1)*stride + 256, 0 without rows.
+        It ends at the last row's head, so no request reaches past the tensor's end."""
+        s = self.s
+        s(f"s_mul_i32 {sr(dst)}, {sr(rows)}, {sr(stride)}", S(rows) + S(stride), S(dst))
+        s(f"s_sub_u32 {sr(dst)}, {sr(dst)}, {sr(stride)}", S(dst) + S(stride), S(dst))
+        s(f"s_add_u32 {sr(dst)}, {sr(dst)}, 0x100", S(dst), S(dst))
+        s(f"s_max_i32 {sr(dst)}, {sr(dst)}, 0", S(dst), S(dst))
+
     def rsrc(self, dst, src, rows, stride, extra, nrec):
         """Descriptor: base src + rows*stride (+ extra), nrec bytes (SGPR)."""
         self.add64(dst, src, rows, stride, extra)
@@ -220,7 +230,7 @@ class Body:
         s(f"s_mul_i32 {sr(T0)}, {sr(B)}, {sr(S_SEQ)}", S(B) + S(S_SEQ), S(T0))
         s(f"s_add_u32 {sr(COL)}, {sr(S_HQ)}, {sr(KVH)}", S(S_HQ) + S(KVH), S(COL))
         s(f"s_lshl_b32 {sr(COL)}, {sr(COL)}, 8", S(COL), S(COL))
-        s(f"s_mul_i32 {sr(NREC)}, {sr(KVL)}, {sr(S_LDB)}", S(KVL) + S(S_LDB), S(NREC))
+        self.nrec_rows(NREC, KVL, S_LDB)
         self.rsrc(S_RK, S_QKV, T0, S_LDB, COL, NREC)
         s(f"s_lshl_b32 {sr(S_TMP + 10)}, {sr(S_HKV)}, 8", S(S_HKV), S(S_TMP + 10))
         s(f"s_add_u32 {sr(COL)}, {sr(COL)}, {sr(S_TMP + 10)}", S(COL) + S(S_TMP + 10), S(COL))
@@ -487,9 +497,9 @@ class Body:
         T0, COL, NREC = S_TMP, S_TMP + 1, S_TMP + 2
         s(f"s_mul_i32 {sr(T0)}, {sr(b)}, {sr(S_SEQ)}", S(b) + S(S_SEQ), S(T0))
         s(f"s_lshl_b32 {sr(COL)}, {sr(h)}, 8", S(h), S(COL))
-        s(f"s_mul_i32 {sr(NREC)}, {sr(S_SEQ)}, {sr(S_LDB)}", S(S_SEQ) + S(S_LDB), S(NREC))
+        self.nrec_rows(NREC, S_SEQ, S_LDB)
         self.rsrc(RQ, S_QKV, T0, S_LDB, COL, NREC)
-        s(f"s_mul_i32 {sr(NREC)}, {sr(S_SEQ)}, {sr(S_LDO)}", S(S_SEQ) + S(S_LDO), S(NREC))
+        self.nrec_rows(NREC, S_SEQ, S_LDO)
         self.rsrc(RDO, S_DOUT, T0, S_LDO, COL, NREC)
         self.rsrc(RO_, S_O, T0, S_LDO, COL, NREC)
         QO, OO = V_T, V_T + 2
@@ -672,7 +682,7 @@ class Body:
         T0, COL, NREC, EPW, ROW4 = S_TMP, S_TMP + 1, S_TMP + 2, S_TMP + 3, S_TMP + 8
         s(f"s_mul_i32 {sr(T0)}, {sr(S_BA)}, {sr(S_SEQ)}", S(S_BA) + S(S_SEQ), S(T0))
         s(f"s_lshl_b32 {sr(COL)}, {sr(S_HA)}, 8", S(S_HA), S(COL))
-        s(f"s_mul_i32 {sr(NREC)}, {sr(S_SEQ)}, {sr(S_LDB)}", S(S_SEQ) + S(S_LDB), S(NREC))
+        self.nrec_rows(NREC, S_SEQ, S_LDB)
         self.rsrc(RQ, S_DQKV, T0, S_LDB, COL, NREC)
         s(f"s_mul_i32 {sr(EPW)}, {sr(S_WAVE)}, {EPI_WAVE}", S(S_WAVE), S(EPW))
         s(f"s_add_u32 {sr(EPW)}, {sr(EPW)}, {LDS_EPI}", S(EPW), S(EPW))

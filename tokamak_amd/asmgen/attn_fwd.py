@@ -150,16 +150,26 @@ class Body:
         s(f"s_add_u32 {sr(dst)}, {sr(src)}, {sr(lo)}", S(src) + S(lo), S(dst) + [("scc", 0)])
         s(f"s_addc_u32 {sr(dst + 1)}, {sr(src + 1)}, {sr(hi)}", S(src + 1) + S(hi) + [("scc", 0)], S(dst + 1))
 
+    def nrec_rows(self, dst, rows, stride):
+        """dst = bytes of a descriptor over `rows` rows of `stride` bytes whose lanes touch
+        the first 256 bytes of each row (one head): (rows-1)*stride + 256, 0 without rows.
+        It ends at the last row's head, so no request reaches past the tensor's end."""
+        s = self.s
+        s(f"s_mul_i32 {sr(dst)}, {sr(rows)}, {sr(stride)}", S(rows) + S(stride), S(dst))
+        s(f"s_sub_u32 {sr(dst)}, {sr(dst)}, {sr(stride)}", S(dst) + S(stride), S(dst))
+        s(f"s_add_u32 {sr(dst)}, {sr(dst)}, 0x100", S(dst), S(dst))
+        s(f"s_max_i32 {sr(dst)}, {sr(dst)}, 0", S(dst), S(dst))
+
     def rsrc_tile(self, dst, base, t, kvend, tmp):
         """dst[0:3] = descriptor of 64-key tile t (SGPR) of the rows at base (64-bit SGPR
-        pair): rows clamp(kvend - 64t, 0, 64) x ldb bytes."""
+        pair): rows clamp(kvend - 64t, 0, 64) of ldb bytes, up to the last row's head."""
         s = self.s
         k0, rows, lo, hi = tmp, tmp + 1, tmp + 2, tmp + 3
         s(f"s_lshl_b32 {sr(k0)}, {sr(t)}, 6", S(t), S(k0))
         s(f"s_sub_i32 {sr(rows)}, {sr(kvend)}, {sr(k0)}", S(kvend) + S(k0), S(rows))
         s(f"s_min_i32 {sr(rows)}, {sr(rows)}, 64", S(rows), S(rows))
         s(f"s_max_i32 {sr(rows)}, {sr(rows)}, 0", S(rows), S(rows))
-        s(f"s_mul_i32 {sr(dst + 2)}, {sr(rows)}, {sr(S_LDB)}", S(rows) + S(S_LDB), S(dst + 2))
+        self.nrec_rows(dst + 2, rows, S_LDB)
         s(f"s_mul_i32 {sr(lo)}, {sr(k0)}, {sr(S_LDB)}", S(k0) + S(S_LDB), S(lo))
         s(f"s_mul_hi_u32 {sr(hi)}, {sr(k0)}, {sr(S_LDB)}", S(k0) + S(S_LDB), S(hi))
         s(f"s_add_u32 {sr(dst)}, {sr(base)}, {sr(lo)}", S(base) + S(lo), S(dst) + [("scc", 0)])
@@ -631,7 +641,7 @@ class Body:
         s(f"s_lshl_b32 {sr(COL)}, {sr(h)}, 8", S(h), S(COL))
         self.add64(RQ, S_QKV, T0, S_LDB, COL, LO, HI)
         s(f"s_and_b32 {sr(RQ + 1)}, {sr(RQ + 1)}, 0xffff", S(RQ + 1), S(RQ + 1))
-        s(f"s_mul_i32 {sr(RQ + 2)}, {sr(S_SEQ)}, {sr(S_LDB)}", S(S_SEQ) + S(S_LDB), S(RQ + 2))
+        self.nrec_rows(RQ + 2, S_SEQ, S_LDB)
         s(f"s_mov_b32 {sr(RQ + 3)}, 0x20000", [], S(RQ + 3))
         QOFF = V_P  # two registers
         p.valu(f"v_lshlrev_b32_e32 {vr(V_T)}, 2, {vr(V_HI4)}", V(V_HI4), V(V_T))     # 16*hi
@@ -722,11 +732,13 @@ class Body:
         p, s = self.p, self.s
         p.comment("epilogue")
         T0, T1, T2 = S_TMP, S_TMP + 1, S_TMP + 2
-        # O descriptor: base out + b*S*ldo, S*ldo bytes
+        # O descriptor: base out + b*S*ldo + h*256, S rows of ldo bytes up to the last row's head
+        T3 = S_TMP + 3
         s(f"s_mul_i32 {sr(T0)}, {sr(S_BA)}, {sr(S_SEQ)}", S(S_BA) + S(S_SEQ), S(T0))
-        self.add64(S_RQ, S_OUT, T0, S_LDO, None, T1, T2)
+        s(f"s_lshl_b32 {sr(T3)}, {sr(S_HA)}, 8", S(S_HA), S(T3))
+        self.add64(S_RQ, S_OUT, T0, S_LDO, T3, T1, T2)
         s(f"s_and_b32 {sr(S_RQ + 1)}, {sr(S_RQ + 1)}, 0xffff", S(S_RQ + 1), S(S_RQ + 1))
-        s(f"s_mul_i32 {sr(S_RQ + 2)}, {sr(S_SEQ)}, {sr(S_LDO)}", S(S_SEQ) + S(S_LDO), S(S_RQ + 2))
+        self.nrec_rows(S_RQ + 2, S_SEQ, S_LDO)
         s(f"s_mov_b32 {sr(S_RQ + 3)}, 0x20000", [], S(S_RQ + 3))
         # LSE descriptor: base lse + (b*Hq + h)*S*4, S*4 bytes (none when lse is null)
         s(f"s_mul_i32 {sr(T0)}, {sr(S_BA)}, {sr(S_HQ)}", S(S_BA) + S(S_HQ), S(T0))
@@ -741,7 +753,6 @@ class Body:
         s(f"s_cmp_eq_u64 {sr(S_LSE, 2)}, 0", S(S_LSE, 2), [("scc", 0)])
         s(f"s_cselect_b32 {sr(S_RL + 2)}, 0, {sr(S_RL + 2)}", S(S_RL + 2) + [("scc", 0)], S(S_RL + 2))
         s(f"s_mov_b32 {sr(S_RL + 3)}, 0x20000", [], S(S_RL + 3))
-        s(f"s_lshl_b32 {sr(T0)}, {sr(S_HA)}, 8", S(S_HA), S(T0))
         Q, LO, L_, INV, LG = 0, 2, 3, 4, 5           # registers in the free score region
         W = 8                                        # 4 values + 2 packed words
         # staging: write address EPW + l32*272 + hi*8, read address EPW + (lane>>4)*272 +
@@ -761,11 +772,11 @@ class Body:
         p.valu(f"v_mul_u32_u24_e32 {vr(BR)}, {EPI_ROW}, {vr(TA)}", V(TA), V(BR))
         p.valu(f"v_lshl_add_u32 {vr(BR)}, {vr(TB)}, 4, {vr(BR)}", V(TB) + V(BR), V(BR))
         p.valu(f"v_add_u32_e32 {vr(BR)}, {sr(EPW)}, {vr(BR)}", S(EPW) + V(BR), V(BR))
-        # global offset of row q0 + (lane >> 4), chunk lane & 15 of this head; +4 rows per read
+        # offset of row q0 + (lane >> 4), chunk lane & 15 from the head's descriptor; +4 rows
+        # per read
         p.valu(f"v_add_u32_e32 {vr(TA)}, {sr(S_Q0)}, {vr(TA)}", S(S_Q0) + V(TA), V(TA))
         p.valu(f"v_mul_lo_u32 {vr(TA)}, {vr(TA)}, {sr(S_LDO)}", V(TA) + S(S_LDO), V(TA))
         p.valu(f"v_lshl_add_u32 {vr(OOS)}, {vr(TB)}, 4, {vr(TA)}", V(TB) + V(TA), V(OOS))
-        p.valu(f"v_add_u32_e32 {vr(OOS)}, {sr(T0)}, {vr(OOS)}", S(T0) + V(OOS), V(OOS))
         for i in range(1, 16):
             p.valu(f"v_add_u32_e32 {vr(OOS + i)}, {sr(ROW4)}, {vr(OOS + i - 1)}", S(ROW4) + V(OOS + i - 1), V(OOS + i))
         for qb in range(2):

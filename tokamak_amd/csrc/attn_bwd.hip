@@ -147,7 +147,7 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
                 kf[ks] = key < kvl ? ld_global16(kp + ks * 16) : u32x4{0u, 0u, 0u, 0u};
             const int vrows = max(0, min(32, kvl - kw0));
             const auto rv = make_rsrc(bqkv + (size_t)kw0 * ld + (size_t)(Hq + Hkv + kvh) * D,
-                                      (uint32_t)vrows * ldb);
+                                      rows_bytes(vrows, ldb, D * 2));
             if (grp == 0) {
 #pragma unroll
                 for (int i = 0; i < 32 / RPI; ++i) {
@@ -167,8 +167,9 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
         auto issue = [&](int it, int buf) __attribute__((always_inline)) {
             const int h = kvh * g + it / nq, qr0 = (qt_begin + it % nq) * BM;
             const uint32_t rows = (uint32_t)min(BM, S - qr0);
-            const auto rq = make_rsrc(bqkv + (size_t)qr0 * ld + (size_t)h * D, rows * ldb);
-            const auto ro = make_rsrc(dout + ((size_t)b * S + qr0) * ldo + (size_t)h * D, rows * ldob);
+            const auto rq = make_rsrc(bqkv + (size_t)qr0 * ld + (size_t)h * D, rows_bytes(rows, ldb, D * 2));
+            const auto ro = make_rsrc(dout + ((size_t)b * S + qr0) * ldo + (size_t)h * D,
+                                      rows_bytes(rows, ldob, D * 2));
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const int r0 = (wave * NI + i) * RPI, r = r0 + dma_r;
@@ -417,7 +418,7 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
     const int dma_r = lane / CPR, dma_p = lane % CPR;
     auto issue = [&](int t, int buf) __attribute__((always_inline)) {
         const int k0 = t * BN;
-        const uint32_t bytes = (uint32_t)min(BN, kv_end - k0) * ldb;
+        const uint32_t bytes = rows_bytes(min(BN, kv_end - k0), ldb, D * 2);
         const auto rk = make_rsrc(Kb + (size_t)k0 * ldb, bytes);
         const auto rv = make_rsrc(Vb + (size_t)k0 * ldb, bytes);
 #pragma unroll

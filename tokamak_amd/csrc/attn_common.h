@@ -178,6 +178,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
                                              __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000);
 }
+// Bytes a descriptor over `rows` rows of `pitch` bytes needs when lanes touch only the first
+// `width` bytes of each row: it ends at the last row's last touched byte, never at the row's
+// pitch, so no request through it can reach past the tensor that holds those rows.
+__device__ __forceinline__ uint32_t rows_bytes(int rows, uint32_t pitch, uint32_t width) {
+    return rows > 0 ? (uint32_t)(rows - 1) * pitch + width : 0u;
+}
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // 16 bytes per lane from rsrc+voffset into LDS at lds + 16*lane (lds is wave-uniform).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voffset) {

@@ -128,7 +128,7 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
     auto issue = [&](int t, int tensor, int buf) __attribute__((always_inline)) {
         const int k0 = t * BN;
         const auto r = make_rsrc((tensor ? Vb : Kb) + (size_t)k0 * ldb,
-                                 (uint32_t)min(BN, kv_end - k0) * ldb);
+                                 rows_bytes(min(BN, kv_end - k0), ldb, D * 2));
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int r0 = (gw * NI + i) * RPI, row = r0 + dma_r;
