@@ -47,6 +47,7 @@ def lib():
         L.ar_widen_f16.argtypes = [_u16p, _f32p, ctypes.c_size_t]
         L.ar_widen_bf16.argtypes = [_u16p, _f32p, ctypes.c_size_t]
         L.ar_attn_fwd.argtypes = [_f32p, _f32p, _f32p, _i32p] + [ctypes.c_int] * 5 + [ctypes.c_float, ctypes.c_int, ctypes.c_int]
+        L.ar_attn_fwd_pround.argtypes = [_f32p, _f32p, _f32p, _i32p] + [ctypes.c_int] * 5 + [ctypes.c_float, ctypes.c_int]
         L.ar_attn_bwd.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i32p] + [ctypes.c_int] * 5 + [ctypes.c_float, ctypes.c_int, ctypes.c_int]
         L.ar_set_threads.argtypes = [ctypes.c_int]
         L.ar_get_threads.restype = ctypes.c_int
@@ -156,15 +157,21 @@ def online_cpus() -> int:
     return lib().ar_online_cpus()
 
 
-def fwd(qkv, B, S, Hq, Hkv, D, scale=None, causal=True, kv_len=None, f64=False):
-    """Returns (O [B][S][Hq*D], LSE [B][Hq][S]) as float32."""
+def fwd(qkv, B, S, Hq, Hkv, D, scale=None, causal=True, kv_len=None, f64=False, p_f16=False):
+    """Returns (O [B][S][Hq*D], LSE [B][Hq][S]) as float32.  p_f16: the reference kernel's
+    order of work, with P rounded to fp16 before the PV product (ar_attn_fwd_pround; f64 is
+    then ignored: it computes in double apart from that rounding)."""
     qkv = np.ascontiguousarray(qkv, dtype=np.float32)
     assert qkv.size == B * S * (Hq + 2 * Hkv) * D
     scale = 1.0 / np.sqrt(np.float32(D)) if scale is None else scale
     o = np.empty((B, S, Hq * D), dtype=np.float32)
     lse = np.empty((B, Hq, S), dtype=np.float32)
     keep, kvp = _kv(kv_len, B)
-    rc = lib().ar_attn_fwd(_fp(qkv), _fp(o), _fp(lse), kvp, B, S, Hq, Hkv, D, float(scale), int(causal), int(f64))
+    if p_f16:
+        rc = lib().ar_attn_fwd_pround(_fp(qkv), _fp(o), _fp(lse), kvp, B, S, Hq, Hkv, D, float(scale),
+                                      int(causal))
+    else:
+        rc = lib().ar_attn_fwd(_fp(qkv), _fp(o), _fp(lse), kvp, B, S, Hq, Hkv, D, float(scale), int(causal), int(f64))
     if rc != 0:
         raise ValueError("ar_attn_fwd rejected its arguments")
     return o, lse

@@ -270,6 +270,76 @@ AR_DEFINE_FWD(fwd_f64, double, exp, log, 0.0)
 AR_DEFINE_BWD(bwd_f32, float, expf)
 AR_DEFINE_BWD(bwd_f64, double, exp)
 
+/* Forward as the reference's kernel orders it (tkm_gpu.cu:359-435), in double apart from
+ * the one rounding it adds: keys in tiles of 16 (kv_base, 359); per tile the running max
+ * m' = max(m, tile scores) with m starting at -1e30 (356, 388-395), alpha = exp(m - m')
+ * (397), p = exp(s - m') accumulated into the row sum unrounded (399-403, 409) but rounded
+ * to fp16 for the PV product (402, 414-424), O *= alpha (406-408); at the end
+ * O = acc / (l + 1e-8), LSE = m + ln(l + 1e-8) (429-430).  Masked keys (key >= kv_len, or
+ * causal and key > row: 393 with this build's kv_len) add nothing; tiles past the last
+ * visible key are skipped, which changes nothing since their p are exactly 0 and alpha 1. */
+static void fwd_pround(const float *qkv, float *o, float *lse, const int32_t *kv_len,
+                       int B, int S, int Hq, int Hkv, int D, float scale, int causal) {
+    const int g = Hq / Hkv;
+    const size_t ld = (size_t)(Hq + 2 * Hkv) * D, ldo = (size_t)Hq * D;
+    const long total = (long)B * Hq * S;
+    _Pragma("omp parallel num_threads(ar_get_threads())")
+    {
+        double *acc = (double *)malloc(sizeof(double) * (size_t)D);
+        _Pragma("omp for schedule(dynamic, 16)")
+        for (long t = 0; t < total; t++) {
+            int i = (int)(t % S), h = (int)((t / S) % Hq), b = (int)(t / ((long)S * Hq));
+            int kh = h / g, kvl = visible_len(kv_len, b, S);
+            int jend = causal ? (i + 1 < kvl ? i + 1 : kvl) : kvl;
+            const float *base = qkv + (size_t)b * S * ld;
+            const float *q = base + (size_t)i * ld + (size_t)h * D;
+            float *orow = o + ((size_t)b * S + i) * ldo + (size_t)h * D;
+            float *lrow = lse ? lse + ((size_t)b * Hq + h) * S + i : NULL;
+            if (jend <= 0) {
+                for (int d = 0; d < D; d++) orow[d] = 0.0f;
+                if (lrow) *lrow = -INFINITY;
+                continue;
+            }
+            double m = -1e30, l = 0.0, sc[16];
+            for (int d = 0; d < D; d++) acc[d] = 0.0;
+            for (int j0 = 0; j0 < jend; j0 += 16) {
+                int n = jend - j0 < 16 ? jend - j0 : 16;
+                double mt = m;
+                for (int c = 0; c < n; c++) {
+                    const float *k = base + (size_t)(j0 + c) * ld + (size_t)(Hq + kh) * D;
+                    double dot = 0.0;
+                    for (int d = 0; d < D; d++) dot += (double)q[d] * (double)k[d];
+                    sc[c] = dot * (double)scale;
+                    if (sc[c] > mt) mt = sc[c];
+                }
+                double alpha = exp(m - mt), rs = 0.0;
+                for (int d = 0; d < D; d++) acc[d] *= alpha;
+                for (int c = 0; c < n; c++) {
+                    double pe = exp(sc[c] - mt);
+                    float p16 = (float)pe;
+                    ar_round_f16(&p16, NULL, 1);
+                    rs += pe;
+                    const float *v = base + (size_t)(j0 + c) * ld + (size_t)(Hq + Hkv + kh) * D;
+                    for (int d = 0; d < D; d++) acc[d] += (double)p16 * (double)v[d];
+                }
+                l = l * alpha + rs;
+                m = mt;
+            }
+            double inv = 1.0 / (l + 1e-8);
+            for (int d = 0; d < D; d++) orow[d] = (float)(acc[d] * inv);
+            if (lrow) *lrow = (float)(m + log(l + 1e-8));
+        }
+        free(acc);
+    }
+}
+
+int ar_attn_fwd_pround(const float *qkv, float *o, float *lse, const int32_t *kv_len,
+                       int B, int S, int Hq, int Hkv, int D, float scale, int causal) {
+    if (check_args(qkv, o, B, S, Hq, Hkv, D)) return -1;
+    fwd_pround(qkv, o, lse, kv_len, B, S, Hq, Hkv, D, scale, causal);
+    return 0;
+}
+
 int ar_attn_fwd(const float *qkv, float *o, float *lse, const int32_t *kv_len,
                 int B, int S, int Hq, int Hkv, int D, float scale, int causal,
                 int acc_f64) {

@@ -69,6 +69,13 @@ int ar_attn_fwd(const float *qkv, float *o, float *lse, const int32_t *kv_len,
                 int B, int S, int Hq, int Hkv, int D, float scale, int causal,
                 int acc_f64);
 
+/* The forward with the reference kernel's order of work and its fp16 P: online softmax
+ * over tiles of 16 keys with a running max, each p = exp(s - m) rounded to fp16 before
+ * the PV product while the row sum adds the unrounded p (tkm_gpu.cu:359-435); double
+ * elsewhere.  It differs from ar_attn_fwd only by that rounding of P. */
+int ar_attn_fwd_pround(const float *qkv, float *o, float *lse, const int32_t *kv_len,
+                       int B, int S, int Hq, int Hkv, int D, float scale, int causal);
+
 /* Backward: D_i = sum_d O_id dO_id from the given (stored) O; P recomputed
  * from lse; dS = P (dP - D); dQ = scale dS K; dK = scale dS^T Q and
  * dV = P^T dO summed over the q-heads of each kv group. */

@@ -71,3 +71,41 @@ def run_gpu_case(device, B, S, Hq, Hkv, D, dtype="f16", causal=True, kv_len=None
         log(f"    {st['name']:>3}: max_abs={st['max_abs']:.3e} max_rel={st['max_rel']:.3e} "
             f"bad={st['n_bad']}/{st['n']}" + (f" e.g. {st.get('examples')}" if st["n_bad"] else ""))
     return res
+
+
+def gradient_term_rms(qkv, o_stored, dout, lse, B, S, Hq, Hkv, D, causal=True, kv_len=None,
+                      scale=None):
+    """Root of the sum of squares of the terms each gradient element sums (float64, from the
+    oracle's state): dV_jd = sum_i P_ij dO_id, dK_jd = scale sum_i dS_ij q_id (both over the
+    q-heads of the kv group), dQ_id = scale sum_j dS_ij k_jd.  A 16-bit kernel rounds P and dS
+    to its storage type before these products (as the reference rounds P and dS,
+    tkm_gpu.cu:402, 552), so each term carries an independent relative error of about one
+    rounding unit u, and the sum's error is of order u * sqrt(sum of squared terms), whatever
+    the sum's own size: the scale of the rounding error where the terms cancel.  Small shapes
+    only (S x S per head)."""
+    scale = 1.0 / np.sqrt(np.float32(D)) if scale is None else scale
+    g = Hq // Hkv
+    x = qkv.reshape(B, S, Hq + 2 * Hkv, D).astype(np.float64)
+    o = o_stored.reshape(B, S, Hq, D).astype(np.float64)
+    do = dout.reshape(B, S, Hq, D).astype(np.float64)
+    rq = np.zeros((B, S, Hq, D))
+    rk = np.zeros((B, S, Hkv, D))
+    rv = np.zeros((B, S, Hkv, D))
+    i = np.arange(S)[:, None]
+    j = np.arange(S)[None, :]
+    for b in range(B):
+        kvl = S if kv_len is None else max(0, min(int(kv_len[b]), S))
+        vis = (j < kvl) & ((j <= i) if causal else True)
+        for h in range(Hq):
+            kh = h // g
+            q, k, v = x[b, :, h], x[b, :, Hq + kh], x[b, :, Hq + Hkv + kh]
+            L = lse[b, h].astype(np.float64)[:, None]
+            with np.errstate(invalid="ignore", over="ignore"):
+                P = np.where(vis, np.exp(scale * (q @ k.T) - np.where(np.isfinite(L), L, 0.0)), 0.0)
+            dP = do[b, :, h] @ v.T
+            Dv = (o[b, :, h] * do[b, :, h]).sum(axis=1, keepdims=True)
+            dS = P * (dP - Dv)
+            rv[b, :, kh] += (P ** 2).T @ (do[b, :, h] ** 2)
+            rk[b, :, kh] += scale ** 2 * (dS ** 2).T @ (q ** 2)
+            rq[b, :, h] = scale ** 2 * (dS ** 2) @ (k ** 2)
+    return np.sqrt(rq), np.sqrt(rk), np.sqrt(rv)

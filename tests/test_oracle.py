@@ -212,6 +212,94 @@ def test_closed_form_kv_len_one_and_zero():
     np.testing.assert_allclose(d4[0, 0, 2 * H:], do[0].sum(axis=0), rtol=1e-6, atol=1e-6)
 
 
+# ---------------------------------------------- the reference's order of work with fp16 P
+def test_pround_two_keys_closed_form():
+    """Two visible keys.  In one 16-key tile the larger score's p is exactly 1 and the other's
+    exp(-|ds|) is rounded to fp16 for PV while the row sum keeps it unrounded
+    (tkm_gpu.cu:399-409): O = (v_big + r(p) v_small) / (1 + p), LSE = s_big + ln(1 + p).
+    With the keys in different tiles (0 and 17, the keys between scored far below) the
+    rounding follows the running max: if key 17 scores higher, key 0 was stored with p = 1
+    and is rescaled by the unrounded alpha = exp(s_0 - s_17), so O = (alpha v_0 + v_17) /
+    (1 + alpha) with no rounding at all; if key 0 scores higher, key 17's p is rounded as in
+    one tile."""
+    B, S, H, D = 1, 24, 2, 64
+    sc = scale_of(D)
+    seen = set()
+    for kvl, keys in ((2, (0, 1)), (18, (0, 17))):
+        inp = oracle.make_inputs(B, S, H, H, D, "f32", seed_qkv=31)
+        x = inp["qkv"].reshape(B, S, 3 * H, D).astype(np.float32)
+        # every key other than the two: k = -40 q-direction, so its score is hugely negative
+        for j in range(S):
+            if j not in keys:
+                for h in range(H):
+                    x[0, j, H + h] = -40.0 * x[0, S - 1, h] / np.linalg.norm(x[0, S - 1, h])
+        o, lse = oracle.fwd(x, B, S, H, H, D, causal=False, kv_len=[kvl], p_f16=True)
+        o4 = o.reshape(B, S, H, D)
+        i = S - 1
+        for h in range(H):
+            q = x[0, i, h].astype(np.float64)
+            (s0, v0), (s1, v1) = [(sc * q @ x[0, j, H + h].astype(np.float64), x[0, j, 2 * H + h].astype(np.float64))
+                                  for j in keys]
+            p = math.exp(-abs(s1 - s0))
+            if kvl == 18 and s1 > s0:          # key 0 stored first with p = 1, then rescaled
+                want, seen_case = (p * v0 + v1) / (1.0 + p + 1e-8), "rescaled"
+            else:                              # the lower key's p rounded to fp16
+                p16 = float(np.float16(np.float32(p)))
+                assert p16 != p
+                v_hi, v_lo = (v0, v1) if s0 >= s1 else (v1, v0)
+                want, seen_case = (v_hi + p16 * v_lo) / (1.0 + p + 1e-8), "rounded"
+            seen.add((kvl, seen_case))
+            np.testing.assert_allclose(o4[0, i, h], want, rtol=2e-6, atol=2e-7)
+            assert abs(lse[0, h, i] - (max(s0, s1) + math.log(1.0 + p + 1e-8))) < 2e-6
+    assert seen == {(2, "rounded"), (18, "rounded"), (18, "rescaled")}, seen
+
+
+def test_pround_uniform_and_single_key():
+    """K = 0: every p is exactly 1 in every tile (alpha 1 after the first), so O is the exact
+    mean of the visible V over several tiles and LSE = ln(#visible); one visible key gives
+    O = v_0."""
+    B, S, H, D = 1, 40, 2, 128
+    inp = oracle.make_inputs(B, S, H, H, D, "f32", seed_qkv=32)
+    x = inp["qkv"].reshape(B, S, 3 * H, D)
+    x[:, :, H:2 * H] = 0.0
+    o, lse = oracle.fwd(x, B, S, H, H, D, causal=True, p_f16=True)
+    v = x[0, :, 2 * H:].astype(np.float64)
+    for i in range(S):
+        np.testing.assert_allclose(o.reshape(B, S, H, D)[0, i], v[:i + 1].mean(axis=0), rtol=1e-6, atol=1e-6)
+        # (the reference's +1e-8 guard on the row sum: ln(n + 1e-8))
+        np.testing.assert_allclose(lse[0, :, i], math.log(i + 1), rtol=1e-7, atol=2e-8)
+    inp = oracle.make_inputs(2, 12, 2, 2, 64, "f32", seed_qkv=33)
+    o, lse = oracle.fwd(inp["qkv"], 2, 12, 2, 2, 64, causal=False, kv_len=[1, 0], p_f16=True)
+    o4 = o.reshape(2, 12, 2, 64)
+    x = inp["qkv"].reshape(2, 12, 6, 64)
+    for i in range(12):
+        np.testing.assert_allclose(o4[0, i], x[0, 0, 4:], rtol=1e-6, atol=1e-7)
+    assert np.all(o4[1] == 0.0) and np.all(np.isneginf(lse[1]))
+
+
+@pytest.mark.parametrize("growth", [0.0, 0.05])
+def test_pround_within_rounding_of_exact(growth):
+    """Against the float64 forward, the only difference is P's fp16 rounding (relative 2^-11
+    per term): |O - O_exact| <= 2^-11 max|v| per row, LSE equal to float resolution.  With
+    scores growing along the keys (growth > 0) the running max moves every tile, so a wrong
+    or missing rescale would break the bound."""
+    B, S, Hq, Hkv, D = 2, 160, 4, 2, 128
+    inp = oracle.make_inputs(B, S, Hq, Hkv, D, "f16", seed_qkv=34)
+    x = inp["qkv"].reshape(B, S, Hq + 2 * Hkv, D).copy()
+    # scores rise with the key index: add growth * j * (q-direction mean) to every key
+    qdir = x[:, :, :Hq].mean(axis=(1, 2))
+    for j in range(S):
+        x[:, j, Hq:Hq + Hkv] += growth * j * qdir[:, None, :] / max(1e-6, float(np.abs(qdir).max()))
+    for causal, kvl in ((True, None), (False, [160, 37])):
+        o_e, l_e = oracle.fwd(x, B, S, Hq, Hkv, D, causal=causal, kv_len=kvl, f64=True)
+        o_p, l_p = oracle.fwd(x, B, S, Hq, Hkv, D, causal=causal, kv_len=kvl, p_f16=True)
+        vmax = float(np.abs(x[:, :, Hq + Hkv:]).max())
+        err = float(np.abs(o_p - o_e).max())
+        assert err <= 2 ** -11 * vmax + 1e-6, err
+        assert err > 0.0                       # the rounding is there
+        np.testing.assert_allclose(l_p, l_e, rtol=1e-6, atol=1e-5)
+
+
 # ----------------------------------------------------------------- finite differences
 def test_finite_differences_fp64():
     B, S, Hq, Hkv, D = 1, 10, 2, 1, 64

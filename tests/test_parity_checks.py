@@ -57,3 +57,66 @@ def test_check16_ulp_bound():
     g = np.array([1.0 + 2.0 ** -10, 1.0 + 2.0 ** -9, 1.0 - 2.0 ** -12])
     # fp16 ulp at 1.0 is 2^-10; bound = 1 ulp + 1e-6 * 1
     assert check16_mask(g, r, "f16", 1, 1e-6).tolist() == [False, True, False]
+
+
+# ----------------------------------------------------- the rounding-aware gradient bound
+def test_gradient_term_rms_closed_forms():
+    """gradient_term_rms on cases with closed forms: one visible key gives P = 1, dS = 0, so
+    dV_0's terms are the dO rows themselves (rms = sqrt(sum_i dO_i^2)) and dQ, dK have none;
+    two visible keys give P_i0 = 1 / (1 + exp(s_1 - s_0))."""
+    import oracle
+    from attn_cases import gradient_term_rms
+    B, S, Hq, Hkv, D = 1, 40, 2, 1, 64
+    inp = oracle.make_inputs(B, S, Hq, Hkv, D, "f16", seed_qkv=3, seed_do=4)
+    do = inp["dout"].reshape(B, S, Hq, D).astype(np.float64)
+    x = inp["qkv"].reshape(B, S, Hq + 2 * Hkv, D).astype(np.float64)
+    sc = 1.0 / np.sqrt(np.float32(D))
+    for kvl in (1, 2):
+        o, lse = oracle.fwd(inp["qkv"], B, S, Hq, Hkv, D, causal=False, kv_len=[kvl], f64=True)
+        rq, rk, rv = gradient_term_rms(inp["qkv"], o, inp["dout"], lse, B, S, Hq, Hkv, D, causal=False,
+                                       kv_len=[kvl])
+        if kvl == 1:
+            np.testing.assert_allclose(rv[0, 0, 0], np.sqrt((do[0] ** 2).sum(axis=(0, 1))), rtol=1e-6)
+            assert np.abs(rq).max() < 1e-6 and np.abs(rk).max() < 1e-6
+        else:
+            s0 = sc * np.einsum("ihd,d->ih", x[0, :, :Hq], x[0, 0, Hq])
+            s1 = sc * np.einsum("ihd,d->ih", x[0, :, :Hq], x[0, 1, Hq])
+            p0 = 1.0 / (1.0 + np.exp(s1 - s0))
+            want = np.sqrt(np.einsum("ih,ihd->d", p0 ** 2, do[0] ** 2))
+            np.testing.assert_allclose(rv[0, 0, 0], want, rtol=1e-6)
+        assert np.all(rv[0, kvl:] == 0.0)       # keys past kv_len have no terms
+
+
+def test_rounding_bound_catches_a_missing_term():
+    """The widened gradient bound (atol + rtol |r| + 4 u rms, u = 2^-11) still fails a
+    gradient that lacks one row's term P_i0 dO_i, in the most cancelling few-key case of the
+    GPU suite, and passes the exact result perturbed by independent fp16 roundings of P."""
+    import oracle
+    from attn_cases import gradient_term_rms, split_dqkv
+    B, S, Hq, Hkv, D = 1, 327, 2, 1, 128
+    inp = oracle.make_inputs(B, S, Hq, Hkv, D, "f16", seed_qkv=739, seed_do=740)
+    o, lse = oracle.fwd(inp["qkv"], B, S, Hq, Hkv, D, causal=True, kv_len=[2], f64=True)
+    o_st, _ = oracle.round_to(o, "f16")
+    d = oracle.bwd(inp["qkv"], o_st, inp["dout"], lse, B, S, Hq, Hkv, D, causal=True, kv_len=[2], f64=True)
+    _, _, dv = split_dqkv(d, B, S, Hq, Hkv, D)
+    _, _, rv = gradient_term_rms(inp["qkv"], o_st, inp["dout"], lse, B, S, Hq, Hkv, D, causal=True, kv_len=[2])
+    bound = 5e-3 + 2e-2 * np.abs(dv) + 4 * 2.0 ** -11 * rv
+    x = inp["qkv"].reshape(B, S, Hq + 2 * Hkv, D).astype(np.float64)
+    do = inp["dout"].reshape(B, S, Hq, D).astype(np.float64)
+    sc = 1.0 / np.sqrt(np.float32(D))
+    s = sc * np.einsum("hd,jd->hj", x[0, 200, :Hq], x[0, :2, Hq])
+    p = np.exp(s - lse[0, :, 200][:, None])                 # row 200's P over keys 0, 1
+    missing = dv.copy()
+    missing[0, 0, 0] -= p[0, 0] * do[0, 200, 0]
+    assert np.any(np.abs(missing - dv) > bound)
+    # fp16 rounding of every P before the dV product: within the bound
+    i = np.arange(S)[:, None]
+    j = np.arange(S)[None, :]
+    dv16 = np.zeros_like(dv[0, :, 0])
+    for h in range(Hq):
+        sc_all = sc * x[0, :, h] @ x[0, :, Hq].T
+        P = np.where((j <= i) & (j < 2), np.exp(sc_all - lse[0, h][:, None]), 0.0)
+        P16 = P.astype(np.float32).astype(np.float16).astype(np.float64)
+        dv16 += P16.T @ do[0, :, h]
+    err = np.abs(dv16 - dv[0, :, 0])
+    assert np.all(err <= bound[0, :, 0]) and err.max() > 5e-3 * 0.2
