@@ -493,6 +493,13 @@ def run_step(args):
     print(json.dumps(res))
 
 
+# roofline.traffic is not measured by this run: hardware counters need a profiler run of their
+# own (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE).  It is read from the committed summary of
+# those runs, and the line says so.
+TRAFFIC_SOURCE = ("profiles/attn_cfg3_traffic.md: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of "
+                  "this kernel at config 3, not this run")
+
+
 def measured_traffic(name):
     """HBM bytes per launch of a kernel at config 3, from the FETCH_SIZE / WRITE_SIZE counter
     runs summarized in profiles/attn_cfg3_traffic.md (None if absent)."""
@@ -635,12 +642,14 @@ def main():
         roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(ach / PEAK_FP16_TFLOPS, 4),
                 "traffic": measured_traffic(dom) if args.config == "cfg3" else None,
+                "traffic_source": TRAFFIC_SOURCE if args.config == "cfg3" else None,
                 "avg_ms": round(dom_avg, 5), "flops_per_launch": credit[dom]}
     else:
         ach = delta_bytes / (dom_avg * 1e-3) / 1e9
         roof = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
                 "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4),
                 "traffic": measured_traffic(dom) if args.config == "cfg3" else None,
+                "traffic_source": TRAFFIC_SOURCE if args.config == "cfg3" else None,
                 "avg_ms": round(dom_avg, 5)}
 
     value = f_total / (ms_step * 1e-3) / 1e12

@@ -1,3 +1,8 @@
+// SPDX-License-Identifier: MPL-2.0-no-copyleft-exception
+// Copyright (c) 2026 BSODsystem32
+// (The declarations below restate the reference's public interface, include/tkm.h, member for
+// member, so they carry its notice; the comments are this build's.)
+
 /*
  * tkm.h -- the public C interface of the Tokamak runtime, declared for this build's HIP runtime
  * (tokamak_amd/csrc/tkm_hip.c) and HIP code generator (tkm_codegen_hip.c).

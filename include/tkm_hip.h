@@ -74,6 +74,12 @@ typedef struct {
                               label per row (B*H*W), uploaded by tkm_runtime_step_tokens */
     uint64_t init_seed;    /* weight initialization (N(0,1)*sqrt(2/fan_in) for GEMM weights) */
     int verbose;           /* 1: print the ignite summary line */
+    int dataset_mode;      /* tkm_dataset_create: 0 (default) resident when the 16-bit copy fits in
+                              half the free device memory, else streaming (the reference's rule);
+                              1 always resident; 2 always streaming */
+    int clear_all_grads;   /* debug: 1 clears the whole gradient arena at every step, as the
+                              reference does, instead of only the slots whose first writer
+                              accumulates (0, the default); the results must not change */
 } tkm_runtime_opts;
 
 TKM_API void tkm_runtime_opts_init(tkm_runtime_opts *o);

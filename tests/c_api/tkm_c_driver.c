@@ -24,7 +24,18 @@
  *       build), from the same initial weights; modes 1 and 2 must agree bit for bit, modes 0
  *       and 1 within rounding (loss, input gradient, every updated weight).
  *
- * The last two use one function of this build's extensions (include/tkm_hip.h).
+ *   tkm_c_driver dataset
+ *       tkm_runtime_train_dataset and tkm_runtime_eval_dataset through a C loader callback
+ *       (docs/C_API.md 6.5): training over the loader's full batches equals stepping the same
+ *       batches by hand on a second runtime (mean loss and every weight bit for bit); evaluation
+ *       with a short final batch counts what tkm_runtime_eval counts over all samples; a loader
+ *       error, a short training batch and an overfull batch make the helpers fail.
+ *   tkm_c_driver infer
+ *       a tensor-output graph built with the front end's own calls: tkm_runtime_ignite_inference
+ *       and tkm_runtime_ignite on it give bit-equal tkm_runtime_forward outputs, and
+ *       tkm_runtime_forward refuses a short output buffer and a loss graph.
+ *
+ * `source` and `registry` use one function of this build's extensions (include/tkm_hip.h).
  */
 #include <math.h>
 #include <stdint.h>
@@ -223,6 +234,158 @@ static int train(const char *path, int batch, int steps, float lr, const char *w
     return rc;
 }
 
+/* ---- dataset helpers through a loader callback ----------------------------------------- */
+
+typedef struct {
+    const float *x;            /* n samples of `per` floats */
+    const uint8_t *y;
+    size_t n, per, pos;
+    int fail_at;               /* >= 0: the call with this index returns -1 */
+    int calls;
+    int overfill;              /* report one sample more than the capacity */
+} loader;
+
+static int next_batch(void *user, float *h_input, uint8_t *h_labels, size_t capacity, size_t *out_count) {
+    loader *L = (loader *)user;
+    if (L->fail_at >= 0 && L->calls++ == L->fail_at) return -1;
+    const size_t left = L->n - L->pos, k = left < capacity ? left : capacity;
+    if (k == 0) return 0;
+    memcpy(h_input, L->x + L->pos * L->per, k * L->per * sizeof(float));
+    memcpy(h_labels, L->y + L->pos, k);
+    L->pos += k;
+    *out_count = k + (L->overfill ? capacity : 0);
+    return 1;
+}
+
+static const char *const MLP = "input: 1x1x32\nmlp: FC(48) -> SiLU -> FC(10) -> SoftmaxCE\n";
+
+static uint8_t *weights_of(TkmRuntime *rt, size_t *n) {
+    *n = tkm_runtime_weight_bytes(rt);
+    uint8_t *w = (uint8_t *)malloc(*n);
+    if (w && !tkm_save_weights_buffer(rt, w, *n, NULL)) {
+        free(w);
+        w = NULL;
+    }
+    return w;
+}
+
+static int dataset(void) {
+    const int B = 4;
+    const size_t per = 32, full = 5, n = full * B + 3;   /* a short final batch of 3 */
+    float *x = (float *)malloc(n * per * sizeof(float));
+    uint8_t *y = (uint8_t *)malloc(n);
+    uint32_t s = 777u;
+    for (size_t i = 0; i < n * per; ++i) x[i] = ((float)(lcg(&s) >> 8) * (1.0f / 16777216.0f) - 0.5f) * 4.0f;
+    for (size_t i = 0; i < n; ++i) y[i] = (uint8_t)((lcg(&s) >> 24) % 10);
+    TkmRuntime *a = tkm_load_string(MLP, B), *b = tkm_load_string(MLP, B);
+    int rc = !a || !b;
+    if (!rc) {
+        /* training: the loader's batches, the short last one an error, so train the full ones */
+        loader L = {x, y, full * B, per, 0, -1, 0, 0};
+        float avg = NAN;
+        const int ok = tkm_runtime_train_dataset(a, next_batch, &L, 0, 0.05f, &avg);
+        double sum = 0.0;
+        for (size_t k = 0; k < full; ++k) sum += tkm_runtime_step(b, x + k * B * per, y + k * B, 0.05f);
+        const float want = (float)(sum / (double)full);
+        size_t na = 0, nb = 0;
+        uint8_t *wa = weights_of(a, &na), *wb = weights_of(b, &nb);
+        const int same = wa && wb && na == nb && !memcmp(wa, wb, na);
+        printf("  train_dataset: ok %d, mean loss %.7f (by hand %.7f), weights %s\n", ok, avg, want,
+               same ? "bit-equal" : "DIFFER");
+        if (!ok || avg != want || !same) rc = 1;
+        free(wa);
+        free(wb);
+        /* max_batches stops early; the loader's position shows it */
+        loader M = {x, y, full * B, per, 0, -1, 0, 0};
+        if (!tkm_runtime_train_dataset(a, next_batch, &M, 2, 0.0f, &avg) || M.pos != 2 * (size_t)B) rc = 1;
+        /* evaluation over all samples, the last batch short */
+        loader E = {x, y, n, per, 0, -1, 0, 0};
+        int correct = -1;
+        size_t samples = 0;
+        const int eok = tkm_runtime_eval_dataset(a, next_batch, &E, 0, &correct, &samples);
+        const int direct = tkm_runtime_eval(a, x, y, (int)n);
+        printf("  eval_dataset: ok %d, %d correct of %zu (tkm_runtime_eval: %d of %zu)\n", eok, correct, samples,
+               direct, n);
+        if (!eok || samples != n || correct != direct) rc = 1;
+        /* failures: a loader error, a short training batch, an overfull batch, no batch at all */
+        loader F = {x, y, n, per, 0, 1, 0, 0}, G = {x, y, n, per, 0, -1, 0, 0}, H = {x, y, n, per, 0, -1, 0, 1},
+               Z = {x, y, 0, per, 0, -1, 0, 0};
+        const int f1 = tkm_runtime_train_dataset(a, next_batch, &F, 0, 0.0f, &avg);
+        const int f2 = tkm_runtime_train_dataset(a, next_batch, &G, 0, 0.0f, &avg);   /* ends short */
+        const int f3 = tkm_runtime_eval_dataset(a, next_batch, &H, 0, &correct, &samples);
+        const int f4 = tkm_runtime_eval_dataset(a, next_batch, &Z, 0, &correct, &samples);
+        printf("  refused: loader error %d, short training batch %d, overfull batch %d, empty %d\n", !f1, !f2,
+               !f3, !f4);
+        if (f1 || f2 || f3 || f4) rc = 1;
+    }
+    if (a) tkm_runtime_free(a);
+    if (b) tkm_runtime_free(b);
+    free(x);
+    free(y);
+    printf("dataset: %s\n", rc ? "FAIL" : "PASS");
+    return rc;
+}
+
+/* ---- the inference runtime ----------------------------------------------------------------- */
+
+static TkmGraph *front_end(const char *text, int batch) {
+    TkmGraph *g = (TkmGraph *)calloc(1, sizeof(TkmGraph));
+    if (!g) return NULL;
+    tkm_parse_dsl(g, text, batch);
+    tkm_optimize_and_bind(g);
+    tkm_plan_memory(g);
+    return g;
+}
+
+static int infer(void) {
+    const int B = 3;
+    TkmGraph *g = front_end("input: 1x4x32\nmlp: FC(48) -> SiLU -> FC(24) -> Tanh\n", B);
+    char *src = g ? tkm_codegen_cuda_string(g) : NULL;
+    TkmRuntime *inf = src ? tkm_runtime_ignite_inference(g, src) : NULL;
+    TkmRuntime *trn = src ? tkm_runtime_ignite(g, src) : NULL;
+    int rc = !inf || !trn;
+    if (!rc) {
+        const size_t nin = tkm_runtime_input_elements(inf), nout = tkm_runtime_output_elements(inf);
+        float *x = (float *)malloc(nin * sizeof(float));
+        float *oi = (float *)calloc(nout, sizeof(float)), *ot = (float *)calloc(nout, sizeof(float));
+        uint32_t s = 99u;
+        for (size_t i = 0; i < nin; ++i) x[i] = ((float)(lcg(&s) >> 8) * (1.0f / 16777216.0f) - 0.5f) * 2.0f;
+        const size_t gi = tkm_runtime_forward(inf, x, oi, nout), gt = tkm_runtime_forward(trn, x, ot, nout);
+        int finite = 1;
+        for (size_t i = 0; i < nout; ++i) finite &= isfinite(oi[i]) && fabsf(oi[i]) <= 1.0f;
+        const int same = gi == nout && gt == nout && !memcmp(oi, ot, nout * sizeof(float));
+        /* a second call reuses the runtime's buffers and gives the same output */
+        const size_t again = tkm_runtime_forward(inf, x, ot, nout);
+        const int stable = again == nout && !memcmp(oi, ot, nout * sizeof(float));
+        const size_t shortcap = tkm_runtime_forward(inf, x, ot, nout - 1);
+        printf("  forward: %zu outputs (B %d x 4 rows x 24), inference vs training runtime %s, repeat %s, "
+               "short buffer -> %zu\n", nout, B, same ? "bit-equal" : "DIFFER", stable ? "equal" : "DIFFERS",
+               shortcap);
+        if (nout != (size_t)B * 4 * 24 || !same || !finite || !stable || shortcap != 0 ||
+            nin != (size_t)B * 4 * 32)
+            rc = 1;
+        free(x);
+        free(oi);
+        free(ot);
+    }
+    TkmRuntime *loss = tkm_load_string(MLP, 2);
+    if (!loss) {
+        rc = 1;
+    } else {
+        float xin[64] = {0}, out[64];
+        const size_t got = tkm_runtime_forward(loss, xin, out, 64);
+        printf("  loss graph: output elements %zu, forward -> %zu\n", tkm_runtime_output_elements(loss), got);
+        if (got != 0 || tkm_runtime_output_elements(loss) != 0) rc = 1;
+        tkm_runtime_free(loss);
+    }
+    if (inf) tkm_runtime_free(inf);
+    if (trn) tkm_runtime_free(trn);
+    free(src);
+    free(g);
+    printf("infer: %s\n", rc ? "FAIL" : "PASS");
+    return rc;
+}
+
 int main(int argc, char **argv) {
     if (argc >= 2 && !strcmp(argv[1], "numcheck")) {
         const int failed = numcheck();
@@ -233,7 +396,10 @@ int main(int argc, char **argv) {
         return train(argv[2], atoi(argv[3]), atoi(argv[4]), (float)atof(argv[5]), argv[6]);
     if (argc >= 5 && !strcmp(argv[1], "source")) return source(atoi(argv[2]), argv[3], atoi(argv[4]));
     if (argc >= 5 && !strcmp(argv[1], "registry")) return registry(argv[2], atoi(argv[3]), argv[4]);
+    if (argc >= 2 && !strcmp(argv[1], "dataset")) return dataset();
+    if (argc >= 2 && !strcmp(argv[1], "infer")) return infer();
     fprintf(stderr, "usage: %s numcheck | train <model.tkm> <batch> <steps> <lr> <weights.bin> | "
-                    "source <mode> <model.tkm> <batch> | registry <model.tkm> <batch> <dir>\n", argv[0]);
+                    "source <mode> <model.tkm> <batch> | registry <model.tkm> <batch> <dir> | dataset | infer\n",
+            argv[0]);
     return 2;
 }

@@ -36,6 +36,7 @@ def test_bench_line_contract():
     assert ro["bound"] == "mfma" and ro["unit"] == "TFLOP/s" and ro["peak"] == 2516.6
     assert ro["frac"] == pytest.approx(ro["achieved"] / ro["peak"], rel=2e-3)
     assert ro["kernel"] in d["kernels"] and isinstance(ro["traffic"], (int, float))
+    assert "profiles/attn_cfg3_traffic.md" in ro["traffic_source"]
     assert d["kernel_path"] == {"attn_fwd": ["fwd_asm"], "bwd_dq": ["dq_asm"], "bwd_dkdv": ["dkdv_asm"]}
     cb = d["cpu_baseline"]
     assert cb["kind"] == "port" and cb["unit"] == "TFLOP/s" and cb["value"] > 0

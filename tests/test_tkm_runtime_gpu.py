@@ -293,6 +293,37 @@ def test_step_matches_chained_oracle(gpu, name, dtype):
 
 
 
+@pytest.mark.parametrize("name", ["llama_small", "exotic_llama"] + _RANDOM)
+def test_planned_gradient_clears_match_full_clears(gpu, name):
+    """The runtime clears only the gradient slots whose first writer accumulates, and the
+    first writers of all other slots overwrite them (plan_grad_writes); the gradient arena is
+    zeroed once at ignite, so a missed clear would only show from the second step on.  Three
+    steps on different batches at lr 0.05 from the same initial weights: losses, every weight
+    and the input gradient equal, bit for bit, a runtime that clears the whole arena every step
+    as the reference does."""
+    from tokamak_amd import runtime as R
+    log(f"[case] {name}: planned gradient clears vs the whole arena, three steps")
+    a = R.Runtime(graph(name), token_labels=True, init_seed=11)
+    b = R.Runtime(graph(name), token_labels=True, init_seed=11, clear_all_grads=True)
+    js = gjson(name)
+    import tkm_graph_oracle as T
+    nodes = T._fix_shapes([dict(n) for n in js["nodes"]])
+    V = nodes[next(n for n in nodes if n["op"] == T.OP_CE)["in0"]]["C"]
+    rows = a.input_elements // nodes[0]["C"]
+    rng = np.random.default_rng(12)
+    for k in range(3):
+        x = rng.standard_normal(a.input_elements).astype(np.float32)
+        y = rng.integers(0, V, rows).astype(np.int32)
+        la, lb = a.step(x, y, 0.05), b.step(x, y, 0.05)
+        ga = _read_device(a.node_device(0, grad=True), a.input_elements * 2)
+        gb = _read_device(b.node_device(0, grad=True), b.input_elements * 2)
+        log(f"    step {k}: loss {la:.6f} / {lb:.6f}")
+        assert np.isfinite(la) and la == lb and ga == gb
+    assert a.save_weights() == b.save_weights()
+    a.close()
+    b.close()
+
+
 def _epoch_lr(peak, min_ratio, step, total, warmup):
     """src/tkm_gpu.cu:1793-1800: linear warm-up, then cosine decay to min_ratio of the peak."""
     w = (step + 1) / warmup if (warmup > 0 and step < warmup) else 1.0
@@ -341,6 +372,44 @@ def test_resident_epoch_matches_steps(gpu, schedule):
     L.tkm_dataset_free(ds)
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("schedule", ["constant", "warmup_cosine"])
+def test_streaming_epoch_matches_resident(gpu, schedule):
+    """The streaming dataset path (two pinned staging slots filled on the host while the other
+    slot's batch trains, copied on a stream of their own; the reference's pinned ping-pong
+    staging, src/tkm_gpu.cu:1856-1879, 1938-1953) forced by the runtime option, against the
+    resident path on a runtime with the same initial weights: two epochs in different sample
+    orders, an odd number of batches each (so the slots alternate across the epoch boundary),
+    give the same mean losses and weights bit for bit."""
+    import ctypes
+    from tokamak_amd import runtime as R
+    log(f"[case] fused_check: streaming vs resident epochs, {schedule} rate")
+    L = R.lib()
+    B, C, nb = 4, 8, 7
+    rng = np.random.default_rng(22)
+    N = B * nb + 2
+    images = rng.standard_normal((N, C)).astype(np.float32)
+    labels = rng.integers(0, 4, N).astype(np.uint8)
+    peak, min_ratio, warm = (0.05, 1.0, 0) if schedule == "constant" else (0.05, 0.2, 3)
+    rts = {mode: R.Runtime(graph("fused_check"), init_seed=5, dataset_mode=mode) for mode in (1, 2)}
+    dss = {mode: L.tkm_dataset_create(rts[mode].rt, images.ctypes.data, labels.ctypes.data, N) for mode in (1, 2)}
+    assert dss[1] and dss[2]
+    assert L.tkm_dataset_is_resident(dss[1]) == 1 and L.tkm_dataset_is_resident(dss[2]) == 0
+    for epoch in range(2):
+        order = rng.permutation(N).astype(np.uint32)
+        avg = {}
+        for mode in (1, 2):
+            v = ctypes.c_float()
+            assert L.tkm_runtime_train_epoch(rts[mode].rt, dss[mode], order.ctypes.data, peak, min_ratio,
+                                             epoch * nb, 2 * nb, warm, ctypes.byref(v))
+            avg[mode] = v.value
+        log(f"    epoch {epoch}: mean loss resident {avg[1]:.7f}, streaming {avg[2]:.7f}")
+        assert np.isfinite(avg[1]) and avg[1] == avg[2]
+        assert rts[1].save_weights() == rts[2].save_weights()
+    for mode in (1, 2):
+        L.tkm_dataset_free(dss[mode])
+        rts[mode].close()
 
 
 def test_eval_counts_first_maximal_logit(gpu):

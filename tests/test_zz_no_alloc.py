@@ -51,12 +51,25 @@ def test_noalloc_matches_workspace_backward_twice(gpu):
 
 
 def test_noalloc_rejects_beyond_scratch(gpu):
+    """A problem whose workspace exceeds the static scratch is rejected before anything runs;
+    every tensor is a real allocation of the size the call names, so the call could not touch
+    memory outside them even if the check were gone (the rejection itself is also checked on
+    the CPU, tests/test_abi.py)."""
+    import torch
     from tokamak_amd import attn
     L = attn.lib()
-    B, S, Hq = 8, 65536, 4  # 2M rows x heads: ~25 MB of workspace > 16 MiB
-    assert L.tkm_attn_bwd_workspace_bytes(B, S, Hq) > 16 << 20
+    L.tkm_attn_bwd_noalloc.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int] * 5 + \
+        [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     L.tkm_attn_bwd_noalloc.restype = ctypes.c_int
-    p = ctypes.c_void_p(0x10000)
-    rc = L.tkm_attn_bwd_noalloc(p, p, p, p, p, None, B, S, Hq, Hq, 128, ctypes.c_float(0.088),
-                                1, 0, None)
+    B, S, Hq, Hkv, D = 1, 1 << 20, 4, 1, 64  # 4M (row, head) pairs: 48 MiB of workspace > 16 MiB
+    assert L.tkm_attn_bwd_workspace_bytes(B, S, Hq) > 16 << 20
+    qkv = torch.zeros((B, S, (Hq + 2 * Hkv) * D), dtype=torch.float16, device=gpu)
+    o = torch.zeros((B, S, Hq * D), dtype=torch.float16, device=gpu)
+    dout = torch.zeros_like(o)
+    lse = torch.zeros((B, Hq, S), dtype=torch.float32, device=gpu)
+    dqkv = torch.full_like(qkv, 1.0)
+    rc = _noalloc(L, qkv, o, dout, lse, dqkv, None, B, S, Hq, Hkv, D, True, attn.F16,
+                  torch.cuda.current_stream())
+    torch.cuda.synchronize()
     assert rc == -4 and b"scratch" in L.tkm_attn_last_error()
+    assert bool((dqkv == 1.0).all())   # nothing ran

@@ -134,6 +134,9 @@ struct TkmRuntime {
     float *h_pin_lr, *h_pin_loss;
     hipGraph_t step_graph[2];        /* [0] clears the loss, [1] accumulates it (epochs) */
     hipGraphExec_t step_exec[2];
+    float *d_out_f32;                /* tkm_runtime_forward's fp32 copy of the output node */
+    float *h_stage_in;               /* pinned batch staging of the callback loops */
+    uint8_t *h_stage_lbl;
     float last_lr;
     int kernel_count, counting;
     int failed;                      /* a launch failed while recording */
@@ -141,20 +144,23 @@ struct TkmRuntime {
 
 struct TkmDataset {
     TkmRuntime *rt;
-    const float *h_images;
+    const float *h_images;           /* caller-owned, NHWC fp32, and one uint8 label per sample */
     const uint8_t *h_labels;
     size_t num_samples, sample_elems;
     int resident;
+    uint32_t *h_order;               /* pinned: the epoch's sample order */
+    /* resident: the samples in the runtime's 16-bit type, the labels, the order */
     void *d_images;
     uint8_t *d_labels;
     uint32_t *d_order;
-    uint32_t *d_counters;            /* batch index, global step */
-    float *d_sched;                  /* peak_lr, min_lr_ratio, total_steps, warmup_steps */
-    float *h_pin_in;
-    uint8_t *h_pin_lbl;
-    uint32_t *h_pin_order;
-    hipGraph_t graph;
-    hipGraphExec_t exec;
+    /* streaming: two staging slots (pinned host rows and labels, their device copies), filled
+     * on the host while the other slot's batch runs; `copy` moves a slot to the device while
+     * `rt->stream` trains on the previous one */
+    float *h_in[2], *d_in[2];
+    uint8_t *h_lbl[2], *d_lbl[2];
+    hipStream_t copy;
+    hipEvent_t copied[2], consumed[2];
+    int used[2];
 };
 
 /* ---- errors ------------------------------------------------------------------------------ */
@@ -545,6 +551,11 @@ static int plan_grad_writes(TkmRuntime *rt) {
         }
     }
     rt->n_clear = nc;
+    if (rt->clear && rt->opts.clear_all_grads && g->total_arena_bytes >= 4) {
+        rt->clear[0][0] = 0;
+        rt->clear[0][1] = g->total_arena_bytes & ~(size_t)3;
+        rt->n_clear = 1;
+    }
     free(written);
     free(clear);
     return rt->clear != NULL;
@@ -663,6 +674,10 @@ TkmRuntime *tkm_runtime_ignite_ex(const TkmGraph *g, const char *src, const tkm_
     else tkm_runtime_opts_init(&opts);
     if (opts.dtype != TKM_ATTN_F16 && opts.dtype != TKM_ATTN_BF16) {
         fprintf(stderr, "[TKM HIP] unknown dtype %d\n", opts.dtype);
+        return NULL;
+    }
+    if (opts.dataset_mode < 0 || opts.dataset_mode > 2) {
+        fprintf(stderr, "[TKM HIP] unknown dataset_mode %d\n", opts.dataset_mode);
         return NULL;
     }
     if (!check_graph(g)) return NULL;
@@ -1107,34 +1122,28 @@ static int output_node(const TkmGraph *g) {
     return -1;
 }
 
+/* One runtime batch of inference (docs/C_API.md 6.2): 0 unless the graph ends in a tensor and
+ * h_output holds all of it.  The output node's 16-bit rows are widened on the device into a
+ * buffer the runtime keeps for later calls, then copied out. */
 size_t tkm_runtime_forward(TkmRuntime *rt, const float *h_input, float *h_output, size_t output_capacity) {
-    if (!rt || !h_input || !h_output) {
-        fprintf(stderr, "[TKM API Error] tkm_runtime_forward requires a runtime and non-null input/output buffers.\n");
+    const char *why = NULL;
+    const size_t n = rt ? tkm_runtime_output_elements(rt) : 0;
+    if (!rt || !h_input || !h_output) why = "a runtime, an input and an output buffer are required";
+    else if (n == 0) why = "the graph ends in a loss, which has no inference output";
+    else if (output_capacity < n) why = "the output buffer is smaller than tkm_runtime_output_elements()";
+    if (why) {
+        fprintf(stderr, "[TKM HIP] tkm_runtime_forward: %s\n", why);
         return 0;
     }
-    const TkmGraph *g = &rt->graph;
-    const int out = output_node(g);
-    if (out < 0 || is_loss(g->nodes[out].op)) {
-        fprintf(stderr, "[TKM API Error] tkm_runtime_forward requires a graph ending in a tensor output, not a loss sink.\n");
-        return 0;
-    }
-    const size_t n = rows_of(g, &g->nodes[out]) * (size_t)g->nodes[out].C;
-    if (output_capacity < n) {
-        fprintf(stderr, "[TKM API Error] Inference output buffer needs %zu floats; capacity is %zu.\n", n, output_capacity);
-        return 0;
-    }
-    float *d_out = NULL;
+    if (!rt->d_out_f32 && !HIP_OK(hipMalloc((void **)&rt->d_out_f32, n * sizeof(float)))) return 0;
     if (tkm_runtime_upload(rt, h_input, NULL, 0)) return 0;
     rt->failed = 0;
-    forward_pass(rt, 1, g->batch_size);
-    if (rt->failed || !HIP_OK(hipMalloc((void **)&d_out, n * sizeof(float)))) return 0;
-    size_t got = 0;
-    if (!tkm_rt_16_to_f32(act(rt, out), d_out, n, rt->dt, rt->stream) &&
-        HIP_OK(hipMemcpyAsync(h_output, d_out, n * sizeof(float), hipMemcpyDeviceToHost, rt->stream)) &&
-        HIP_OK(hipStreamSynchronize(rt->stream)))
-        got = n;
-    hipFree(d_out);
-    return got;
+    forward_pass(rt, 1, rt->graph.batch_size);
+    if (rt->failed || tkm_rt_16_to_f32(act(rt, output_node(&rt->graph)), rt->d_out_f32, n, rt->dt, rt->stream) ||
+        !HIP_OK(hipMemcpyAsync(h_output, rt->d_out_f32, n * sizeof(float), hipMemcpyDeviceToHost, rt->stream)) ||
+        !HIP_OK(hipStreamSynchronize(rt->stream)))
+        return 0;
+    return n;
 }
 
 float tkm_eval_current_loss(TkmRuntime *rt) {
@@ -1275,156 +1284,154 @@ int tkm_load_weights_buffer(TkmRuntime *rt, const void *buffer, size_t size) {
     return HIP_OK(hipStreamSynchronize(rt->stream));
 }
 
+/* ---- host files ---------------------------------------------------------------------------- */
+
+/* The whole file at `path` in a malloc'd buffer with one spare byte past its end (set to 0), its
+ * size in *size; NULL if it cannot be read or is empty (the reason goes to stderr). */
+static char *file_slurp(const char *path, size_t *size) {
+    char *data = NULL;
+    long len = -1;
+    FILE *f = fopen(path, "rb");
+    if (f && fseek(f, 0, SEEK_END) == 0) len = ftell(f);
+    if (f && len > 0 && fseek(f, 0, SEEK_SET) == 0 && (data = (char *)malloc((size_t)len + 1)) != NULL &&
+        fread(data, 1, (size_t)len, f) == (size_t)len) {
+        data[len] = '\0';
+        *size = (size_t)len;
+    } else {
+        fprintf(stderr, "[TKM HIP] cannot read '%s'%s\n", path, f ? "" : " (open failed)");
+        free(data);
+        data = NULL;
+    }
+    if (f) fclose(f);
+    return data;
+}
+
+/* Writes n bytes to `path` (created or truncated); 1 on success. */
+static int file_write(const char *path, const void *data, size_t n) {
+    FILE *f = fopen(path, "wb");
+    const int ok = f && fwrite(data, 1, n, f) == n;
+    if (f && fclose(f) != 0) return 0;
+    if (!ok) fprintf(stderr, "[TKM HIP] cannot write '%s'\n", path);
+    return ok;
+}
+
+/* Checkpoint files hold exactly the bytes of tkm_save_weights_buffer (docs/C_API.md 6.4). */
 int tkm_save_weights(TkmRuntime *rt, const char *bin_path) {
-    if (!rt || !bin_path) return 0;
-    const size_t n = tkm_runtime_weight_bytes(rt);
-    uint8_t *buf = (uint8_t *)malloc(n);
-    if (!buf || !tkm_save_weights_buffer(rt, buf, n, NULL)) {
-        free(buf);
-        return 0;
-    }
-    FILE *f = fopen(bin_path, "wb");
-    if (!f) {
-        perror(bin_path);
-        free(buf);
-        return 0;
-    }
-    const int ok = fwrite(buf, 1, n, f) == n;
-    fclose(f);
+    const size_t n = rt && bin_path ? tkm_runtime_weight_bytes(rt) : 0;
+    void *buf = n ? malloc(n) : NULL;
+    const int ok = buf && tkm_save_weights_buffer(rt, buf, n, NULL) && file_write(bin_path, buf, n);
     free(buf);
     if (ok && rt->opts.verbose)
-        printf("  [TKM I/O] Saved %d learnable tensors (%lld params) to '%s'\n", rt->n_tensors, rt->total_elems,
-               bin_path);
+        printf("  [TKM HIP] checkpoint '%s': %zu bytes, %d tensors\n", bin_path, n, rt->n_tensors);
     return ok;
 }
 
 int tkm_load_weights(TkmRuntime *rt, const char *bin_path) {
-    if (!rt || !bin_path) return 0;
-    FILE *f = fopen(bin_path, "rb");
-    if (!f) {
-        perror(bin_path);
-        return 0;
-    }
-    if (fseek(f, 0, SEEK_END) != 0) { fclose(f); return 0; }
-    const long sz = ftell(f);
-    if (sz <= 0 || fseek(f, 0, SEEK_SET) != 0) { fclose(f); return 0; }
-    uint8_t *buf = (uint8_t *)malloc((size_t)sz);
-    const int rd = buf && fread(buf, 1, (size_t)sz, f) == (size_t)sz;
-    fclose(f);
-    const int ok = rd && tkm_load_weights_buffer(rt, buf, (size_t)sz);
+    size_t n = 0;
+    char *buf = rt && bin_path ? file_slurp(bin_path, &n) : NULL;
+    const int ok = buf && tkm_load_weights_buffer(rt, buf, n);
     free(buf);
     if (ok && rt->opts.verbose)
-        printf("  [TKM I/O] Loaded %d learnable tensors (%lld params) from '%s'\n", rt->n_tensors, rt->total_elems,
-               bin_path);
+        printf("  [TKM HIP] checkpoint '%s' loaded: %d tensors\n", bin_path, rt->n_tensors);
     return ok;
 }
 
-/* ---- loading from .tkm text (needs the reference's front end linked in) ---------------------- */
+/* ---- loading from .tkm text ---------------------------------------------------------------
+ * The front end (parsing, fusion, arena plan) is the reference's own code, which the
+ * application links in; this library only generates, compiles and runs what it produces. */
+
+/* A training runtime from NUL-terminated .tkm text, which it takes over and frees. */
+static TkmRuntime *runtime_from_text(char *text, int batch_size) {
+    TkmRuntime *rt = NULL;
+    TkmGraph *g = NULL;
+    char *src = NULL;
+    if (!tkm_parse_dsl || !tkm_optimize_and_bind || !tkm_plan_memory)
+        fprintf(stderr, "[TKM HIP] tkm_load_*: link the .tkm front end (tkm_core.c, tkm_registry.c) to load text\n");
+    else if ((g = (TkmGraph *)calloc(1, sizeof *g)) != NULL) {
+        tkm_parse_dsl(g, text, batch_size);
+        tkm_optimize_and_bind(g);
+        tkm_plan_memory(g);
+        if ((src = tkm_codegen_cuda_string(g)) != NULL) rt = tkm_runtime_ignite(g, src);
+    }
+    free(src);
+    free(g);
+    free(text);
+    return rt;
+}
 
 TkmRuntime *tkm_load_buffer(const char *dsl_data, size_t dsl_size, int batch_size) {
-    if (!dsl_data || dsl_size == 0 || batch_size <= 0 || dsl_size > SIZE_MAX - 1) return NULL;
-    if (!tkm_parse_dsl || !tkm_optimize_and_bind || !tkm_plan_memory) {
-        fprintf(stderr, "[TKM HIP] tkm_load_*: the .tkm front end (tkm_core.c, tkm_registry.c) is not linked in\n");
-        return NULL;
+    char *text = NULL;
+    if (dsl_data && dsl_size > 0 && dsl_size < SIZE_MAX && batch_size > 0 && (text = (char *)malloc(dsl_size + 1))) {
+        memcpy(text, dsl_data, dsl_size);   /* the caller may free its bytes on return */
+        text[dsl_size] = '\0';
+        return runtime_from_text(text, batch_size);
     }
-    TkmGraph *g = (TkmGraph *)calloc(1, sizeof(TkmGraph));
-    char *text = (char *)malloc(dsl_size + 1);
-    if (!g || !text) {
-        free(g);
-        free(text);
-        return NULL;
-    }
-    memcpy(text, dsl_data, dsl_size);
-    text[dsl_size] = '\0';
-    tkm_parse_dsl(g, text, batch_size);
-    tkm_optimize_and_bind(g);
-    tkm_plan_memory(g);
-    char *src = tkm_codegen_cuda_string(g);
-    TkmRuntime *rt = src ? tkm_runtime_ignite(g, src) : NULL;
-    free(src);
-    free(text);
-    free(g);
-    return rt;
+    return NULL;
 }
 
 TkmRuntime *tkm_load_string(const char *dsl_text, int batch_size) {
-    if (!dsl_text || batch_size <= 0) return NULL;
-    return tkm_load_buffer(dsl_text, strlen(dsl_text), batch_size);
+    return dsl_text ? tkm_load_buffer(dsl_text, strlen(dsl_text), batch_size) : NULL;
 }
 
 TkmRuntime *tkm_load_file(const char *tkm_path, int batch_size) {
-    if (!tkm_path || batch_size <= 0) return NULL;
-    FILE *f = fopen(tkm_path, "rb");
-    if (!f) {
-        perror(tkm_path);
-        return NULL;
-    }
-    if (fseek(f, 0, SEEK_END) != 0) { fclose(f); return NULL; }
-    const long sz = ftell(f);
-    if (sz <= 0 || fseek(f, 0, SEEK_SET) != 0) { fclose(f); return NULL; }
-    char *buf = (char *)malloc((size_t)sz);
-    const int rd = buf && fread(buf, 1, (size_t)sz, f) == (size_t)sz;
-    fclose(f);
-    TkmRuntime *rt = rd ? tkm_load_buffer(buf, (size_t)sz, batch_size) : NULL;
-    free(buf);
-    return rt;
+    size_t n = 0;
+    char *text = tkm_path && batch_size > 0 ? file_slurp(tkm_path, &n) : NULL;
+    return text ? runtime_from_text(text, batch_size) : NULL;
 }
 
-/* ---- datasets and epochs (src/tkm_gpu.cu:1767-1997) ------------------------------------------- */
+/* ---- batches from a caller's loader (docs/C_API.md 6.5) -------------------------------------
+ * One loop serves training and evaluation: it asks the loader for a batch into the runtime's
+ * pinned staging rows, checks the count against the mode's rule (training: exactly B;
+ * evaluation: 1..B), and hands the batch to the mode's step. */
+
+typedef struct {
+    int train;
+    float lr;
+    double total;        /* training: sum of the batch losses; evaluation: correct samples */
+    size_t batches, samples;
+} batch_loop;
+
+static int loop_batches(TkmRuntime *rt, TkmDatasetNext next, void *user, size_t max_batches, batch_loop *L) {
+    const size_t B = (size_t)rt->graph.batch_size;
+    if ((!rt->h_stage_in && !HIP_OK(hipHostMalloc((void **)&rt->h_stage_in, rt->in_elems * sizeof(float),
+                                                  hipHostMallocDefault))) ||
+        (!rt->h_stage_lbl && !HIP_OK(hipHostMalloc((void **)&rt->h_stage_lbl, B, hipHostMallocDefault))))
+        return 0;
+    while (max_batches == 0 || L->batches < max_batches) {
+        size_t got = 0;
+        const int more = next(user, rt->h_stage_in, rt->h_stage_lbl, B, &got);
+        if (more == 0) break;                                    /* end of the dataset */
+        if (more < 0 || got == 0 || got > B || (L->train && got != B)) return 0;
+        if (L->train) {
+            const float loss = tkm_runtime_step(rt, rt->h_stage_in, rt->h_stage_lbl, L->lr);
+            if (!isfinite(loss)) return 0;
+            L->total += loss;
+        } else {
+            L->total += tkm_runtime_eval(rt, rt->h_stage_in, rt->h_stage_lbl, (int)got);
+            if (rt->failed) return 0;
+        }
+        L->batches++;
+        L->samples += got;
+    }
+    return L->batches > 0;
+}
 
 int tkm_runtime_train_dataset(TkmRuntime *rt, TkmDatasetNext next_batch, void *user, size_t max_batches, float lr,
                               float *out_average_loss) {
-    if (out_average_loss) *out_average_loss = 0.0f;
-    if (!rt || !next_batch || rt->opts.token_labels) return 0;
-    const size_t B = (size_t)rt->graph.batch_size;
-    float *in = (float *)malloc(rt->in_elems * sizeof(float));
-    uint8_t *lbl = (uint8_t *)malloc(B);
-    if (!in || !lbl) { free(in); free(lbl); return 0; }
-    size_t batches = 0;
-    double sum = 0.0;
-    int ok = 1;
-    while (max_batches == 0 || batches < max_batches) {
-        size_t count = 0;
-        const int st = next_batch(user, in, lbl, B, &count);
-        if (st == 0) break;
-        if (st < 0 || count != B) { ok = 0; break; }
-        const float l = tkm_runtime_step(rt, in, lbl, lr);
-        if (!isfinite(l)) { ok = 0; break; }
-        sum += l;
-        ++batches;
-    }
-    if (ok && batches > 0 && out_average_loss) *out_average_loss = (float)(sum / (double)batches);
-    free(in);
-    free(lbl);
-    return ok && batches > 0;
+    batch_loop L = {1, lr, 0.0, 0, 0};
+    const int ok = rt && next_batch && rt->training && !rt->opts.token_labels &&
+                   loop_batches(rt, next_batch, user, max_batches, &L);
+    if (out_average_loss) *out_average_loss = ok ? (float)(L.total / (double)L.batches) : 0.0f;
+    return ok;
 }
 
 int tkm_runtime_eval_dataset(TkmRuntime *rt, TkmDatasetNext next_batch, void *user, size_t max_batches,
                              int *out_correct, size_t *out_samples) {
-    if (out_correct) *out_correct = 0;
-    if (out_samples) *out_samples = 0;
-    if (!rt || !next_batch || rt->opts.token_labels) return 0;
-    const size_t B = (size_t)rt->graph.batch_size;
-    float *in = (float *)malloc(rt->in_elems * sizeof(float));
-    uint8_t *lbl = (uint8_t *)malloc(B);
-    if (!in || !lbl) { free(in); free(lbl); return 0; }
-    size_t batches = 0, samples = 0;
-    long long correct = 0;
-    int ok = 1;
-    while (max_batches == 0 || batches < max_batches) {
-        size_t count = 0;
-        const int st = next_batch(user, in, lbl, B, &count);
-        if (st == 0) break;
-        if (st < 0 || count == 0 || count > B) { ok = 0; break; }
-        correct += tkm_runtime_eval(rt, in, lbl, (int)count);
-        samples += count;
-        ++batches;
-    }
-    if (out_correct) *out_correct = (int)correct;
-    if (out_samples) *out_samples = samples;
-    free(in);
-    free(lbl);
-    return ok && batches > 0;
+    batch_loop L = {0, 0.0f, 0.0, 0, 0};
+    const int ok = rt && next_batch && !rt->opts.token_labels && loop_batches(rt, next_batch, user, max_batches, &L);
+    if (out_correct) *out_correct = (int)L.total;
+    if (out_samples) *out_samples = L.samples;
+    return ok;
 }
 
 /* lr of a step: linear warm-up, then cosine decay to min_lr_ratio (src/tkm_gpu.cu:1793-1800) */
@@ -1435,43 +1442,49 @@ static float epoch_lr(float peak_lr, float min_lr_ratio, size_t step, size_t tot
     return peak_lr * warmup * (min_lr_ratio + (1.0f - min_lr_ratio) * cosine);
 }
 
+/* Resident (the samples converted once to the runtime's 16-bit type in device memory) when
+ * that copy fits in half the free device memory, else streaming (docs/C_API.md 6.2); the
+ * runtime's dataset_mode option can force either. */
 TkmDataset *tkm_dataset_create(TkmRuntime *rt, const float *h_images, const uint8_t *h_labels, size_t num_samples) {
     if (!rt || !rt->training || rt->opts.token_labels || !h_images || !h_labels || num_samples == 0) return NULL;
+    const size_t per = rt->in_elems / (size_t)rt->graph.batch_size;
+    if (num_samples > SIZE_MAX / 4 / per) return NULL;
     TkmDataset *ds = (TkmDataset *)calloc(1, sizeof *ds);
     if (!ds) return NULL;
-    ds->rt = rt;
-    ds->h_images = h_images;
-    ds->h_labels = h_labels;
-    ds->num_samples = num_samples;
-    ds->sample_elems = rt->in_elems / (size_t)rt->graph.batch_size;
-    if (num_samples > SIZE_MAX / ds->sample_elems / 4) {
-        free(ds);
-        return NULL;
-    }
+    *ds = (TkmDataset){.rt = rt, .h_images = h_images, .h_labels = h_labels, .num_samples = num_samples,
+                       .sample_elems = per};
     size_t free_b = 0, total_b = 0;
-    HIP_OK(hipMemGetInfo(&free_b, &total_b));
-    const size_t bytes16 = num_samples * ds->sample_elems * 2 + num_samples;
-    ds->resident = bytes16 <= free_b / 2;
-    if (!HIP_OK(hipHostMalloc((void **)&ds->h_pin_order, num_samples * 4, hipHostMallocDefault))) goto fail;
+    if (!HIP_OK(hipMemGetInfo(&free_b, &total_b))) goto fail;
+    ds->resident = rt->opts.dataset_mode == 1 ||
+                   (rt->opts.dataset_mode == 0 && num_samples * (per * 2 + 1) <= free_b / 2);
+    if (!HIP_OK(hipHostMalloc((void **)&ds->h_order, num_samples * 4, hipHostMallocDefault))) goto fail;
     if (ds->resident) {
-        if (!HIP_OK(hipMalloc(&ds->d_images, num_samples * ds->sample_elems * 2)) ||
-            !HIP_OK(hipMalloc((void **)&ds->d_labels, num_samples)) ||
+        const size_t total = num_samples * per;
+        if (!HIP_OK(hipMalloc(&ds->d_images, total * 2)) || !HIP_OK(hipMalloc((void **)&ds->d_labels, num_samples)) ||
             !HIP_OK(hipMalloc((void **)&ds->d_order, num_samples * 4)))
             goto fail;
-        /* convert in chunks of the runtime's input staging buffer */
-        const size_t chunk = rt->in_elems;
-        for (size_t off = 0, total = num_samples * ds->sample_elems; off < total; off += chunk) {
-            const size_t n = total - off < chunk ? total - off : chunk;
-            if (!HIP_OK(hipMemcpyAsync(rt->d_input_f32, h_images + off, n * 4, hipMemcpyHostToDevice, rt->stream)) ||
+        /* through the runtime's fp32 input rows, one batch's worth at a time (after any work
+         * still queued on them) */
+        if (!HIP_OK(hipStreamSynchronize(rt->stream))) goto fail;
+        for (size_t off = 0; off < total; off += rt->in_elems) {
+            const size_t n = total - off < rt->in_elems ? total - off : rt->in_elems;
+            if (!HIP_OK(hipMemcpy(rt->d_input_f32, h_images + off, n * 4, hipMemcpyHostToDevice)) ||
                 tkm_rt_f32_to_16(rt->d_input_f32, (uint8_t *)ds->d_images + off * 2, n, rt->dt, rt->stream) ||
                 !HIP_OK(hipStreamSynchronize(rt->stream)))
                 goto fail;
         }
         if (!HIP_OK(hipMemcpy(ds->d_labels, h_labels, num_samples, hipMemcpyHostToDevice))) goto fail;
     } else {
-        if (!HIP_OK(hipHostMalloc((void **)&ds->h_pin_in, rt->in_elems * 4, hipHostMallocDefault)) ||
-            !HIP_OK(hipHostMalloc((void **)&ds->h_pin_lbl, (size_t)rt->graph.batch_size, hipHostMallocDefault)))
-            goto fail;
+        const size_t B = (size_t)rt->graph.batch_size;
+        if (!HIP_OK(hipStreamCreateWithFlags(&ds->copy, hipStreamNonBlocking))) goto fail;
+        for (int k = 0; k < 2; ++k)
+            if (!HIP_OK(hipHostMalloc((void **)&ds->h_in[k], rt->in_elems * 4, hipHostMallocDefault)) ||
+                !HIP_OK(hipHostMalloc((void **)&ds->h_lbl[k], B, hipHostMallocDefault)) ||
+                !HIP_OK(hipMalloc((void **)&ds->d_in[k], rt->in_elems * 4)) ||
+                !HIP_OK(hipMalloc((void **)&ds->d_lbl[k], B)) ||
+                !HIP_OK(hipEventCreateWithFlags(&ds->copied[k], hipEventDisableTiming)) ||
+                !HIP_OK(hipEventCreateWithFlags(&ds->consumed[k], hipEventDisableTiming)))
+                goto fail;
     }
     return ds;
 fail:
@@ -1481,18 +1494,54 @@ fail:
 
 void tkm_dataset_free(TkmDataset *ds) {
     if (!ds) return;
-    if (ds->exec) hipGraphExecDestroy(ds->exec);
-    if (ds->graph) hipGraphDestroy(ds->graph);
+    if (ds->copy) hipStreamSynchronize(ds->copy);
+    if (ds->rt) hipStreamSynchronize(ds->rt->stream);
+    for (int k = 0; k < 2; ++k) {
+        if (ds->h_in[k]) hipHostFree(ds->h_in[k]);
+        if (ds->h_lbl[k]) hipHostFree(ds->h_lbl[k]);
+        hipFree(ds->d_in[k]);
+        hipFree(ds->d_lbl[k]);
+        if (ds->copied[k]) hipEventDestroy(ds->copied[k]);
+        if (ds->consumed[k]) hipEventDestroy(ds->consumed[k]);
+    }
+    if (ds->copy) hipStreamDestroy(ds->copy);
     hipFree(ds->d_images);
     hipFree(ds->d_labels);
     hipFree(ds->d_order);
-    if (ds->h_pin_in) hipHostFree(ds->h_pin_in);
-    if (ds->h_pin_lbl) hipHostFree(ds->h_pin_lbl);
-    if (ds->h_pin_order) hipHostFree(ds->h_pin_order);
+    if (ds->h_order) hipHostFree(ds->h_order);
     free(ds);
 }
 
 int tkm_dataset_is_resident(const TkmDataset *ds) { return ds ? ds->resident : 0; }
+
+/* Batch b of a streaming epoch into the runtime's input rows and labels, on rt->stream.  Slot
+ * b & 1 is refilled on the host once the batch that last used it has been converted (its
+ * `consumed` event), copied to the device on the copy stream (which first waits for that same
+ * event, since the device slot is reused too), and converted into the input node on rt->stream
+ * after the copy.  So the host gathers batch b + 1 and the copy engine moves it while
+ * rt->stream trains on batch b. */
+static int stream_batch(TkmDataset *ds, size_t b) {
+    TkmRuntime *rt = ds->rt;
+    const size_t B = (size_t)rt->graph.batch_size, per = ds->sample_elems;
+    const int k = (int)(b & 1);
+    if (ds->used[k] && !HIP_OK(hipEventSynchronize(ds->consumed[k]))) return 0;
+    for (size_t r = 0; r < B; ++r) {
+        const uint32_t src = ds->h_order[b * B + r];
+        memcpy(ds->h_in[k] + r * per, ds->h_images + (size_t)src * per, per * 4);
+        ds->h_lbl[k][r] = ds->h_labels[src];
+    }
+    if ((ds->used[k] && !HIP_OK(hipStreamWaitEvent(ds->copy, ds->consumed[k], 0))) ||
+        !HIP_OK(hipMemcpyAsync(ds->d_in[k], ds->h_in[k], rt->in_elems * 4, hipMemcpyHostToDevice, ds->copy)) ||
+        !HIP_OK(hipMemcpyAsync(ds->d_lbl[k], ds->h_lbl[k], B, hipMemcpyHostToDevice, ds->copy)) ||
+        !HIP_OK(hipEventRecord(ds->copied[k], ds->copy)) ||
+        !HIP_OK(hipStreamWaitEvent(rt->stream, ds->copied[k], 0)) ||
+        tkm_rt_f32_to_16(ds->d_in[k], act(rt, 0), rt->in_elems, rt->dt, rt->stream) ||
+        !HIP_OK(hipMemcpyAsync(rt->d_labels, ds->d_lbl[k], B, hipMemcpyDeviceToDevice, rt->stream)) ||
+        !HIP_OK(hipEventRecord(ds->consumed[k], rt->stream)))
+        return 0;
+    ds->used[k] = 1;
+    return 1;
+}
 
 int tkm_runtime_train_epoch(TkmRuntime *rt, TkmDataset *ds, const uint32_t *h_order, float peak_lr,
                             float min_lr_ratio, size_t global_step_start, size_t total_steps, size_t warmup_steps,
@@ -1503,31 +1552,23 @@ int tkm_runtime_train_epoch(TkmRuntime *rt, TkmDataset *ds, const uint32_t *h_or
         return 0;
     const size_t B = (size_t)rt->graph.batch_size, full = ds->num_samples / B;
     if (full == 0) return 0;
+    /* the previous epoch's last copies must be done before its order is overwritten */
+    if (!HIP_OK(hipStreamSynchronize(rt->stream))) return 0;
     for (size_t i = 0; i < ds->num_samples; ++i) {
-        ds->h_pin_order[i] = h_order ? h_order[i] : (uint32_t)i;
-        if (ds->h_pin_order[i] >= ds->num_samples) return 0;
+        ds->h_order[i] = h_order ? h_order[i] : (uint32_t)i;
+        if (ds->h_order[i] >= ds->num_samples) return 0;
     }
     if (!ensure_step_graph(rt, 1)) return 0;
     if (tkm_rt_fill_u32(rt->d_loss, 4, 0, rt->stream)) return 0;
     if (ds->resident &&
-        !HIP_OK(hipMemcpyAsync(ds->d_order, ds->h_pin_order, ds->num_samples * 4, hipMemcpyHostToDevice, rt->stream)))
+        !HIP_OK(hipMemcpyAsync(ds->d_order, ds->h_order, ds->num_samples * 4, hipMemcpyHostToDevice, rt->stream)))
         return 0;
     for (size_t b = 0; b < full; ++b) {
-        if (ds->resident) {
-            if (tkm_rt_gather(ds->d_images, ds->d_labels, ds->d_order, (long long)(b * B), (int)B, ds->sample_elems,
-                              act(rt, 0), (uint8_t *)rt->d_labels, rt->stream))
-                return 0;
-        } else {
-            if (!HIP_OK(hipStreamSynchronize(rt->stream))) return 0;   /* pinned buffers are reused */
-            for (size_t r = 0; r < B; ++r) {
-                const uint32_t src = ds->h_pin_order[b * B + r];
-                memcpy(ds->h_pin_in + r * ds->sample_elems, ds->h_images + (size_t)src * ds->sample_elems,
-                       ds->sample_elems * 4);
-                ds->h_pin_lbl[r] = ds->h_labels[src];
-            }
-            if (tkm_runtime_upload(rt, ds->h_pin_in, ds->h_pin_lbl, B)) return 0;
-        }
-        if (!set_lr(rt, epoch_lr(peak_lr, min_lr_ratio, global_step_start + b, total_steps, warmup_steps)) ||
+        const int staged = ds->resident ? !tkm_rt_gather(ds->d_images, ds->d_labels, ds->d_order, (long long)(b * B),
+                                                         (int)B, ds->sample_elems, act(rt, 0),
+                                                         (uint8_t *)rt->d_labels, rt->stream)
+                                        : stream_batch(ds, b);
+        if (!staged || !set_lr(rt, epoch_lr(peak_lr, min_lr_ratio, global_step_start + b, total_steps, warmup_steps)) ||
             !HIP_OK(hipGraphLaunch(rt->step_exec[1], rt->stream)))
             return 0;
     }
@@ -1608,6 +1649,9 @@ static void free_runtime(TkmRuntime *rt) {
     hipFree(rt->save_block);
     hipFree(rt->d_sgd);
     free(rt->clear);
+    hipFree(rt->d_out_f32);
+    if (rt->h_stage_in) hipHostFree(rt->h_stage_in);
+    if (rt->h_stage_lbl) hipHostFree(rt->h_stage_lbl);
     if (rt->h_pin_lr) hipHostFree(rt->h_pin_lr);
     if (rt->ev_fork) hipEventDestroy(rt->ev_fork);
     if (rt->ev_join) hipEventDestroy(rt->ev_join);

@@ -29,7 +29,7 @@ _lib = None
 
 class Opts(ctypes.Structure):
     _fields_ = [("dtype", _i), ("training", _i), ("token_labels", _i), ("init_seed", ctypes.c_uint64),
-                ("verbose", _i)]
+                ("verbose", _i), ("dataset_mode", _i), ("clear_all_grads", _i)]
 
 
 def lib() -> ctypes.CDLL:
@@ -133,12 +133,13 @@ class Runtime:
     """A runtime ignited from a graph buffer (tkm_runtime_ignite_ex)."""
 
     def __init__(self, graph, dtype=attn.F16, training=True, token_labels=False, init_seed=0x7417,
-                 verbose=False, src=None):
+                 verbose=False, src=None, dataset_mode=0, clear_all_grads=False):
         L = lib()
         o = Opts()
         L.tkm_runtime_opts_init(ctypes.byref(o))
         o.dtype, o.training, o.token_labels, o.init_seed, o.verbose = (dtype, int(training), int(token_labels),
                                                                          init_seed, int(verbose))
+        o.dataset_mode, o.clear_all_grads = dataset_mode, int(clear_all_grads)
         self.graph = graph
         self.rt = L.tkm_runtime_ignite_ex(graph, None if src is None else src.encode(), ctypes.byref(o))
         if not self.rt:
