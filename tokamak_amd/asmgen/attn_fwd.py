@@ -452,6 +452,43 @@ class Body:
                 reads_issued += 1
             self.s_mfma(i, J, init)
 
+    def prescale_block(self, blk, T):
+        """Q block blk = qb*8 + ks (four words) of the next item: from its AGPRs, times
+        scale*log2(e), rounded to fp16 pairs, into the Q AGPRs.  Temporaries: T .. T+47."""
+        p = self.p
+        for j in range(4):
+            w = blk * 4 + j
+            r, lo = T + w % 16, T + 16 + (w % 16) * 2
+            p.valu(f"v_accvgpr_read_b32 {vr(r)}, {ar(A_QN + w)}", A(A_QN + w), V(r))
+            p.valu(f"v_fma_mix_f32 {vr(lo)}, {vr(r)}, {sr(S_SL2)}, 0 op_sel_hi:[1,0,0]", V(r) + S(S_SL2), V(lo))
+            p.valu(f"v_fma_mix_f32 {vr(lo + 1)}, {vr(r)}, {sr(S_SL2)}, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]",
+                   V(r) + S(S_SL2), V(lo + 1))
+            p.valu(f"v_cvt_pk_f16_f32 {vr(r)}, {vr(lo)}, {vr(lo + 1)}", V(lo, 2), V(r))
+            p.valu(f"v_accvgpr_write_b32 {ar(A_Q + w)}, {vr(r)}", V(r), A(A_Q + w))
+
+    def stage_s_prescaled(self, J, kbase):
+        """S(J) = K Q^T from the K buffer at kbase (accumulating from 0) while the next item's
+        Q is prescaled into the Q AGPRs: each block of Q is prescaled just before the first
+        MFMA that reads it, and one more block after every MFMA, so that the VALU work runs
+        beside the MFMAs; the temporaries are the free score set J^1."""
+        T = V_SET[J ^ 1]
+        order = [qb * 8 + ks for ks in range(8) for qb in range(2)]
+        done = 0
+        reads_issued = 0
+        for i in range(32):
+            ri, qb = i // 2, i % 2
+            need = order.index(qb * 8 + ri % 8)
+            while done <= need:
+                self.prescale_block(order[done], T)
+                done += 1
+            while reads_issued < 16 and reads_issued * 2 - LK <= i:
+                self.k_read(reads_issued, kbase)
+                reads_issued += 1
+            self.s_mfma(i, J, "zero")
+            if done < 16:
+                self.prescale_block(order[done], T)
+                done += 1
+
     def stage_softmax(self, J):
         for n in range(33):
             if n < 32:
@@ -630,10 +667,11 @@ class Body:
         p.branch(f"s_branch .Ldisp{Jn}", skip_xdl=ACC)
 
     # ---------------------------------------------------------------- item start / end
-    def q_loads(self, b, h, q0, dst_acc):
+    def q_loads(self, b, h, q0, dst_acc, untracked=False):
         """Issue the loads of Q rows q0 + 32qb + l32 of (batch b, head h) for this wave: lane
-        (l32, hi) loads bytes hi*16 + 32ks .. +15; into VGPRs 0..63 (tracked) or, dst_acc,
-        into the next-item AGPRs (untracked: the next loop body's vmcnt(0) covers them)."""
+        (l32, hi) loads bytes hi*16 + 32ks .. +15; into VGPRs 0..63 (tracked, or untracked when
+        the caller waits for them itself) or, dst_acc, into the next-item AGPRs (untracked: the
+        next loop body's vmcnt(0) covers them)."""
         p, s = self.p, self.s
         RQ = S_TMP + 16
         T0, COL, LO, HI = S_TMP + 8, S_TMP + 9, S_TMP + 10, S_TMP + 11
@@ -656,15 +694,13 @@ class Body:
                 i = (qb * 8 + ks) * 4
                 dst, regs = (ar(A_QN + i, 4), A(A_QN + i, 4)) if dst_acc else (vr(i, 4), V(i, 4))
                 p.vmem_load(f"buffer_load_dwordx4 {dst}, {vr(QOFF + qb)}, {sr(RQ, 4)}, 0 offen offset:{ks * 32}",
-                            regs, V(QOFF + qb) + S(RQ, 4), untracked=dst_acc)
+                            regs, V(QOFF + qb) + S(RQ, 4), untracked=dst_acc or untracked)
 
-    def q_prescale(self, from_acc):
-        """Q words (VGPRs 0..63, or the next-item AGPRs) -> two f32 (x * sl2) -> fp16 pair
-        -> the Q AGPRs."""
+    def q_prescale(self):
+        """Q words (VGPRs 0..63, as loaded) -> two f32 (x * sl2) -> fp16 pair -> the Q AGPRs
+        (the prologue; later items prescale beside their first scores, stage_s_prescaled)."""
         p = self.p
         for i in range(64):
-            if from_acc:
-                p.valu(f"v_accvgpr_read_b32 {vr(i)}, {ar(A_QN + i)}", A(A_QN + i), V(i))
             t0, t1 = V_CINIT, V_CINIT + 1
             p.valu(f"v_fma_mix_f32 {vr(t0)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t0))
             p.valu(f"v_fma_mix_f32 {vr(t1)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t1))
@@ -702,25 +738,39 @@ class Body:
             p.valu(f"v_mov_b32_e32 {vr(V_LSUM + qb)}, 0", [], V(V_LSUM + qb))
             p.valu(f"v_mov_b32_e32 {vr(V_LMAX + qb)}, 0", [], V(V_LMAX + qb))
 
-    def start_item(self, u, sfx, fixed_m, prefetch=True):
+    def start_item(self, u, sfx, fixed_m, prefetch=True, drain=False, prescale=False):
         """Tile 0 of the current item (stream parity u): S(0) into set u when the wave uses
         it, its mask, and m = its row max (first pass) or S(0) from the start values -m
         (fixed_m: the exact pass after an overflow); one barrier (the first body's requests
-        overwrite K buffer u); the loads of the next item's Q (prefetch); then the first
-        body."""
+        overwrite K buffer u; drain: every DMA of this wave done before it, for the prologue,
+        whose K(1) and V(0) may still be in flight); the loads of the next item's Q
+        (prefetch); then the first body.  prescale: the item's Q is still in the next-item
+        AGPRs; it is prescaled into the Q AGPRs beside S(0)'s MFMAs (or alone, when the wave
+        uses no tile of the item), and the O accumulators are reset first."""
         p, s = self.p, self.s
         p.comment(f"start {u}")
+        if prescale:
+            self.reset_acc()
         s(f"s_cmp_eq_u32 {sr(S_ACTEND)}, 0", S(S_ACTEND), [("scc", 0)])
         p.branch(f"s_cbranch_scc1 .Lsn_{sfx}", [("scc", 0)], skip_xdl=ACC)
-        self.stage_s(u, LDS_K[u], "cinit" if fixed_m else "zero")
+        if prescale:
+            self.stage_s_prescaled(u, LDS_K[u])
+        else:
+            self.stage_s(u, LDS_K[u], "cinit" if fixed_m else "zero")
         s(f"s_cmp_eq_u32 {sr(S_MASKB)}, 0", S(S_MASKB), [("scc", 0)])
         p.branch(f"s_cbranch_scc0 .Lsm_{sfx}", [("scc", 0)], skip_xdl=ACC)
         self.stage_mask(u, S_IT)
         p.label(f".Lsm_{sfx}")
         if not fixed_m:
             self.row_max_set_m(u)
+        if prescale:
+            p.branch(f"s_branch .Lsj_{sfx}", skip_xdl=ACC)
         p.label(f".Lsn_{sfx}")
-        p.waitcnt(lgkm=0)
+        if prescale:
+            for blk in range(16):
+                self.prescale_block(blk, V_SET[u ^ 1])
+            p.label(f".Lsj_{sfx}")
+        p.waitcnt(vm=0 if drain else None, lgkm=0)
         p.barrier()
         if prefetch:
             self.prefetch_next_q(sfx)
@@ -885,18 +935,22 @@ def build(check_ldb: int = 12288) -> str:
     p.valu(f"v_lshlrev_b32_e32 {vr(V_HI4)}, 2, {vr(HI)}", V(HI), V(V_HI4))
     p.valu(f"v_mov_b32_e32 {vr(V_NINF)}, 0xff800000", [], V(V_NINF))
     # ------------------------------------------------------------------ first item
+    # The wave's Q rows are requested first and K(0) next, so that the prescale and S(0) wait
+    # only for those while K(1) and V(0) are still arriving (every workgroup requests its first
+    # rows at once, and HBM serves them roughly in order).
     for r in (S_KA, S_KD, S_PASS):
         sal(f"s_mov_b32 {sr(r)}, 0", [], S(r))
-    b.decode_d("p0")
-    b.stream_start(0, "p")
     b.item_index(S_KA, S_TMP + 15, S_TMP + 12)
     b.decode_a(S_TMP + 15, "p")
-    b.q_loads(S_BA, S_HA, S_Q0, False)
-    b.q_prescale(False)
+    b.q_loads(S_BA, S_HA, S_Q0, False, untracked=True)      # 16 loads
+    b.decode_d("p0")
+    b.stream_start(0, "p")                                   # K(0), K(1), V(0): 4 DMAs each
     b.reset_acc()
-    p.waitcnt(vm=0)
+    p.waitcnt(vm=12)                                         # the Q rows
+    b.q_prescale()
+    p.waitcnt(vm=8)                                          # this wave's part of K(0)
     p.barrier()
-    b.start_item(0, "p", False)
+    b.start_item(0, "p", False, drain=True)
     for u in range(2):
         _dispatch(b, u)
     for u in range(2):
@@ -965,9 +1019,7 @@ def _boundary(b: Body, u: int):
     p.comment("next q")
     b.decode_a(I, f"b{u}")
     s(f"s_mov_b32 {sr(S_PASS)}, 0", [], S(S_PASS))
-    b.q_prescale(True)
-    b.reset_acc()
-    b.start_item(u, f"b{u}", False)
+    b.start_item(u, f"b{u}", False, prescale=True)
 
 
 def _redo(b: Body, u: int):
