@@ -109,3 +109,42 @@ def gradient_term_rms(qkv, o_stored, dout, lse, B, S, Hq, Hkv, D, causal=True, k
             rk[b, :, kh] += scale ** 2 * (dS ** 2).T @ (q ** 2)
             rq[b, :, h] = scale ** 2 * (dS ** 2) @ (k ** 2)
     return np.sqrt(rq), np.sqrt(rk), np.sqrt(rv)
+
+
+def fp16_forward_repeats(qkv, B, S, Hq, Hkv, D, causal):
+    """The fp16 D = 128 assembly forward's overflow test (tokamak_amd/asmgen/attn_fwd.py:
+    overflow_vote), evaluated on the CPU for every item (b, h, block of
+    256 query rows): per row, m = max over the item's first tile (keys 0..63, visible ones) of
+    s' = (q . k) * sl2 (fp32, sl2 = scale * log2 e); for every tile, each lane sums exp2(s' - m) over its 32 keys
+    of the tile (the keys whose index mod 8 is in the lane's half); the item repeats if any
+    such sum reaches 65504.  Returns (number of items, items that repeat, largest
+    max_j(s') - m over all rows in log2 units; the repeat needs about 16)."""
+    sl2 = np.float32(np.float32(1.0) / np.sqrt(np.float32(D)) * np.float32(1.4426950408889634))
+    x = qkv.reshape(B, S, Hq + 2 * Hkv, D)
+    g = Hq // Hkv
+    n_items = n_redo = 0
+    growth = -np.inf
+    i = np.arange(S)[:, None]
+    j = np.arange(S)[None, :]
+    vis = (j <= i) if causal else np.ones((S, S), bool)
+    half = (np.arange(S) % 8) // 4          # the lane half that holds key j
+    tile = np.arange(S) // 64
+    nt = (S + 63) // 64
+    for b in range(B):
+        for h in range(Hq):
+            q = x[b, :, h].astype(np.float32)
+            k = x[b, :, Hq + h // g].astype(np.float32)
+            s = (q @ k.T) * sl2                                   # fp32, log2 units
+            s = np.where(vis, s, -np.inf)
+            first = np.where(tile[None, :] == 0, s, -np.inf).max(axis=1)
+            m = np.where(np.isfinite(first), first, 0.0)
+            growth = max(growth, float(np.nanmax(np.where(vis, s - m[:, None], -np.inf))))
+            with np.errstate(over="ignore"):
+                p = np.where(vis, np.exp2(np.minimum(s - m[:, None], 126.0)), 0.0)
+            sums = np.zeros((S, nt, 2))
+            np.add.at(sums, (slice(None), tile, half), p)       # per row, tile, lane half
+            bad_row = (sums >= 65504.0).any(axis=(1, 2))
+            for z in range((S + 255) // 256):
+                n_items += 1
+                n_redo += bool(bad_row[256 * z:256 * z + 256].any())
+    return n_items, n_redo, growth

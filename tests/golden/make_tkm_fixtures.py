@@ -17,7 +17,9 @@ and runs it on each model below, then packs the outputs into:
   tests/golden/tkm_layout.json    sizeof / offsetof of every struct of the reference's tkm.h
 
 Models: BASELINE config 4's decoder (tests/golden/models/cfg4_llama.tkm, batch 8), a small
-two-layer decoder for the chained-oracle parity test (llama_small.tkm, batch 2), the
+two-layer decoder for the chained-oracle parity test (llama_small.tkm, batch 2), a two-layer
+head-dim-128 decoder trained on an induction task by the trained-attention test (induction.tkm,
+batch 4), the
 reference's models/exotic_llama.tkm (batch 2) and models/llama3_style.tkm (batch 1; its
 structure only), and the inputs of the reference's GPU gradient check (src/main.c:202-306):
 one "input: 1x1x32 / test: <op> -> SoftmaxCE" graph per checked op (batch 2) and its fused
@@ -91,6 +93,7 @@ RANDOM_DECODER_SEEDS = (1000, 1005, 1008, 1010, 1015, 1021, 1029, 1037, 2021)
 def models():
     out = [("cfg4", os.path.join(HERE, "models", "cfg4_llama.tkm"), 8, None),
            ("llama_small", os.path.join(HERE, "models", "llama_small.tkm"), 2, None),
+           ("induction", os.path.join(HERE, "models", "induction.tkm"), 4, None),
            ("exotic_llama", os.path.join(REF, "models", "exotic_llama.tkm"), 2, None),
            ("llama3_style", os.path.join(REF, "models", "llama3_style.tkm"), 1, None),
            ("fused_check", None, 4, FUSED_CHECK)]

@@ -109,7 +109,8 @@ def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, overflow=()):
             stored[key] = stored.get(key, 0) + 1
         elif words[0] == "next" and words[1] == "q":
             # the next item's Q, loaded into the next-item AGPRs during this item
-            next_q[(w.wg, w.wave)] = [(o, base) for o, base in w.loads if o[0] == "a"]
+            next_q[(w.wg, w.wave)] = [(o, base) for o, base in w.loads
+                                      if o[0] == "a" and attn_fwd.A_QN <= o[1] < attn_fwd.A_QN + 64]
             w.loads.clear()
         elif words[0] == "start" and (w.wg, w.wave) in next_q:
             b, h, _, _, _ = item_of(w)

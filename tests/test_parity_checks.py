@@ -120,3 +120,25 @@ def test_rounding_bound_catches_a_missing_term():
         dv16 += P16.T @ do[0, :, h]
     err = np.abs(dv16 - dv[0, :, 0])
     assert np.all(err <= bound[0, :, 0]) and err.max() > 5e-3 * 0.2
+
+
+def test_fp16_forward_repeats_flags_growth():
+    """The CPU evaluation of the fp16 forward's overflow test: random N(0,1) rows never repeat
+    an item (their scores stay within a few log2 units of the first tile's maximum); keys whose
+    scores grow along the sequence past the fp16 range do, and the reported growth says by how
+    much."""
+    import oracle
+    from attn_cases import fp16_forward_repeats
+    B, S, Hq, Hkv, D = 1, 512, 2, 1, 128
+    x = oracle.make_inputs(B, S, Hq, Hkv, D, "f16", seed_qkv=1)["qkv"].reshape(B, S, Hq + 2 * Hkv, D)
+    items, redo, growth = fp16_forward_repeats(x, B, S, Hq, Hkv, D, True)
+    assert (items, redo) == (4, 0) and growth < 8
+    u = x[0, :, :Hq].mean(axis=(0, 1))
+    u /= np.linalg.norm(u)
+    for gr, want in ((0.05, 0), (0.4, 4)):
+        y = x.copy()
+        y[0, :, Hq:Hq + Hkv] += gr * np.arange(S)[:, None, None] * u
+        y = y.astype(np.float16).astype(np.float32)
+        items, redo, growth = fp16_forward_repeats(y, B, S, Hq, Hkv, D, True)
+        assert redo == want, (gr, redo, growth)
+        assert (growth > 16) == (want > 0)

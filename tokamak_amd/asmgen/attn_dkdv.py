@@ -12,8 +12,8 @@ Instead of LSE and D it reads the workspace's row values -LSE*log2(e) and -D, st
 padded to a multiple of 32 with zeros), which the pass that computes D writes.
 
 Work decomposition: persistent, one workgroup (4 waves, one per SIMD) per compute unit walks
-items (batch, kv head, block of 128 keys), the key blocks of a head together on one XCD.  A wave owns 32 keys: K (prescaled by
-scale*log2(e)) and V of those keys sit in AGPRs as the B operands of S = Q K^T and
+items (batch, kv head, block of 128 keys), the key blocks of a head together on one XCD.  A wave owns 32 keys: K and V of those keys
+(fp16, as loaded) sit in AGPRs as the B operands of S = Q K^T and
 dP = dO V^T, and the accumulators dV^T, dK^T (C[m = head dim][n = key]) in AGPRs.  The
 workgroup walks the query tiles (32 rows) of every q-head of the group from the last one down
 (causal: to its own key block's first); each tile's Q and dO rows go HBM -> LDS by buffer DMA into one of four buffers
@@ -21,16 +21,20 @@ workgroup walks the query tiles (32 rows) of every q-head of the group from the 
 bytes of row values into its own slot.  The DMA descriptors are fixed for the kernel (whole batch, so rows
 past S read as zero); a tile's position enters as an offset added to the lane offsets.
 Per tile:
-    S  = Q K'^T  + (-LSE*log2e)   8 MFMAs, C[m = query][n = key]: lane = key
-    dP = dO V^T  + (-D)           8 MFMAs (the offsets are the accumulators' start values:
-                                  four consecutive rows per register group, read by each
-                                  half-wave as one 16-byte broadcast LDS read)
-    P = exp2(S), dS = P * dP      masked to 0 where the key is hidden
+    S  = Q K^T                    8 MFMAs, C[m = query][n = key]: lane = key (unscaled
+                                  scores, exact products summed in fp32)
+    dP = dO V^T  + (-D)           8 MFMAs (-D: the accumulators' start values)
+    P = exp2(fma(S, scale*log2e, -LSE*log2e)), dS = P * dP
+                                  masked to 0 where the key is hidden; the scale is applied
+                                  in fp32, as the reference's kernel does (a scale folded into
+                                  K and rounded to fp16 moves a score s by up to |s|*2^-12)
+    (the row values -LSE*log2e and -D: four consecutive rows per register group, read by each
+     half-wave as one 16-byte broadcast LDS read)
     dV^T += dO^T P, dK^T += Q^T dS 16 MFMAs, P and dS packed to fp16 in place as B operands,
                                   dO^T and Q^T read transposed (ds_read_b64_tr_b16)
 Each loop body runs 32 MFMA slots: S/dP of the next tile with the elementwise work of this
-tile between them, one workgroup barrier, then dV/dK of this tile with the next-but-one
-tile's start values and the request of the tile three ahead in between.  The scalar
+tile between them, one workgroup barrier, then dV/dK of this tile with the next tile's
+-LSE*log2e, the next-but-one tile's -D and the request of the tile three ahead in between.  The scalar
 bookkeeping (descriptors of the requested tile, the next body's variant) is spread between
 the MFMAs; a body ends by jumping straight into the next body's common variant.
 """
@@ -106,7 +110,7 @@ assert V_PT + 13 <= 256
 
 # ---- AGPRs
 A_DV, A_DK, A_K, A_V = 0, 64, 128, 160
-A_NK, A_NV = 192, 224     # the next item's K and V rows as loaded (before the K scaling)
+A_NK, A_NV = 192, 224     # the next item's K and V rows as loaded
 ACC = set(A(A_DV, 128))
 
 # variants of a body: (label, S/dP of the next tile, elementwise + dV/dK of this tile, masked)
@@ -253,23 +257,25 @@ class Body:
                            V(dst + 2 * tt, 2), V(V_VOFF + tt * 4 + db))
 
     def cinit_read(self, jb, k):
-        """Start values of accumulator registers 4g .. 4g+3 (g = k % 4) of S (k < 4: -LSE*log2e)
-        or dP (k >= 4: -D): query rows 8g + 4hi .. +3 of the tile in buffer jb, the same for
-        every lane of a half-wave (one 16-byte broadcast read per half)."""
+        """Row values of accumulator registers 4g .. 4g+3 (g = k % 4): k < 4, -LSE*log2e (the
+        exps' offset of S); k >= 4, -D (dP's start values): query rows 8g + 4hi .. +3 of the
+        tile in buffer jb, the same for every lane of a half-wave (one 16-byte broadcast read
+        per half)."""
         g, which = k % 4, k // 4
         base = (V_CS if which == 0 else V_CD) + 4 * g
         self.p.ds_read(f"ds_read_b128 {vr(base, 4)}, {vr(V_LDR)} offset:{jb * LDB + 128 * which + 32 * g}",
                        V(base, 4), V(V_LDR))
 
-    def cinit(self, jb):
-        for k in range(8):
+    def cinit(self, jb, ks=range(8)):
+        for k in ks:
             self.cinit_read(jb, k)
 
     # ---------------------------------------------------------------- MFMAs
     def sdp_mfma(self, i, J):
+        """S (unscaled scores, from 0) or dP (from -D), k-step i // 2."""
         ks, which = i // 2, i % 2
         dst = V_SD[J] + 16 * which
-        c = (V_CS if which == 0 else V_CD) if ks == 0 else dst
+        c = (None if which == 0 else V_CD) if ks == 0 else dst
         b = (A_K if which == 0 else A_V) + ks * 4
         self.p.mfma(MFMA, dst, V_RB + (i % NRB) * 4, b, c, b_acc=True)
 
@@ -284,6 +290,12 @@ class Body:
 
     # ---------------------------------------------------------------- elementwise (set J)
     def ew_exp(self, J, n):
+        """P = exp2(fma(S, scale*log2e, -LSE*log2e)) of registers 2n, 2n+1 of set J: the scale
+        applied in fp32 to the exact scores (the row values of the same tile are in V_CS)."""
+        for r in (2 * n, 2 * n + 1):
+            x = V_SD[J] + r
+            self.p.valu(f"v_fma_f32 {vr(x)}, {vr(x)}, {sr(S_SL2)}, {vr(V_CS + r)}", V(x) + S(S_SL2) + V(V_CS + r),
+                        V(x))
         for r in (2 * n, 2 * n + 1):
             x = V_SD[J] + r
             self.p.trans(f"v_exp_f32_e32 {vr(x)}, {vr(x)}", V(x), V(x))
@@ -522,7 +534,7 @@ class Body:
         self.advance_qt(S_QT1)
 
     def kv_load(self):
-        """K (into VGPRs 0..31, to be scaled) and V (into its AGPRs) of the current item's
+        """K (into VGPRs 0..31) and V (into its AGPRs) of the current item's
         wave keys: lane (l32, hi) loads key kw0 + l32, bytes hi*16 + 32ks .. +15."""
         p, s = self.p, self.s
         RK, RV = S_TMP + 6, S_TMP + 10   # 4-aligned
@@ -591,18 +603,13 @@ class Body:
                             A(base + ks * 4, 4), V(KO) + S(rs, 4), untracked=True)
 
     def kv_take(self):
-        """The prefetched K and V into place: V as loaded, K scaled by scale*log2e to fp16."""
+        """The prefetched K and V into place, as loaded."""
         p = self.p
         p.waitcnt(vm=0)
         for i in range(32):
             p.valu(f"v_accvgpr_mov_b32 {ar(A_V + i)}, {ar(A_NV + i)}", A(A_NV + i), A(A_V + i))
-        t0, t1 = V_T + 1, V_T + 2
-        for i in range(32):   # K * scale*log2e, rounded to fp16
-            p.valu(f"v_accvgpr_read_b32 {vr(i)}, {ar(A_NK + i)}", A(A_NK + i), V(i))
-            p.valu(f"v_fma_mix_f32 {vr(t0)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t0))
-            p.valu(f"v_fma_mix_f32 {vr(t1)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t1))
-            p.valu(f"v_cvt_pk_f16_f32 {vr(i)}, {vr(t0)}, {vr(t1)}", V(t0, 2), V(i))
-            p.valu(f"v_accvgpr_write_b32 {ar(A_K + i)}, {vr(i)}", V(i), A(A_K + i))
+        for i in range(32):
+            p.valu(f"v_accvgpr_mov_b32 {ar(A_K + i)}, {ar(A_NK + i)}", A(A_NK + i), A(A_K + i))
 
     def zero_acc(self):
         p = self.p
@@ -611,14 +618,10 @@ class Body:
         for i in range(8):   # dV, dK := 0 with eight MFMAs of zero operands
             p.mfma(MFMA, A_DV + 16 * i, V_TB, V_TB, None, dst_acc=True)
 
-    def scale_k(self):
-        p = self.p
-        t0, t1 = V_T + 1, V_T + 2
-        for i in range(32):   # K * scale*log2e, rounded to fp16
-            p.valu(f"v_fma_mix_f32 {vr(t0)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t0))
-            p.valu(f"v_fma_mix_f32 {vr(t1)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t1))
-            p.valu(f"v_cvt_pk_f16_f32 {vr(i)}, {vr(t0)}, {vr(t1)}", V(t0, 2), V(i))
-            p.valu(f"v_accvgpr_write_b32 {ar(A_K + i)}, {vr(i)}", V(i), A(A_K + i))
+    def take_k(self):
+        """K as loaded (VGPRs 0..31) into its AGPRs."""
+        for i in range(32):
+            self.p.valu(f"v_accvgpr_write_b32 {ar(A_K + i)}, {vr(i)}", V(i), A(A_K + i))
 
     def epilogue(self):
         """dK^T * scale and dV^T of the current item into dqkv.  A lane holds key kw0 + l32,
@@ -701,7 +704,7 @@ class Body:
             self.sdp_mfma(i, u % 2)
         p.label(f".Lss_{sfx}")
         self.code()
-        self.cinit((u + 1) % 4)
+        self.cinit((u + 1) % 4, range(4, 8))   # -D of tile it+1 (its exps' row values come in body it)
         for i in range(LK):
             self.row_read(i, (u + 1) % 4)
         p.branch(f"s_branch .Ldisp{u}", keep_lgkm=True, skip_xdl=ACC)
@@ -762,8 +765,8 @@ class Body:
                 while tissued < 16 and 16 + tissued - LV <= s_:
                     self.tr_read(tissued, jb0)
                     tissued += 1
-            if 16 <= s_ < 24:
-                self.cinit_read(jb2, s_ - 16)
+            if 16 <= s_ < 24:   # -LSE*log2e of tile it+1 (its exps, next body), -D of tile it+2
+                self.cinit_read(jb1 if s_ < 20 else jb2, s_ - 16)
             p.ins.extend(h2[s_ - 16])
             if s_ in dma_at:
                 which, i = self.DMA_ORDER[dma_at[s_]]
@@ -869,7 +872,7 @@ def build(check_ldb: int = 12288, check_ldo: int = 4096) -> str:
     tr_read_offsets(L, V_VOFF, (LANE, L32, HI), (TA, TB, TC, V_PT + 9, V_PT + 10, V_PT + 11, V_PT + 12))
     _check_lanes(L, check_ldb, check_ldo)
     b.zero_acc()
-    b.scale_k()
+    b.take_k()
     p.waitcnt(vm=0)
     p.barrier()
     b.start_item(0, "p")

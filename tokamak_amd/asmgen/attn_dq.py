@@ -12,14 +12,15 @@ kernel reads; otherwise it reads D from delta.
 Work decomposition: persistent, one workgroup (4 waves, one per SIMD) per compute unit walks
 items (batch, q-head, block of 256 query rows; block fastest) in snake order over rounds of
 NWG items, consecutive items of a round on one XCD (xcd_slot), so that the blocks of a head
-share K/V tiles in its L2 and, for causal, long and short blocks of consecutive rounds pair up.  A wave owns 64 query rows (two blocks of 32): Q (prescaled by
-scale*log2(e)) and dO of its rows sit in AGPRs as the B operands of S^T = K Q^T and
+share K/V tiles in its L2 and, for causal, long and short blocks of consecutive rounds pair up.  A wave owns 64 query rows (two blocks of 32): Q and dO of its rows (fp16,
+as loaded) sit in AGPRs as the B operands of S^T = K Q^T and
 dP^T = V dO^T, dQ^T (C[m = head dim][n = query]) accumulates in AGPRs.  K and V tiles of 32
 keys go HBM -> LDS by buffer DMA into four buffers, requested three tiles ahead; the DMA
 stream runs on across item boundaries.  Per tile and wave (lane = query row):
-    S^T  = K Q'^T + (-LSE*log2e)     16 MFMAs (the offsets are the accumulators' start values,
-    dP^T = V dO^T + (-D)             16 MFMAs  constant for the item)
-    dS^T = exp2(S^T) dP^T            masked to 0 where the key is hidden, packed to fp16 in
+    S^T  = K Q^T                     16 MFMAs (unscaled scores, exact products summed in fp32)
+    dP^T = V dO^T + (-D)             16 MFMAs (-D: the accumulators' start values, per item)
+    dS^T = exp2(fma(S^T, scale*log2e, -LSE*log2e)) dP^T
+                                     masked to 0 where the key is hidden, packed to fp16 in
                                      dP^T's registers as the B operand of
     dQ^T += K^T dS^T                 16 MFMAs, K^T read transposed (ds_read_b64_tr_b16)
 Every K or V operand read from LDS feeds two MFMAs (both 32-row blocks).  A loop body runs 48
@@ -73,7 +74,7 @@ NEXT_FREE_SGPR = 96
 V_SET = (0, 64)         # set J: S^T qb at +16qb, dP^T qb at +32+16qb; after the elementwise
                         # step, the packed dS^T (qb, ks) in dP^T qb's registers 4ks .. 4ks+3
 V_CD = (128, 176)       # -D of the lane's row, 16 copies per qb (dP^T's start values)
-V_CS = 144              # -LSE*log2e of the lane's row, 16 copies per qb (S^T's start values)
+V_CS = 144              # -LSE*log2e of the lane's row, at +16qb (the exps' offset)
 V_RB = 192              # row-read buffers
 V_TB = V_RB + 4 * NRB   # transposed-read buffers
 V_KOFF = V_TB + 4 * NTB
@@ -352,7 +353,7 @@ class Body:
         which, qb = k4 // 2, k4 % 2
         dst = sblk(J, which, qb)
         if ks == 0:
-            c = V_CS + 16 * qb if which == 0 else V_CD[qb]
+            c = None if which == 0 else V_CD[qb]
         else:
             c = dst
         b = (A_Q if which == 0 else A_O) + (qb * 8 + ks) * 4
@@ -378,7 +379,10 @@ class Body:
         return qb, ks, w, sblk(J, 0, qb) + r0, sblk(J, 1, qb) + r0, r0
 
     def ew_exp(self, J, n):
-        _, _, _, x, _, _ = self.ew_regs(J, n)
+        qb, _, _, x, _, _ = self.ew_regs(J, n)
+        for r in (x, x + 1):
+            self.p.valu(f"v_fma_f32 {vr(r)}, {vr(r)}, {sr(S_SL2)}, {vr(V_CS + 16 * qb)}",
+                        V(r) + S(S_SL2) + V(V_CS + 16 * qb), V(r))
         for r in (x, x + 1):
             self.p.trans(f"v_exp_f32_e32 {vr(r)}, {vr(r)}", V(r), V(r))
 
@@ -650,23 +654,17 @@ class Body:
                          V(V_T + 7) + V(QD) + S(RQD, 4))
 
     def finish_rows(self, do_in_acc=False):
-        """dO -> AGPRs (unless loaded there), Q * scale*log2e -> AGPRs, start values
-        -LSE*log2e, -D."""
+        """dO -> AGPRs (unless loaded there), Q -> AGPRs, -LSE*log2e (the exps' offset) and
+        -D (dP^T's start values)."""
         p = self.p
         p.waitcnt(vm=0)
         for i in range(0 if do_in_acc else 64):
             p.valu(f"v_accvgpr_write_b32 {ar(A_O + i)}, {vr(64 + i)}", V(64 + i), A(A_O + i))
-        t0, t1 = 128, 129
         for i in range(64):
-            p.valu(f"v_fma_mix_f32 {vr(t0)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t0))
-            p.valu(f"v_fma_mix_f32 {vr(t1)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t1))
-            p.valu(f"v_cvt_pk_f16_f32 {vr(i)}, {vr(t0)}, {vr(t1)}", V(t0, 2), V(i))
             p.valu(f"v_accvgpr_write_b32 {ar(A_Q + i)}, {vr(i)}", V(i), A(A_Q + i))
         for qb in range(2):
             c = V_CS + 16 * qb
             p.valu(f"v_mul_f32_e32 {vr(c)}, 0xbfb8aa3b, {vr(V_T + 5 + qb)}", V(V_T + 5 + qb), V(c))
-            for r in range(1, 16):
-                p.valu(f"v_mov_b32_e32 {vr(c + r)}, {vr(c)}", V(c), V(c + r))
             d = V_CD[qb]
             p.valu(f"v_sub_f32_e32 {vr(d)}, 0, {vr(V_ND + qb)}", V(V_ND + qb), V(d))
             for r in range(1, 16):

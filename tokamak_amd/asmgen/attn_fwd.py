@@ -11,8 +11,7 @@ Work decomposition: persistent, one workgroup (4 waves, one per SIMD) per comput
 items (batch, q-head, block of 256 query rows; block fastest) in snake order over rounds of NWG
 items, consecutive items of a round on one XCD (xcd_slot): the query blocks of a head, and the
 q-heads of a kv group, read the same K/V tiles through that XCD's L2, and for causal the long
-and short blocks of consecutive rounds pair up.  A wave owns 64 query rows: Q (prescaled by scale*log2(e), rounded to
-fp16) sits in AGPRs as two 32-row blocks, so every K or V operand read from LDS feeds two
+and short blocks of consecutive rounds pair up.  A wave owns 64 query rows: Q (fp16, as loaded) sits in AGPRs as two 32-row blocks, so every K or V operand read from LDS feeds two
 MFMAs, and its O^T accumulators sit in AGPRs.  K/V tiles of 64 keys go HBM -> LDS by buffer
 DMA into two K and two V buffers (rows past the valid range read as zero), row-major with the
 XOR chunk swizzle chunk' = chunk ^ (4*(row&3) + (row>>2&3)).  The DMA stream is a cursor of
@@ -22,9 +21,12 @@ item ends, the next item's first tiles are already in LDS.
 Per tile t a wave runs a fixed 64-slot schedule (one v_mfma_f32_32x32x16_f16 per slot):
   slots  0..31   S(t+1) = K(t+1) Q^T into the free score register set;
   slots 32..63   O^T += V(t)^T P(t)^T, V^T read from the row-major tile by ds_read_b64_tr_b16;
-the softmax of S(t) runs between the MFMAs of slots 0..56: P = exp2(S) (the accumulator
-starts at -m, m = the row max of the item's first tile), packed to fp16 for the MFMA, row
-sums accumulated in fp32 by v_add_f32.  The eight DMA requests of K(t+2) and V(t+1) go one
+the softmax of S(t) runs between the MFMAs of slots 0..56: P = exp2(fma(S, scale*log2(e),
+-m)) with m the row max of the item's first tile in log2 units.  The scores are the unscaled
+fp16 products, summed in fp32, and the scale is applied in fp32, as the reference's kernel
+does: a scale folded into Q and rounded to fp16 moves a score s by up to |s|*2^-12, which
+trained attention logits turn into errors past the bars.  P is packed to fp16 for the MFMA,
+and the row sums accumulate in fp32 by v_add_f32.  The eight DMA requests of K(t+2) and V(t+1) go one
 every four slots; the scalar bookkeeping (the stream's next tile descriptors, the next
 body's variant) is spliced between the MFMAs of slots 32..63, and a body jumps straight into
 the next common body.  A wave's last active tile (the only one that can need a mask: causal
@@ -90,7 +92,7 @@ NEXT_FREE_SGPR = 96
 
 # ---- VGPRs
 V_SET = (0, 64)         # score register sets; block (kb, qb) at +(kb*2+qb)*16
-V_CINIT = 128           # -m replicated: qb*16 + r
+V_NEGM = 128            # -m of the lane's row in log2 units, per qb
 V_P = 160               # P[qb][ks] at 160 + (qb*4+ks)*4
 V_KBUF = 192
 V_VBUF = V_KBUF + 4 * NKB
@@ -111,7 +113,7 @@ V_T = V_P + 4               # temporaries of the item boundary, when P is free (
 # ---- AGPRs
 A_O = 0                 # o[db][qb] at (db*2+qb)*16
 A_Q = 128               # q[qb][ks] at 128 + (qb*8+ks)*4
-A_QN = 192              # the next item's Q as loaded (same order), before the prescale
+A_QN = 192              # the next item's Q as loaded (same order)
 ACC = set(A(A_O, 128))
 
 # body variants by code: 4*act(t+1) + 2*act(t) + mask(t); 8 = the item's end
@@ -389,17 +391,14 @@ class Body:
                            V(dst + 2 * tt, 2), V(V_VOFF + tt * 4 + db))
 
     # ---------------------------------------------------------------- MFMAs
-    def s_mfma(self, i, J, init):
-        """S MFMA i of set J: ri = i//2, qb = i%2, kb = ri//8, ks = ri%8.  init for the first
-        k-step: 'zero' (accumulate from 0) or 'cinit' (from -m)."""
+    def s_mfma(self, i, J, qbase=A_Q):
+        """S MFMA i of set J (unscaled scores, from 0): ri = i//2, qb = i%2, kb = ri//8,
+        ks = ri%8; Q from the AGPRs at qbase."""
         ri, qb = i // 2, i % 2
         kb, ks = ri // 8, ri % 8
         dst = sblk(J, kb, qb)
-        if ks == 0:
-            c = None if init == "zero" else V_CINIT + qb * 16
-        else:
-            c = dst
-        self.p.mfma(MFMA, dst, V_KBUF + (ri % NKB) * 4, A_Q + (qb * 8 + ks) * 4, c, b_acc=True)
+        c = None if ks == 0 else dst
+        self.p.mfma(MFMA, dst, V_KBUF + (ri % NKB) * 4, qbase + (qb * 8 + ks) * 4, c, b_acc=True)
 
     def pv_mfma(self, j):
         vi, qb = j // 2, j % 2
@@ -420,7 +419,10 @@ class Body:
         return x0, qb, ks, w
 
     def sm_exp(self, J, n):
-        x0, _, _, _ = self.sm_regs(J, n)
+        x0, qb, _, _ = self.sm_regs(J, n)
+        for x in (x0, x0 + 1):
+            self.p.valu(f"v_fma_f32 {vr(x)}, {vr(x)}, {sr(S_SL2)}, {vr(V_NEGM + qb)}",
+                        V(x) + S(S_SL2) + V(V_NEGM + qb), V(x))
         for x in (x0, x0 + 1):
             self.p.trans(f"v_exp_f32_e32 {vr(x)}, {vr(x)}", V(x), V(x))
 
@@ -443,51 +445,35 @@ class Body:
         self.p.valu(f"v_max_f32_e32 {vr(V_LMAX + qb)}, {vr(V_LMAX + qb)}, {vr(lt)}", V(V_LMAX + qb) + V(lt), V(V_LMAX + qb))
 
     # ---- whole stages (unpipelined)
-    def stage_s(self, J, kbase, init):
+    def stage_s(self, J, kbase):
         """S(J) = K Q^T from the K buffer at kbase; reads run LK slots ahead."""
         reads_issued = 0
         for i in range(32):
             while reads_issued < 16 and reads_issued * 2 - LK <= i:
                 self.k_read(reads_issued, kbase)
                 reads_issued += 1
-            self.s_mfma(i, J, init)
+            self.s_mfma(i, J)
 
-    def prescale_block(self, blk, T):
-        """Q block blk = qb*8 + ks (four words) of the next item: from its AGPRs, times
-        scale*log2(e), rounded to fp16 pairs, into the Q AGPRs.  Temporaries: T .. T+47."""
-        p = self.p
-        for j in range(4):
-            w = blk * 4 + j
-            r, lo = T + w % 16, T + 16 + (w % 16) * 2
-            p.valu(f"v_accvgpr_read_b32 {vr(r)}, {ar(A_QN + w)}", A(A_QN + w), V(r))
-            p.valu(f"v_fma_mix_f32 {vr(lo)}, {vr(r)}, {sr(S_SL2)}, 0 op_sel_hi:[1,0,0]", V(r) + S(S_SL2), V(lo))
-            p.valu(f"v_fma_mix_f32 {vr(lo + 1)}, {vr(r)}, {sr(S_SL2)}, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]",
-                   V(r) + S(S_SL2), V(lo + 1))
-            p.valu(f"v_cvt_pk_f16_f32 {vr(r)}, {vr(lo)}, {vr(lo + 1)}", V(lo, 2), V(r))
-            p.valu(f"v_accvgpr_write_b32 {ar(A_Q + w)}, {vr(r)}", V(r), A(A_Q + w))
-
-    def stage_s_prescaled(self, J, kbase):
-        """S(J) = K Q^T from the K buffer at kbase (accumulating from 0) while the next item's
-        Q is prescaled into the Q AGPRs: each block of Q is prescaled just before the first
-        MFMA that reads it, and one more block after every MFMA, so that the VALU work runs
-        beside the MFMAs; the temporaries are the free score set J^1."""
-        T = V_SET[J ^ 1]
-        order = [qb * 8 + ks for ks in range(8) for qb in range(2)]
-        done = 0
+    def stage_s_next(self, J, kbase):
+        """S(J) = K Q^T of a new item from the next item's Q AGPRs, where its loads put it,
+        while those words are copied into the Q AGPRs for the item's bodies: two copies after
+        every MFMA, beside the MFMAs."""
         reads_issued = 0
+        copied = 0
         for i in range(32):
-            ri, qb = i // 2, i % 2
-            need = order.index(qb * 8 + ri % 8)
-            while done <= need:
-                self.prescale_block(order[done], T)
-                done += 1
             while reads_issued < 16 and reads_issued * 2 - LK <= i:
                 self.k_read(reads_issued, kbase)
                 reads_issued += 1
-            self.s_mfma(i, J, "zero")
-            if done < 16:
-                self.prescale_block(order[done], T)
-                done += 1
+            self.s_mfma(i, J, A_QN)
+            for _ in range(2):
+                self.p.valu(f"v_accvgpr_mov_b32 {ar(A_Q + copied)}, {ar(A_QN + copied)}", A(A_QN + copied),
+                            A(A_Q + copied))
+                copied += 1
+
+    def copy_next_q(self):
+        """The next item's Q into the Q AGPRs (a wave that uses no tile of the item)."""
+        for w in range(64):
+            self.p.valu(f"v_accvgpr_mov_b32 {ar(A_Q + w)}, {ar(A_QN + w)}", A(A_QN + w), A(A_Q + w))
 
     def stage_softmax(self, J):
         for n in range(33):
@@ -556,7 +542,7 @@ class Body:
                            V(base + r) + V(V_NINF) + [("vcc", 0)], V(base + r))
 
     def row_max_set_m(self, J):
-        """m = row max of set J (0 if -inf); cinit = -m; set J -= m."""
+        """m = row max of set J (unscaled; 0 if -inf): -m in log2 units for the exps."""
         p = self.p
         for qb in range(2):
             mx = V_P + qb * 2          # P registers are free here
@@ -570,16 +556,12 @@ class Body:
             p.valu(f"v_max_f32_e32 {vr(mx)}, {vr(mx)}, {vr(tmp)}", V(mx) + V(tmp), V(mx))
             p.valu(f"v_cmp_eq_f32_e32 vcc, {vr(V_NINF)}, {vr(mx)}", V(V_NINF) + V(mx), [("vcc", 0)])
             p.valu(f"v_cndmask_b32_e64 {vr(mx)}, {vr(mx)}, 0, vcc", V(mx) + [("vcc", 0)], V(mx))
-            self.set_cinit(qb, mx)
-            for x in regs:
-                p.valu(f"v_sub_f32_e32 {vr(x)}, {vr(x)}, {vr(mx)}", V(x) + V(mx), V(x))
+            self.set_negm(qb, mx)
 
-    def set_cinit(self, qb, mx):
-        p = self.p
-        ci = V_CINIT + qb * 16
-        p.valu(f"v_sub_f32_e32 {vr(ci)}, 0, {vr(mx)}", V(mx), V(ci))
-        for r in range(1, 16):
-            p.valu(f"v_mov_b32_e32 {vr(ci + r)}, {vr(ci)}", V(ci), V(ci + r))
+    def set_negm(self, qb, mx):
+        """-m in log2 units for the unscaled row max mx."""
+        self.p.valu(f"v_mul_f32_e64 {vr(V_NEGM + qb)}, -{sr(S_SL2)}, {vr(mx)}", S(S_SL2) + V(mx),
+                    V(V_NEGM + qb))
 
     def tile_max_into(self, J, mxs):
         """mxs[qb] = max(mxs[qb], row max of set J) (exact pass)."""
@@ -626,7 +608,7 @@ class Body:
                 i = dma_at[s_]
                 self.dma_m0(LDS_K[J] if i < 4 else LDS_V[Jn], i % 4)
             if s_ < 32:
-                self.s_mfma(s_, Jn, "cinit")
+                self.s_mfma(s_, Jn)
             else:
                 self.pv_mfma(s_ - 32)
                 self.p.ins.extend(h[s_ - 32])
@@ -667,11 +649,11 @@ class Body:
         p.branch(f"s_branch .Ldisp{Jn}", skip_xdl=ACC)
 
     # ---------------------------------------------------------------- item start / end
-    def q_loads(self, b, h, q0, dst_acc, untracked=False):
-        """Issue the loads of Q rows q0 + 32qb + l32 of (batch b, head h) for this wave: lane
-        (l32, hi) loads bytes hi*16 + 32ks .. +15; into VGPRs 0..63 (tracked, or untracked when
-        the caller waits for them itself) or, dst_acc, into the next-item AGPRs (untracked: the
-        next loop body's vmcnt(0) covers them)."""
+    def q_loads(self, b, h, q0, abase):
+        """Issue the loads of Q rows q0 + 32qb + l32 of (batch b, head h) for this wave into
+        the AGPRs at abase (untracked: the prologue waits for them itself, and for the next
+        item's, in the next-item AGPRs, the next loop body's vmcnt(0)): lane (l32, hi) loads
+        bytes hi*16 + 32ks .. +15."""
         p, s = self.p, self.s
         RQ = S_TMP + 16
         T0, COL, LO, HI = S_TMP + 8, S_TMP + 9, S_TMP + 10, S_TMP + 11
@@ -692,20 +674,8 @@ class Body:
         for qb in range(2):
             for ks in range(8):
                 i = (qb * 8 + ks) * 4
-                dst, regs = (ar(A_QN + i, 4), A(A_QN + i, 4)) if dst_acc else (vr(i, 4), V(i, 4))
-                p.vmem_load(f"buffer_load_dwordx4 {dst}, {vr(QOFF + qb)}, {sr(RQ, 4)}, 0 offen offset:{ks * 32}",
-                            regs, V(QOFF + qb) + S(RQ, 4), untracked=dst_acc or untracked)
-
-    def q_prescale(self):
-        """Q words (VGPRs 0..63, as loaded) -> two f32 (x * sl2) -> fp16 pair -> the Q AGPRs
-        (the prologue; later items prescale beside their first scores, stage_s_prescaled)."""
-        p = self.p
-        for i in range(64):
-            t0, t1 = V_CINIT, V_CINIT + 1
-            p.valu(f"v_fma_mix_f32 {vr(t0)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t0))
-            p.valu(f"v_fma_mix_f32 {vr(t1)}, {vr(i)}, {sr(S_SL2)}, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]", V(i) + S(S_SL2), V(t1))
-            p.valu(f"v_cvt_pk_f16_f32 {vr(i)}, {vr(t0)}, {vr(t1)}", V(t0, 2), V(i))
-            p.valu(f"v_accvgpr_write_b32 {ar(A_Q + i)}, {vr(i)}", V(i), A(A_Q + i))
+                p.vmem_load(f"buffer_load_dwordx4 {ar(abase + i, 4)}, {vr(QOFF + qb)}, {sr(RQ, 4)}, 0 offen offset:{ks * 32}",
+                            A(abase + i, 4), V(QOFF + qb) + S(RQ, 4), untracked=True)
 
     def prefetch_next_q(self, sfx):
         """Loads of the next round's item's Q rows into the next-item AGPRs (none after the
@@ -724,7 +694,7 @@ class Body:
         s(f"s_lshl_b32 {sr(QB)}, {sr(QB)}, 8", S(QB), S(QB))
         s(f"s_lshl_b32 {sr(Z)}, {sr(S_WAVE)}, 6", S(S_WAVE), S(Z))
         s(f"s_add_u32 {sr(QB)}, {sr(QB)}, {sr(Z)}", S(QB) + S(Z), S(QB))
-        self.q_loads(B, H, QB, True)
+        self.q_loads(B, H, QB, A_QN)
         p.label(f".Lpq_{sfx}")
 
     def reset_acc(self):
@@ -738,37 +708,36 @@ class Body:
             p.valu(f"v_mov_b32_e32 {vr(V_LSUM + qb)}, 0", [], V(V_LSUM + qb))
             p.valu(f"v_mov_b32_e32 {vr(V_LMAX + qb)}, 0", [], V(V_LMAX + qb))
 
-    def start_item(self, u, sfx, fixed_m, prefetch=True, drain=False, prescale=False):
+    def start_item(self, u, sfx, fixed_m, prefetch=True, drain=False, next_q=False):
         """Tile 0 of the current item (stream parity u): S(0) into set u when the wave uses
         it, its mask, and m = its row max (first pass) or S(0) from the start values -m
         (fixed_m: the exact pass after an overflow); one barrier (the first body's requests
         overwrite K buffer u; drain: every DMA of this wave done before it, for the prologue,
         whose K(1) and V(0) may still be in flight); the loads of the next item's Q
-        (prefetch); then the first body.  prescale: the item's Q is still in the next-item
-        AGPRs; it is prescaled into the Q AGPRs beside S(0)'s MFMAs (or alone, when the wave
-        uses no tile of the item), and the O accumulators are reset first."""
+        (prefetch); then the first body.  next_q: the item's Q is still in the next-item
+        AGPRs; S(0) reads it there while it is copied into the Q AGPRs (or only copied, when
+        the wave uses no tile of the item), and the O accumulators are reset first."""
         p, s = self.p, self.s
         p.comment(f"start {u}")
-        if prescale:
+        if next_q:
             self.reset_acc()
         s(f"s_cmp_eq_u32 {sr(S_ACTEND)}, 0", S(S_ACTEND), [("scc", 0)])
         p.branch(f"s_cbranch_scc1 .Lsn_{sfx}", [("scc", 0)], skip_xdl=ACC)
-        if prescale:
-            self.stage_s_prescaled(u, LDS_K[u])
+        if next_q:
+            self.stage_s_next(u, LDS_K[u])
         else:
-            self.stage_s(u, LDS_K[u], "cinit" if fixed_m else "zero")
+            self.stage_s(u, LDS_K[u])
         s(f"s_cmp_eq_u32 {sr(S_MASKB)}, 0", S(S_MASKB), [("scc", 0)])
         p.branch(f"s_cbranch_scc0 .Lsm_{sfx}", [("scc", 0)], skip_xdl=ACC)
         self.stage_mask(u, S_IT)
         p.label(f".Lsm_{sfx}")
         if not fixed_m:
             self.row_max_set_m(u)
-        if prescale:
+        if next_q:
             p.branch(f"s_branch .Lsj_{sfx}", skip_xdl=ACC)
         p.label(f".Lsn_{sfx}")
-        if prescale:
-            for blk in range(16):
-                self.prescale_block(blk, V_SET[u ^ 1])
+        if next_q:
+            self.copy_next_q()
             p.label(f".Lsj_{sfx}")
         p.waitcnt(vm=0 if drain else None, lgkm=0)
         p.barrier()
@@ -847,7 +816,7 @@ class Body:
             p.trans(f"v_log_f32_e32 {vr(LG)}, {vr(L_)}", V(L_), V(LG))
             p.valu(f"v_cmp_lt_f32_e32 vcc, 0, {vr(L_)}", V(L_), [("vcc", 0)])
             p.valu(f"v_cndmask_b32_e64 {vr(INV)}, 0, {vr(INV)}, vcc", V(INV) + [("vcc", 0)], V(INV))
-            p.valu(f"v_sub_f32_e32 {vr(LG)}, {vr(LG)}, {vr(V_CINIT + qb * 16)}", V(LG) + V(V_CINIT + qb * 16), V(LG))
+            p.valu(f"v_sub_f32_e32 {vr(LG)}, {vr(LG)}, {vr(V_NEGM + qb)}", V(LG) + V(V_NEGM + qb), V(LG))
             p.valu(f"v_mul_f32_e32 {vr(LG)}, 0x3f317218, {vr(LG)}", V(LG), V(LG))
             p.valu(f"v_cndmask_b32_e32 {vr(LG)}, {vr(V_NINF)}, {vr(LG)}, vcc", V(V_NINF) + V(LG) + [("vcc", 0)], V(LG))
             p.vmem_store(f"buffer_store_dword {vr(LG)}, {vr(LO)}, {sr(S_RL, 4)}, 0 offen nt", V(LG) + V(LO) + S(S_RL, 4))
@@ -935,20 +904,18 @@ def build(check_ldb: int = 12288) -> str:
     p.valu(f"v_lshlrev_b32_e32 {vr(V_HI4)}, 2, {vr(HI)}", V(HI), V(V_HI4))
     p.valu(f"v_mov_b32_e32 {vr(V_NINF)}, 0xff800000", [], V(V_NINF))
     # ------------------------------------------------------------------ first item
-    # The wave's Q rows are requested first and K(0) next, so that the prescale and S(0) wait
-    # only for those while K(1) and V(0) are still arriving (every workgroup requests its first
-    # rows at once, and HBM serves them roughly in order).
+    # The wave's Q rows are requested first and K(0) next, so that S(0) waits only for those
+    # while K(1) and V(0) are still arriving (every workgroup requests its first rows at once,
+    # and HBM serves them roughly in order).
     for r in (S_KA, S_KD, S_PASS):
         sal(f"s_mov_b32 {sr(r)}, 0", [], S(r))
     b.item_index(S_KA, S_TMP + 15, S_TMP + 12)
     b.decode_a(S_TMP + 15, "p")
-    b.q_loads(S_BA, S_HA, S_Q0, False, untracked=True)      # 16 loads
+    b.q_loads(S_BA, S_HA, S_Q0, A_Q)                         # 16 loads
     b.decode_d("p0")
     b.stream_start(0, "p")                                   # K(0), K(1), V(0): 4 DMAs each
     b.reset_acc()
-    p.waitcnt(vm=12)                                         # the Q rows
-    b.q_prescale()
-    p.waitcnt(vm=8)                                          # this wave's part of K(0)
+    p.waitcnt(vm=8)                                          # the Q rows, this wave's part of K(0)
     p.barrier()
     b.start_item(0, "p", False, drain=True)
     for u in range(2):
@@ -1019,7 +986,7 @@ def _boundary(b: Body, u: int):
     p.comment("next q")
     b.decode_a(I, f"b{u}")
     s(f"s_mov_b32 {sr(S_PASS)}, 0", [], S(S_PASS))
-    b.start_item(u, f"b{u}", False, prescale=True)
+    b.start_item(u, f"b{u}", False, next_q=True)
 
 
 def _redo(b: Body, u: int):
@@ -1050,7 +1017,7 @@ def _redo(b: Body, u: int):
     p.barrier()
     s(f"s_cmp_lt_u32 {sr(T)}, {sr(S_ACTEND)}", S(T) + S(S_ACTEND), [("scc", 0)])
     p.branch(f"s_cbranch_scc0 .Lxs{u}", [("scc", 0)], skip_xdl=ACC)
-    b.stage_s(0, LDS_K[0], "zero")
+    b.stage_s(0, LDS_K[0])
     s(f"s_cmp_lt_u32 {sr(T)}, {sr(S_MASKB)}", S(T) + S(S_MASKB), [("scc", 0)])
     p.branch(f"s_cbranch_scc1 .Lxn{u}", [("scc", 0)], skip_xdl=ACC)
     b.stage_mask(0, T)
@@ -1066,7 +1033,7 @@ def _redo(b: Body, u: int):
         mx = MX[qb]
         p.valu(f"v_cmp_eq_f32_e32 vcc, {vr(V_NINF)}, {vr(mx)}", V(V_NINF) + V(mx), [("vcc", 0)])
         p.valu(f"v_cndmask_b32_e64 {vr(mx)}, {vr(mx)}, 0, vcc", V(mx) + [("vcc", 0)], V(mx))
-        b.set_cinit(qb, mx)
+        b.set_negm(qb, mx)
     b.reset_acc()
     # the stream back to the item's tile 0, its first requests into the buffers of parity u
     s(f"s_mov_b32 {sr(S_KD)}, {sr(S_KA)}", S(S_KA), S(S_KD))

@@ -25,12 +25,13 @@
 // immediate.  The two waves of a SIMD (different workgroups) overlap each other's softmax
 // with MFMAs.
 //
-// fp16: Q is multiplied by scale*log2e once (per element, rounded to fp16) and the S
-// accumulator starts at -m, so P = exp2(acc) needs no further arithmetic.  m is set from
+// Scores are the unscaled 16-bit products summed in fp32; scale*log2e and -m are applied in
+// fp32 with one FMA per score, P = exp2(fma(s, c, -m)), as the reference's kernel scales in
+// fp32 (a scale folded into Q and rounded to 16 bits would move a score s by up to
+// |s|*2^-12, which trained attention logits turn into errors past the bars).  m is set from
 // the first tile and never moved: rows whose max later grows beyond the 16-bit range (an
 // overflowing P, i.e. a growth of more than 2^15 for fp16) make the workgroup redo its rows
-// with the exact row max from an extra pass.  bf16 keeps Q unscaled (its 8-bit mantissa
-// would perturb the scores) and applies scale and -m with one FMA per score.
+// with the exact row max from an extra pass.
 // Causal: tiles above the diagonal are neither loaded nor computed, tiles crossing the
 // diagonal (or the kv_len / S edge) are masked, heaviest query blocks are launched first.
 #include <type_traits>
@@ -51,7 +52,6 @@ __global__ __launch_bounds__(256 * KSPLIT) __attribute__((amdgpu_waves_per_eu(2,
 void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
                    float* __restrict__ lse, const int32_t* __restrict__ kv_len, int B, int S,
                    int Hq, int Hkv, float sl2, int causal, int n_qblk) {
-    constexpr bool PRE = (DT == DT_F16);  // scale folded into Q, -m into the accumulator
     constexpr bool SPL = Split<DT>::on;   // bf16: P as hi + lo
     constexpr int NW = 4;                 // waves per group (two workgroups, or one of two groups, per CU)
     constexpr int WR = 32 * QB;           // query rows per wave
@@ -97,17 +97,7 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
         const uint16_t* qp = bqkv + (size_t)q * ld + (size_t)h * D + hi * 8;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            const u32x4 raw = q < S ? ld_global16(qp + ks * 16) : u32x4{0u, 0u, 0u, 0u};
-            if constexpr (PRE) {
-                const f16x2 x0 = as_f16x2(raw[0]), x1 = as_f16x2(raw[1]);
-                const f16x2 x2 = as_f16x2(raw[2]), x3 = as_f16x2(raw[3]);
-                qf[qb][ks] = u32x4{pack2<DT>((float)x0[0] * sl2, (float)x0[1] * sl2),
-                                   pack2<DT>((float)x1[0] * sl2, (float)x1[1] * sl2),
-                                   pack2<DT>((float)x2[0] * sl2, (float)x2[1] * sl2),
-                                   pack2<DT>((float)x3[0] * sl2, (float)x3[1] * sl2)};
-            } else {
-                qf[qb][ks] = raw;
-            }
+            qf[qb][ks] = q < S ? ld_global16(qp + ks * 16) : u32x4{0u, 0u, 0u, 0u};
         }
     }
 
@@ -165,12 +155,10 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) o[db][qb] = f32x16{};
     float m[QB], lsum[QB];      // m: running max (log2 units) once tile 0 is done
-    f32x16 cinit[QB];           // PRE: -m in every element (S accumulator init)
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         m[qb] = 0.f;
         lsum[qb] = 0.f;
-        cinit[qb] = f32x16{};
     }
     f32x16 sr[1][NKB][QB];  // scores of the current tile
     u32x4 pr[1][QB][PKS];   // its P (hi part for bf16)
@@ -178,7 +166,7 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    // S(tile) into register set J: S^T = K Q^T (+ cinit = -m for PRE).
+    // S(tile) into register set J: S^T = K Q^T (unscaled).
     auto stage_s = [&](const char* kt, auto Jc) __attribute__((always_inline)) {
         constexpr int J = decltype(Jc)::value;
 #pragma unroll
@@ -188,7 +176,7 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
                 const u32x4 a = ld_lds16((const uint16_t*)(kt + kb * 32 * ROWB + koff[ks]));
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb)
-                    sr[J][kb][qb] = mfma32<DT>(a, qf[qb][ks], ks == 0 ? cinit[qb] : sr[J][kb][qb]);
+                    sr[J][kb][qb] = mfma32<DT>(a, qf[qb][ks], ks == 0 ? f32x16{} : sr[J][kb][qb]);
             }
     };
     auto stage_mask = [&](int t, auto Jc) __attribute__((always_inline)) {
@@ -207,7 +195,7 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
         }
     };
     // exp2 of the scores in set J (relative to mm[qb]), packed to 16 bits into P set J;
-    // lt[qb] = the lane's fp32 sum of the packed values.  PRE: scores are S*c - m already.
+    // lt[qb] = the lane's fp32 sum of the packed values.
     auto stage_exp = [&](auto Jc, const float (&mm)[QB], float (&lt)[QB]) __attribute__((always_inline)) {
         constexpr int J = decltype(Jc)::value;
 #pragma unroll
@@ -219,13 +207,8 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
                     float x0 = sr[J][kb][qb][r0 + 2 * w], x1 = sr[J][kb][qb][r0 + 2 * w + 1];
-                    if constexpr (PRE) {
-                        x0 -= mm[qb];
-                        x1 -= mm[qb];
-                    } else {
-                        x0 = __builtin_fmaf(x0, sl2, -mm[qb]);
-                        x1 = __builtin_fmaf(x1, sl2, -mm[qb]);
-                    }
+                    x0 = __builtin_fmaf(x0, sl2, -mm[qb]);
+                    x1 = __builtin_fmaf(x1, sl2, -mm[qb]);
                     const float p0 = fast_exp2(x0), p1 = fast_exp2(x1);
                     if constexpr (SPL) {
                         const u32x2 hl = pack_split_bf16(p0, p1);
@@ -270,35 +253,24 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
             mx[qb] = half_max(v);
         }
     };
-    auto set_cinit = [&]() __attribute__((always_inline)) {
-        if constexpr (PRE) {
-#pragma unroll
-            for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) cinit[qb][r] = -m[qb];
-        }
-    };
-    // Tile 0 (scores relative to 0: cinit is still 0): establishes m, which then stays fixed.
+    // Tile 0: establishes m (log2 units), which then stays fixed.
     auto softmax_first = [&](auto Jc) __attribute__((always_inline)) {
         float mx[QB];
         row_max(Jc, mx);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-            const float v = PRE ? mx[qb] : mx[qb] * sl2;
+            const float v = mx[qb] * sl2;
             m[qb] = (v == -INFINITY) ? 0.f : v;
         }
         stage_exp(Jc, m, lsum);
-        set_cinit();
     };
     // Later tiles, against the fixed m.  An overflowing P (the row max grew beyond the
     // 16-bit range) cannot be repaired in place without keeping O in VALU-addressable
     // registers; the wave flags the workgroup instead, which redoes its rows with the exact
     // row max (below).  lsum is not used once the flag is set.
     auto softmax_next = [&](auto Jc) __attribute__((always_inline)) {
-        float lt[QB], mm[QB];
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) mm[qb] = PRE ? 0.f : m[qb];
-        stage_exp(Jc, mm, lt);
+        float lt[QB];
+        stage_exp(Jc, m, lt);
         bool bad = false;
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
@@ -351,10 +323,7 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
         // repeats the main loop with m fixed to it (every P <= 1, nothing can overflow).
         float mx[QB];
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            mx[qb] = -INFINITY;
-            cinit[qb] = f32x16{};
-        }
+        for (int qb = 0; qb < QB; ++qb) mx[qb] = -INFINITY;
         for (int i = 0; i < nit; ++i) {
             const int t = tb + i;
             if (t < te) issue(t, 0, 0);
@@ -366,7 +335,7 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
                 float tm[QB];
                 row_max(I0{}, tm);
 #pragma unroll
-                for (int qb = 0; qb < QB; ++qb) mx[qb] = fmaxf(mx[qb], PRE ? tm[qb] : tm[qb] * sl2);
+                for (int qb = 0; qb < QB; ++qb) mx[qb] = fmaxf(mx[qb], tm[qb] * sl2);
             }
             __syncthreads();
         }
@@ -377,7 +346,6 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
 #pragma unroll
             for (int db = 0; db < NDB; ++db) o[db][qb] = f32x16{};
         }
-        set_cinit();
         main_loop(true);
     }
 
