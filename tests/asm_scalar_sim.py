@@ -2,9 +2,9 @@
 
 It runs every workgroup of a launch wave by wave: scalar ALU, scalar loads from the kernel
 arguments and kv_len, branches, M0, barriers, and the buffer descriptors of every DMA and
-store.  Vector work is skipped: the two vector results the scalar code consumes are the wave
-index (v_readfirstlane of v0 >> 6) and the fp16 overflow vote (taken as "no overflow", or
-forced by the caller).  Waves of a workgroup run until each reaches its next s_barrier, so
+store.  Vector work is skipped: the vector results the scalar code consumes are the wave index
+(v_readfirstlane of v0 >> 6) and lane masks of vector compares (the forward's rescale test:
+every lane, or none, as the caller chooses).  Waves of a workgroup run until each reaches its next s_barrier, so
 a barrier that not all four waves reach fails the run instead of hanging a GPU.
 
 What the kernels under test must show: every workgroup terminates; each DMA and store
@@ -130,12 +130,12 @@ def _s32(x):
 class Sim:
     """kernarg: bytes of the argument segment; mem: name -> (base, bytes, row pitch, bytes a
     lane row touches) of the tensors the descriptors may cover; kv_len: list or None (its pointer in the arguments is nonzero then);
-    n_wg: grid; overflow: set of (wg, item round) whose overflow vote says yes; expect: a
+    n_wg: grid; vcmp_lanes: the lane mask every v_cmp_*_e64 writes; expect: a
     callable (wave, event words) -> list of checks [(lds_base, base, nrec)] of LDS tiles
     the wave reads at that event, or None; on_event(wave, words) for bookkeeping; wave_vgpr:
     the VGPR holding v0 >> 6 when the prologue reads the wave index from it."""
 
-    def __init__(self, lines, kernarg, mem, kv_len, n_wg, expect, on_event=None, overflow=(),
+    def __init__(self, lines, kernarg, mem, kv_len, n_wg, expect, on_event=None, vcmp_lanes=M64,
                  tile_bytes=16384, max_steps=2_000_000, wave_vgpr=64, lane_max=None):
         self.ins, self.labels = parse(lines)
         self.lane_max = dict(lane_max or {})
@@ -146,7 +146,7 @@ class Sim:
         self.n_wg = n_wg
         self.expect = expect
         self.on_event = on_event
-        self.overflow = set(overflow)
+        self.vcmp_lanes = vcmp_lanes
         self.tile_bytes = tile_bytes
         self.max_steps = max_steps
         self.stores = []
@@ -207,7 +207,6 @@ class Sim:
         self.lds = {}        # 1 KB slot -> (phase, base, nrec)
         self.reads = {}      # (phase) -> set of slots read
         self.writes = {}     # (phase) -> set of slots written
-        self.votes = 0
         phase = 0
         steps = 0
         while True:
@@ -288,14 +287,12 @@ class Sim:
             return
         if op == "v_readfirstlane_b32":
             src = a[1]
-            if src == ("v", self.wave_vgpr, 1):
-                w.put(a[0], w.wave)       # wave index (v0 >> 6 in the prologue)
-            else:
-                key = (w.wg, w.s.get(32))
-                w.put(a[0], 1 if key in self.overflow else 0)
+            if src != ("v", self.wave_vgpr, 1):
+                raise Fail(f"v_readfirstlane of an unmodelled register: {text}")
+            w.put(a[0], w.wave)           # wave index (v0 >> 6 in the prologue)
             return
         if op.startswith("v_cmp") and op.endswith("_e64"):
-            w.put(a[0], M64, True)         # every lane passes (overflow vote: no bad lane)
+            w.put(a[0], self.vcmp_lanes, True)
             return
         if op.startswith("s_load_dword"):
             cnt = {"s_load_dword": 1, "s_load_dwordx2": 2, "s_load_dwordx4": 4, "s_load_dwordx8": 8,

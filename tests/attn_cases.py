@@ -111,40 +111,41 @@ def gradient_term_rms(qkv, o_stored, dout, lse, B, S, Hq, Hkv, D, causal=True, k
     return np.sqrt(rq), np.sqrt(rk), np.sqrt(rv)
 
 
-def fp16_forward_repeats(qkv, B, S, Hq, Hkv, D, causal):
-    """The fp16 D = 128 assembly forward's overflow test (tokamak_amd/asmgen/attn_fwd.py:
-    overflow_vote), evaluated on the CPU for every item (b, h, block of
-    256 query rows): per row, m = max over the item's first tile (keys 0..63, visible ones) of
-    s' = (q . k) * sl2 (fp32, sl2 = scale * log2 e); for every tile, each lane sums exp2(s' - m) over its 32 keys
-    of the tile (the keys whose index mod 8 is in the lane's half); the item repeats if any
-    such sum reaches 65504.  Returns (number of items, items that repeat, largest
-    max_j(s') - m over all rows in log2 units; the repeat needs about 16)."""
+def fp16_forward_rescales(qkv, B, S, Hq, Hkv, D, causal, threshold=None):
+    """The fp16 D = 128 assembly forward's lazy rescale (tokamak_amd/asmgen/attn_fwd.py:
+    rescale_test, rescale_if), evaluated on the CPU.  Per wave (64 query rows of one q-head):
+    m_row starts as the row max over the first 64-key tile of s' = (q . k) * sl2 (fp32, log2
+    units, visible keys only; 0 for a row with none there); each later tile the wave uses is
+    tested, and if any of the wave's rows has a visible s' above m_row + threshold, every row
+    takes m_row = max(m_row, its max over the tile).  Returns (tiles tested, tiles rescaled,
+    largest max_j(s') - (first tile's max) over all rows, in log2 units).  The threshold is the
+    kernel's RESCALE_LOG2 unless given."""
+    if threshold is None:
+        from tokamak_amd.asmgen.attn_fwd import RESCALE_LOG2 as threshold
     sl2 = np.float32(np.float32(1.0) / np.sqrt(np.float32(D)) * np.float32(1.4426950408889634))
     x = qkv.reshape(B, S, Hq + 2 * Hkv, D)
     g = Hq // Hkv
-    n_items = n_redo = 0
+    tested = rescaled = 0
     growth = -np.inf
     i = np.arange(S)[:, None]
     j = np.arange(S)[None, :]
     vis = (j <= i) if causal else np.ones((S, S), bool)
-    half = (np.arange(S) % 8) // 4          # the lane half that holds key j
-    tile = np.arange(S) // 64
     nt = (S + 63) // 64
     for b in range(B):
         for h in range(Hq):
             q = x[b, :, h].astype(np.float32)
             k = x[b, :, Hq + h // g].astype(np.float32)
-            s = (q @ k.T) * sl2                                   # fp32, log2 units
-            s = np.where(vis, s, -np.inf)
-            first = np.where(tile[None, :] == 0, s, -np.inf).max(axis=1)
-            m = np.where(np.isfinite(first), first, 0.0)
-            growth = max(growth, float(np.nanmax(np.where(vis, s - m[:, None], -np.inf))))
-            with np.errstate(over="ignore"):
-                p = np.where(vis, np.exp2(np.minimum(s - m[:, None], 126.0)), 0.0)
-            sums = np.zeros((S, nt, 2))
-            np.add.at(sums, (slice(None), tile, half), p)       # per row, tile, lane half
-            bad_row = (sums >= 65504.0).any(axis=(1, 2))
-            for z in range((S + 255) // 256):
-                n_items += 1
-                n_redo += bool(bad_row[256 * z:256 * z + 256].any())
-    return n_items, n_redo, growth
+            s = np.where(vis, (q @ k.T) * sl2, -np.inf)            # fp32, log2 units
+            tmax = np.stack([s[:, 64 * t:64 * t + 64].max(axis=1) for t in range(nt)], axis=1)
+            m0 = np.where(np.isfinite(tmax[:, 0]), tmax[:, 0], 0.0)
+            growth = max(growth, float(np.max(np.where(np.isfinite(tmax), tmax - m0[:, None], -np.inf))))
+            for r0 in range(0, S, 64):
+                m = m0[r0:r0 + 64].copy()
+                last = min(nt, r0 // 64 + 1) if causal else nt
+                for t in range(1, last):
+                    tm = tmax[r0:r0 + 64, t]
+                    tested += 1
+                    if np.any(tm > m + threshold):
+                        rescaled += 1
+                        m = np.maximum(m, tm)
+    return tested, rescaled, growth

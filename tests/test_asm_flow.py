@@ -8,7 +8,7 @@ import pytest
 
 from tokamak_amd.asmgen import attn_fwd, gfx950
 
-from asm_scalar_sim import Fail, Sim
+from asm_scalar_sim import M64, Fail, Sim
 
 QKV, OUT, LSE, KVLEN = 0x10000000, 0x40000000, 0x70000000, 0x7F000000
 
@@ -43,7 +43,7 @@ def fwd_lines():
     return _lines["fwd"]
 
 
-def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, overflow=()):
+def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, vcmp_lanes=M64):
     n_qblk = (S + 255) // 256
     bhq, G = B * Hq, Hq // Hkv
     n_items = n_qblk * bhq
@@ -122,7 +122,7 @@ def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, overflow=()):
                 raise Fail(f"next-item Q loads of another head: {sorted({base for _, base in loads})}")
             checked[0] += 1
 
-    sim = Sim(fwd_lines(), args, mem, kv, n_wg, expect, on_event, overflow=overflow)
+    sim = Sim(fwd_lines(), args, mem, kv, n_wg, expect, on_event, vcmp_lanes=vcmp_lanes, max_steps=8_000_000)
     sim.run()
     want = {(b, h, 256 * z + 64 * wv) for b in range(B) for h in range(Hq) for z in range(n_qblk) for wv in range(4)}
     assert set(stored) == want and all(c == 1 for c in stored.values()), \
@@ -151,11 +151,12 @@ def test_fwd_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg):
     run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg)
 
 
-def test_fwd_scalar_flow_redo():
-    """An overflow vote in some items: the item is repeated with the stream rewound, every
-    tile still arrives as expected and each item is stored once."""
-    run_fwd(2, 700, 4, 2, True, None, 3, overflow={(0, 0), (1, 2), (2, 5)})
-    run_fwd(1, 512, 2, 1, False, [300], 2, overflow={(0, 1), (1, 0)})
+def test_fwd_scalar_flow_without_rescale():
+    """The rescale test failing everywhere (no lane ever needs a larger m) leaves the same
+    flow: every tile arrives as expected and each item is stored once (the other tests run
+    with every test passing, so every body takes the rescale)."""
+    run_fwd(2, 700, 4, 2, True, None, 3, vcmp_lanes=0)
+    run_fwd(1, 512, 2, 1, False, [300], 2, vcmp_lanes=0)
 
 
 # ---------------------------------------------------------------- backward kernels

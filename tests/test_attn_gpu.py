@@ -269,14 +269,20 @@ def test_deterministic(gpu):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+@pytest.mark.parametrize("causal,kv_len", [(True, None), (False, None), (False, 450), (True, 450)],
+                         ids=["causal", "full", "full-kv450", "causal-kv450"])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-def test_growing_scores_redo_path(gpu, causal, dtype):
+def test_growing_scores_move_m(gpu, causal, kv_len, dtype):
     """Scores that grow by ~40 nats along the keys: the max from the first tile is stale by
-    far more than the 16-bit range, P overflows and the workgroup recomputes its rows with
-    the exact row max.  Must still match the oracle."""
+    far more than the 16-bit range.  The fp16 D = 128 forward raises m and rescales O and the
+    row sums as the scores grow; the HIP forward (bf16) sees a P overflow and recomputes its
+    rows with the exact row max.  With kv_len = 450 the largest scores lie past the visible
+    keys, in the masked part of the last tile and beyond: m must follow the visible keys only
+    (a rescale from unmasked scores would push every visible P below the fp16 range).  Must
+    still match the oracle, and the rescale model (tests/attn_cases.py) must see m move."""
     import torch
     from tokamak_amd import attn
+    from attn_cases import fp16_forward_rescales
     B, S, H, D = 1, 700, 2, 128
     rng = np.random.default_rng(7)
     u = rng.standard_normal(D)
@@ -289,17 +295,25 @@ def test_growing_scores_redo_path(gpu, causal, dtype):
             + 0.3 * rng.standard_normal((S, D))                                        # K
         x[0, :, 2 * H + h] = rng.standard_normal((S, D))                               # V
     qkv_r, bits = oracle.round_to(x.reshape(B, S, -1), dtype)
-    log(f"[case] growing scores S{S} {dtype} causal={int(causal)}")
+    log(f"[case] growing scores S{S} {dtype} causal={int(causal)} kv_len={kv_len}")
     qkv = to_device(bits, dtype, gpu)
-    o, lse = attn.gqa_fwd(qkv, B, S, H, H, D, causal=causal)
+    kvl = None if kv_len is None else torch.tensor([kv_len], dtype=torch.int32, device=gpu)
+    o, lse = attn.gqa_fwd(qkv, B, S, H, H, D, causal=causal, kv_len=kvl)
     torch.cuda.synchronize()
-    o_ref, lse_ref = oracle.fwd(qkv_r, B, S, H, H, D, causal=causal, f64=True)
+    kvs = None if kv_len is None else [kv_len]
+    o_ref, lse_ref = oracle.fwd(qkv_r, B, S, H, H, D, causal=causal, kv_len=kvs, f64=True)
     # the growth is real: some row's max score exceeds its max over keys 0..63 by > 20 nats
     xs = qkv_r.reshape(B, S, 3 * H, D).astype(np.float64)
     sc = np.einsum("sd,td->st", xs[0, :, 0], xs[0, :, H]) / np.sqrt(D)
     if causal:
         sc = np.where(np.tril(np.ones((S, S), dtype=bool)), sc, -np.inf)
+    if kv_len is not None:
+        sc[:, kv_len:] = -np.inf
     assert float((sc.max(axis=1) - sc[:, :64].max(axis=1)).max()) > 20.0
+    if kv_len is None:
+        tested, rescaled, _ = fp16_forward_rescales(qkv_r, B, S, H, H, D, causal)
+        log(f"    rescale model: {rescaled} of {tested} (wave, tile) steps move m")
+        assert rescaled > 0
     res = [compare("O", from_device(o), o_ref, TOL_FWD), compare("LSE", from_device(lse), lse_ref, TOL_FWD)]
     for st in res:
         log(f"    {st['name']}: max_abs={st['max_abs']:.3e} bad={st['n_bad']}")

@@ -122,23 +122,26 @@ def test_rounding_bound_catches_a_missing_term():
     assert np.all(err <= bound[0, :, 0]) and err.max() > 5e-3 * 0.2
 
 
-def test_fp16_forward_repeats_flags_growth():
-    """The CPU evaluation of the fp16 forward's overflow test: random N(0,1) rows never repeat
-    an item (their scores stay within a few log2 units of the first tile's maximum); keys whose
-    scores grow along the sequence past the fp16 range do, and the reported growth says by how
-    much."""
+def test_fp16_forward_rescales_flags_growth():
+    """The CPU evaluation of the fp16 forward's lazy rescale: random N(0,1) rows never move m
+    (their scores stay within a few log2 units of the first tile's maximum); keys whose
+    scores grow along the sequence make the waves rescale, about once per growth of the
+    threshold, and the reported growth says by how much."""
     import oracle
-    from attn_cases import fp16_forward_repeats
+    from attn_cases import fp16_forward_rescales
+    from tokamak_amd.asmgen.attn_fwd import RESCALE_LOG2
     B, S, Hq, Hkv, D = 1, 512, 2, 1, 128
     x = oracle.make_inputs(B, S, Hq, Hkv, D, "f16", seed_qkv=1)["qkv"].reshape(B, S, Hq + 2 * Hkv, D)
-    items, redo, growth = fp16_forward_repeats(x, B, S, Hq, Hkv, D, True)
-    assert (items, redo) == (4, 0) and growth < 8
+    tested, rescaled, growth = fp16_forward_rescales(x, B, S, Hq, Hkv, D, True)
+    assert tested == Hq * sum(range(8)) and rescaled == 0 and growth < 8
     u = x[0, :, :Hq].mean(axis=(0, 1))
     u /= np.linalg.norm(u)
-    for gr, want in ((0.05, 0), (0.4, 4)):
+    for gr in (0.05, 0.4):
         y = x.copy()
         y[0, :, Hq:Hq + Hkv] += gr * np.arange(S)[:, None, None] * u
         y = y.astype(np.float16).astype(np.float32)
-        items, redo, growth = fp16_forward_repeats(y, B, S, Hq, Hkv, D, True)
-        assert redo == want, (gr, redo, growth)
-        assert (growth > 16) == (want > 0)
+        tested, rescaled, growth = fp16_forward_rescales(y, B, S, Hq, Hkv, D, True)
+        assert (rescaled > 0) == (growth > RESCALE_LOG2), (gr, rescaled, growth)
+        assert gr < 0.1 or (growth > 40 and rescaled >= growth // RESCALE_LOG2), (gr, rescaled, growth)
+        # a threshold above every growth never rescales; a tiny one rescales at every rise
+        assert fp16_forward_rescales(y, B, S, Hq, Hkv, D, True, threshold=growth + 1)[1] == 0

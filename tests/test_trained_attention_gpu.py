@@ -1,18 +1,17 @@
 """The attention kernels on trained weights (GPU).
 
-The fp16 D = 128 forward fixes each row's softmax offset m at the row maximum of the item's
-first 64-key tile and repeats an item with the exact maximum when a later P overflows fp16
-(tokamak_amd/asmgen/attn_fwd.py).  Random N(0,1) inputs never take the repeat; trained
-attention that singles out a far key could.  This test trains tests/golden/models/induction.tkm
+The fp16 D = 128 forward starts each row's softmax offset m at the row maximum of the item's
+first 64-key tile and raises it only when a later tile has a score more than RESCALE_LOG2 = 15
+log2 units above it (a lazy rescale of O and the row sums, tokamak_amd/asmgen/attn_fwd.py).  Random
+N(0,1) inputs never rescale; trained attention that singles out a far key does.  This test trains tests/golden/models/induction.tkm
 (two layers, GQA 4:2, head dim 128, causal, fp16) on an induction task -- the second half of
 every sequence repeats the first, so the loss of the second half can only fall through
 attention to the key half a sequence back -- and then, on each attention layer's actual input
 rows:
 
-- counts the work items whose forward takes the repeat, by evaluating the kernel's own test on
-  the CPU (scores (q . k) * scale * log2 e in fp32, m from the first tile, the overflow vote on
-  the per-lane partial sums of each 64-key tile), and reports the largest growth of a row's
-  score over its first-tile maximum against the threshold;
+- counts the (wave, tile) steps whose test moves m, by evaluating the kernel's own test on the
+  CPU (scores (q . k) * scale * log2 e in fp32, m from the first tile, raised per wave), and
+  reports the largest growth of a row's score over its first-tile maximum;
 - checks the forward against the CPU oracle with the plain bar;
 - checks the backward on the oracle's state (its O rounded to fp16 and its LSE, the inputs
   tkm_attn_bwd receives) against the oracle's backward, and the backward on the GPU forward's
@@ -36,7 +35,7 @@ import numpy as np
 import pytest
 
 import oracle
-from attn_cases import (TOL_BWD, TOL_FWD, compare, fp16_forward_repeats, from_device, gradient_term_rms, log,
+from attn_cases import (TOL_BWD, TOL_FWD, compare, fp16_forward_rescales, from_device, gradient_term_rms, log,
                         split_dqkv, to_device)
 
 pytestmark = pytest.mark.gpu
@@ -78,6 +77,7 @@ def _time_fwd(qkv, B, S, Hq, Hkv, D, n=20):
 
 def test_trained_induction_attention(gpu):
     import torch
+    from tokamak_amd.asmgen.attn_fwd import RESCALE_LOG2
     from tokamak_amd import attn
     from tokamak_amd import runtime as R
     buf, js = _fixture("induction")
@@ -114,9 +114,9 @@ def test_trained_induction_attention(gpu):
         C = (Hq + 2 * Hkv) * D
         bits = _read16(rt.node_device(n["in0"]), B * S * C)
         xq = oracle.widen(bits, "f16").reshape(B, S, C)
-        items, redo, growth = fp16_forward_repeats(xq, B, S, Hq, Hkv, D, bool(n["causal"]))
-        log(f"    layer {li}: {redo} of {items} forward items take the exact-max repeat; largest score "
-            f"growth over the first tile's maximum {growth:.2f} (log2 units; the repeat needs ~16)")
+        tested, rescaled, growth = fp16_forward_rescales(xq, B, S, Hq, Hkv, D, bool(n["causal"]))
+        log(f"    layer {li}: {rescaled} of {tested} tested (wave, tile) steps move m; largest score "
+            f"growth over the first tile's maximum {growth:.2f} (log2 units; a move needs {RESCALE_LOG2})")
         qkv = to_device(bits, "f16", dev)
         o, lse = attn.gqa_fwd(qkv, B, S, Hq, Hkv, D, causal=True)
         assert attn.last_kernels() == ["fwd_asm"]

@@ -22,7 +22,7 @@ Per tile t a wave runs a fixed 64-slot schedule (one v_mfma_f32_32x32x16_f16 per
   slots  0..31   S(t+1) = K(t+1) Q^T into the free score register set;
   slots 32..63   O^T += V(t)^T P(t)^T, V^T read from the row-major tile by ds_read_b64_tr_b16;
 the softmax of S(t) runs between the MFMAs of slots 0..56: P = exp2(fma(S, scale*log2(e),
--m)) with m the row max of the item's first tile in log2 units.  The scores are the unscaled
+-m)), m in log2 units.  The scores are the unscaled
 fp16 products, summed in fp32, and the scale is applied in fp32, as the reference's kernel
 does: a scale folded into Q and rounded to fp16 moves a score s by up to |s|*2^-12, which
 trained attention logits turn into errors past the bars.  P is packed to fp16 for the MFMA,
@@ -32,11 +32,15 @@ body's variant) is spliced between the MFMAs of slots 32..63, and a body jumps s
 the next common body.  A wave's last active tile (the only one that can need a mask: causal
 diagonal or kv_len edge) runs unpipelined; tiles past it only move data.
 
-At an item's end the workgroup checks P for fp16 overflow (a P above 65504 makes its lane's
-partial row sum of that tile exceed 65504).  If any wave overflowed, it computes the exact
-row max in an extra pass over the item's keys, rewinds the DMA stream to the item's first
-tile and repeats the item with m fixed.  O leaves through per-wave LDS staging rows so that
-each store writes whole 256-byte rows.
+The row offset m starts as the row max of the item's first tile and moves only when it has
+to (a lazy online softmax): between the MFMAs of slots 17..61 each lane takes the max of its
+scores in S(t+1), and if any lane of the wave has a score above m + RESCALE_LOG2 (log2
+units) the wave raises m of every row to max(m, row max of S(t+1)) after the body and
+multiplies its O accumulators and row sums by 2^(m_old - m_new) (exactly 1 for the rows whose
+m stays).  So no P exceeds 2^RESCALE_LOG2 and the fp16 pack cannot overflow, while inputs
+whose later keys stay near the first tile's scores never pay for the rescale.  A wave's
+masked last tile makes the same check after its mask.  O leaves through per-wave LDS staging
+rows so that each store writes whole 256-byte rows.
 
 The generated code's per-lane address arithmetic is evaluated here over all 4 x 64 lanes and
 checked against the HIP kernel's index formulas before any text is written.
@@ -55,8 +59,7 @@ ROWB = D * 2            # bytes per K/V row in LDS
 TILE = 64 * ROWB        # one 64-key tile
 LDS_K = (0, TILE)       # K buffers
 LDS_V = (2 * TILE, 3 * TILE)
-LDS_FLAG = 4 * TILE         # one overflow flag dword per wave
-LDS_EPI = 4 * TILE + 16     # per wave: 32 rows of 272 B staging O for the store
+LDS_EPI = 4 * TILE          # per wave: 32 rows of 272 B staging O for the store
 EPI_ROW = 272               # 256 B + 16 B pad: rows 16 B apart in the banks
 EPI_WAVE = 32 * EPI_ROW
 LDS_BYTES = LDS_EPI + 4 * EPI_WAVE
@@ -66,6 +69,10 @@ NKB = 4                 # K operand registers in rotation (need 2*NKB > LK + 2)
 NVB = 4
 assert 2 * NKB > LK + 2 and 2 * NVB > LV + 2   # a read reuses its register four reads later
 DMA0 = 2                # slot of the first DMA request (then one every four slots)
+RESCALE_LOG2 = 15.0     # m moves when a score exceeds it by more than this (P <= 32768)
+# slots of the 32 lane-max instructions of S(t+1) (blocks kb = 0 first) and of the test
+MAX_SLOTS = tuple(range(17, 33)) + tuple(range(44, 60))
+TEST_SLOT = 61
 MFMA = "v_mfma_f32_32x32x16_f16"
 
 # kernel arguments (byte offsets in the kernarg segment): qkv, out, lse, kv_len, then
@@ -82,17 +89,20 @@ S_SEQ, S_HQ, S_HKV, S_SL2, S_CAUSAL, S_NQBLK, S_LDB, S_LDO = 16, 17, 18, 19, 20,
 S_G, S_NWG, S_NI, S_BHQ, S_MAGNQ, S_MAGHQ, S_MAGG = 24, 25, 26, 27, 28, 29, 30
 # the current item
 S_KA, S_IT, S_NT, S_ACTEND, S_MASKB, S_Q0, S_KVL, S_BA = 32, 33, 34, 35, 36, 37, 38, 39
-S_HA, S_CODE, S_WAVE, S_PASS, S_LDSW, S_KVEND, S_KVHA = 40, 41, 42, 43, 44, 45, 46
+S_HA, S_CODE, S_WAVE, S_THR, S_LDSW, S_KVEND, S_KVHA = 40, 41, 42, 43, 44, 45, 46
 # the DMA stream: round KD's item, tile TD of the K position, TDP of the V position (one back)
 S_KD, S_TD, S_NTD, S_KVEND_D, S_TDP, S_KVEND_DP = 47, 48, 49, 50, 51, 52
 S_KB, S_VB, S_VBP = 54, 56, 58      # K / V row-0 addresses of the stream's items (64-bit)
 S_RK, S_RV, S_RQ, S_RL = 60, 64, 68, 72
 S_TMP = 76                          # s76..s95
-NEXT_FREE_SGPR = 96
+S_RSF = 96                          # lanes whose S(t+1) needs a larger m (64-bit mask)
+NEXT_FREE_SGPR = 98
 
 # ---- VGPRs
 V_SET = (0, 64)         # score register sets; block (kb, qb) at +(kb*2+qb)*16
 V_NEGM = 128            # -m of the lane's row in log2 units, per qb
+V_MX = 130              # the lane's max unscaled score of the next tile, per qb
+V_RT = 132              # rescale temporaries (2)
 V_P = 160               # P[qb][ks] at 160 + (qb*4+ks)*4
 V_KBUF = 192
 V_VBUF = V_KBUF + 4 * NKB
@@ -101,8 +111,7 @@ V_VOFF = V_KOFF + 8         # 8: tt*4 + db
 V_DOFF = V_VOFF + 8         # 4
 V_LSUM = V_DOFF + 4         # row sums (fp32 P, this lane's half of the keys), per qb
 V_LT = V_LSUM + 2           # this tile's partial sums: qb*2 + (0, 1)
-V_LMAX = V_LT + 4           # largest per-tile partial sum (fp16 overflow check), per qb
-V_NINF = V_LMAX + 2
+V_NINF = V_LT + 4
 V_TMP = V_NINF + 1          # 1
 V_L32 = V_TMP + 1           # lane & 31
 V_HI4 = V_TMP + 2           # 4 * (lane >> 5)
@@ -410,7 +419,9 @@ class Body:
     #      ks = n // 8, qb = (n % 8) // 4, w = n % 4, i.e. scores r0 + 2w, r0 + 2w + 1 of block
     #      (kb = ks // 2, qb), r0 = 8 (ks % 2).  The exp half writes exp2 in place; the pack
     #      half packs the pair to fp16 (the MFMA operand) and adds both fp32 values to this
-    #      tile's partial sums of the row (two accumulators per block of 32 rows).
+    #      tile's partial sums of the row (two accumulators per block of 32 rows), as the
+    #      reference sums the fp32 P (tkm_gpu.cu:403).  (A v_dot2_f32_f16 of each packed pair
+    #      with (1, 1) instead of the two adds measured 4 us slower per forward.)
     @staticmethod
     def sm_regs(J, n):
         ks, qb, w = n // 8, (n % 8) // 4, n % 4
@@ -438,11 +449,76 @@ class Body:
                 self.p.valu(f"v_add_f32_e32 {vr(lt)}, {vr(lt)}, {vr(x0 + i)}", V(lt) + V(x0 + i), V(lt))
 
     def sm_finish(self, qb):
-        """Tile done: row sum += partial sum; track the largest partial sum."""
+        """Tile done: row sum += partial sum."""
         lt = V_LT + qb * 2
         self.p.valu(f"v_add_f32_e32 {vr(lt)}, {vr(lt)}, {vr(lt + 1)}", V(lt, 2), V(lt))
         self.p.valu(f"v_add_f32_e32 {vr(V_LSUM + qb)}, {vr(V_LSUM + qb)}, {vr(lt)}", V(V_LSUM + qb) + V(lt), V(V_LSUM + qb))
-        self.p.valu(f"v_max_f32_e32 {vr(V_LMAX + qb)}, {vr(V_LMAX + qb)}, {vr(lt)}", V(V_LMAX + qb) + V(lt), V(V_LMAX + qb))
+
+    # ---- the lazy rescale: lane max of a score set, the test against m, the rescale
+    @staticmethod
+    def lane_max_steps(J):
+        """The 32 instructions that leave in V_MX + qb the lane's max of set J's scores of
+        block qb: per (qb, kb) block of 16 registers, 8 steps (v_max3 over two or three)."""
+        steps = []
+        for qb, kb in ((0, 0), (1, 0), (0, 1), (1, 1)):
+            base, mx = sblk(J, kb, qb), V_MX + qb
+            if kb == 0:
+                steps.append(("v_max3_f32", mx, (base, base + 1, base + 2)))
+                for k in range(1, 7):
+                    steps.append(("v_max3_f32", mx, (mx, base + 2 * k + 1, base + 2 * k + 2)))
+                steps.append(("v_max_f32_e32", mx, (mx, base + 15)))
+            else:
+                for k in range(8):
+                    steps.append(("v_max3_f32", mx, (mx, base + 2 * k, base + 2 * k + 1)))
+        return steps
+
+    def lane_max_step(self, step):
+        op, dst, srcs = step
+        regs = []
+        for r in srcs:
+            regs += V(r)
+        self.p.valu(f"{op} {vr(dst)}, " + ", ".join(vr(r) for r in srcs), regs, V(dst))
+
+    def rescale_test(self):
+        """S_RSF = lanes where fma(lane max, scale log2 e, -m) > RESCALE_LOG2 for either
+        block of rows."""
+        p = self.p
+        for qb in range(2):
+            p.valu(f"v_fma_f32 {vr(V_RT + qb)}, {vr(V_MX + qb)}, {sr(S_SL2)}, {vr(V_NEGM + qb)}",
+                   V(V_MX + qb) + S(S_SL2) + V(V_NEGM + qb), V(V_RT + qb))
+        p.valu(f"v_max_f32_e32 {vr(V_RT)}, {vr(V_RT)}, {vr(V_RT + 1)}", V(V_RT, 2), V(V_RT))
+        p.valu(f"v_cmp_lt_f32_e64 {sr(S_RSF, 2)}, {sr(S_THR)}, {vr(V_RT)}", S(S_THR) + V(V_RT), S(S_RSF, 2))
+
+    def rescale_if(self, label):
+        """When S_RSF has a lane: m of every row = max(m, the row max of the tested set)
+        (both lane halves), O accumulators and row sums times 2^(m_old - m_new)."""
+        p, s = self.p, self.s
+        s(f"s_cmp_lg_u64 {sr(S_RSF, 2)}, 0", S(S_RSF, 2), [("scc", 0)])
+        p.branch(f"s_cbranch_scc0 {label}", [("scc", 0)], skip_xdl=ACC)
+        p.nop(16)      # the O accumulators' last MFMAs, on every path here
+        W = V_P        # the P registers are free between bodies
+        for qb in range(2):
+            mx, nm, al = V_MX + qb, V_RT, V_RT + 1
+            p.valu(f"v_mov_b32_e32 {vr(nm)}, {vr(mx)}", V(mx), V(nm))
+            p.emit(f"v_permlane32_swap_b32_e32 {vr(nm)}, {vr(mx)}", PERMLANE, V(nm) + V(mx), V(nm) + V(mx))
+            p.valu(f"v_max_f32_e32 {vr(mx)}, {vr(mx)}, {vr(nm)}", V(mx) + V(nm), V(mx))
+            p.valu(f"v_mul_f32_e64 {vr(nm)}, -{sr(S_SL2)}, {vr(mx)}", S(S_SL2) + V(mx), V(nm))
+            p.valu(f"v_min_f32_e32 {vr(nm)}, {vr(nm)}, {vr(V_NEGM + qb)}", V(nm) + V(V_NEGM + qb), V(nm))
+            p.valu(f"v_sub_f32_e32 {vr(al)}, {vr(nm)}, {vr(V_NEGM + qb)}", V(nm) + V(V_NEGM + qb), V(al))
+            p.trans(f"v_exp_f32_e32 {vr(al)}, {vr(al)}", V(al), V(al))
+            p.valu(f"v_mov_b32_e32 {vr(V_NEGM + qb)}, {vr(nm)}", V(nm), V(V_NEGM + qb))
+            p.valu(f"v_mul_f32_e32 {vr(V_LSUM + qb)}, {vr(V_LSUM + qb)}, {vr(al)}", V(V_LSUM + qb) + V(al), V(V_LSUM + qb))
+            for db in range(4):
+                o = A_O + (db * 2 + qb) * 16
+                for j0 in (0, 8):
+                    for j in range(8):
+                        p.valu(f"v_accvgpr_read_b32 {vr(W + j)}, {ar(o + j0 + j)}", A(o + j0 + j), V(W + j))
+                    for j in range(8):
+                        p.valu(f"v_mul_f32_e32 {vr(W + j)}, {vr(W + j)}, {vr(al)}", V(W + j) + V(al), V(W + j))
+                    for j in range(8):
+                        p.valu(f"v_accvgpr_write_b32 {ar(o + j0 + j)}, {vr(W + j)}", V(W + j), A(o + j0 + j))
+                    W = V_P if W == V_P + 8 else V_P + 8
+        p.label(label)
 
     # ---- whole stages (unpipelined)
     def stage_s(self, J, kbase):
@@ -563,19 +639,6 @@ class Body:
         self.p.valu(f"v_mul_f32_e64 {vr(V_NEGM + qb)}, -{sr(S_SL2)}, {vr(mx)}", S(S_SL2) + V(mx),
                     V(V_NEGM + qb))
 
-    def tile_max_into(self, J, mxs):
-        """mxs[qb] = max(mxs[qb], row max of set J) (exact pass)."""
-        p = self.p
-        for qb in range(2):
-            mx, tmp = mxs[qb], V_TMP
-            for kb in range(2):
-                for r in range(16):
-                    x = sblk(J, kb, qb) + r
-                    p.valu(f"v_max_f32_e32 {vr(mx)}, {vr(mx)}, {vr(x)}", V(mx) + V(x), V(mx))
-            p.valu(f"v_mov_b32_e32 {vr(tmp)}, {vr(mx)}", V(mx), V(tmp))
-            p.emit(f"v_permlane32_swap_b32_e32 {vr(tmp)}, {vr(mx)}", PERMLANE, V(tmp) + V(mx), V(tmp) + V(mx))
-            p.valu(f"v_max_f32_e32 {vr(mx)}, {vr(mx)}, {vr(tmp)}", V(mx) + V(tmp), V(mx))
-
     # ---------------------------------------------------------------- loop bodies
     def tile_pipe(self, J, h):
         """Tile t with set J (= the parity of the stream position of tile t): S(t+1) into set
@@ -586,9 +649,16 @@ class Body:
         e(n) = floor(7n/4) and its pack half one slot later (P[*][ks] is complete at slot
         e(8ks+7) + 1 <= 32 + 8ks); the DMA instructions go one every four slots from slot 2
         so the vector memory path never backs up into the issue of the MFMA stream; the
-        scalar chunks h[0..31] go between the MFMAs of slots 32..63."""
+        scalar chunks h[0..31] go between the MFMAs of slots 32..63.  The lane max of S(t+1)
+        takes one instruction in each of the slots MAX_SLOTS (each block of rows after its
+        last MFMA: blocks kb = 0 end at slots 14/15, kb = 1 at 30/31), and the rescale test
+        follows at TEST_SLOT."""
         Jn = J ^ 1
         kbase, vbase = LDS_K[Jn], LDS_V[J]
+        max_at = dict(zip(MAX_SLOTS, self.lane_max_steps(Jn)))
+        assert len(max_at) == 32 and max(MAX_SLOTS) < TEST_SLOT < 64
+        assert min(k for k, st in max_at.items() if st[2][-1] >= sblk(Jn, 1, 0)) >= 33
+        assert min(max_at) >= 17
         exp_at = {(7 * n) // 4: n for n in range(32)}
         pack_at = {(7 * n) // 4 + 1: n for n in range(32)}
         dma_at = {DMA0 + 4 * i: i for i in range(8)}
@@ -618,6 +688,10 @@ class Body:
                 self.sm_pack(J, pack_at[s_])
             if s_ in (57, 59):
                 self.sm_finish((s_ - 57) // 2)
+            if s_ in max_at:
+                self.lane_max_step(max_at[s_])
+            if s_ == TEST_SLOT:
+                self.rescale_test()
             if s_ in dma_at:
                 i = dma_at[s_]
                 self.dma_ld(S_RK if i < 4 else S_RV, i % 4)
@@ -636,6 +710,10 @@ class Body:
         else:
             if variant == "lastm":
                 self.stage_mask(u, S_IT)
+                for st in self.lane_max_steps(u):
+                    self.lane_max_step(st)
+                self.rescale_test()
+                self.rescale_if(f".Lnr_lastm{u}")
             self.dma_tile(S_RK, LDS_K[u])
             self.dma_tile(S_RV, LDS_V[Jn])
             if variant != "idle":
@@ -644,6 +722,11 @@ class Body:
                 p.ins.extend(c)
         p.waitcnt(vm=0)
         p.barrier()
+        if variant == "full":
+            # S(t+1)'s test stands unless tile t+1 gets a mask first (its body tests again)
+            self.s(f"s_bitcmp1_b32 {sr(S_CODE)}, 0", S(S_CODE), [("scc", 0)])
+            p.branch(f"s_cbranch_scc1 .Lnr_full{u}", [("scc", 0)], skip_xdl=ACC)
+            self.rescale_if(f".Lnr_full{u}")
         self.s(f"s_cmp_eq_u32 {sr(S_CODE)}, 6", S(S_CODE), [("scc", 0)])
         p.branch(f"s_cbranch_scc1 .Lfull{Jn}", [("scc", 0)], skip_xdl=ACC)
         p.branch(f"s_branch .Ldisp{Jn}", skip_xdl=ACC)
@@ -698,7 +781,7 @@ class Body:
         p.label(f".Lpq_{sfx}")
 
     def reset_acc(self):
-        """O accumulators, row sums and overflow trackers to 0 (O by 8 MFMAs of zeros)."""
+        """O accumulators and row sums to 0 (O by 8 MFMAs of zeros)."""
         p = self.p
         for i in range(4):
             p.valu(f"v_mov_b32_e32 {vr(V_KBUF + i)}, 0", [], V(V_KBUF + i))
@@ -706,12 +789,10 @@ class Body:
             p.mfma(MFMA, A_O + 16 * i, V_KBUF, V_KBUF, None, dst_acc=True)
         for qb in range(2):
             p.valu(f"v_mov_b32_e32 {vr(V_LSUM + qb)}, 0", [], V(V_LSUM + qb))
-            p.valu(f"v_mov_b32_e32 {vr(V_LMAX + qb)}, 0", [], V(V_LMAX + qb))
 
-    def start_item(self, u, sfx, fixed_m, prefetch=True, drain=False, next_q=False):
+    def start_item(self, u, sfx, prefetch=True, drain=False, next_q=False):
         """Tile 0 of the current item (stream parity u): S(0) into set u when the wave uses
-        it, its mask, and m = its row max (first pass) or S(0) from the start values -m
-        (fixed_m: the exact pass after an overflow); one barrier (the first body's requests
+        it, its mask, and m = its row max; one barrier (the first body's requests
         overwrite K buffer u; drain: every DMA of this wave done before it, for the prologue,
         whose K(1) and V(0) may still be in flight); the loads of the next item's Q
         (prefetch); then the first body.  next_q: the item's Q is still in the next-item
@@ -731,8 +812,7 @@ class Body:
         p.branch(f"s_cbranch_scc0 .Lsm_{sfx}", [("scc", 0)], skip_xdl=ACC)
         self.stage_mask(u, S_IT)
         p.label(f".Lsm_{sfx}")
-        if not fixed_m:
-            self.row_max_set_m(u)
+        self.row_max_set_m(u)
         if next_q:
             p.branch(f"s_branch .Lsj_{sfx}", skip_xdl=ACC)
         p.label(f".Lsn_{sfx}")
@@ -837,32 +917,6 @@ class Body:
                 p.vmem_store(f"buffer_store_dwordx4 {vr(R, 4)}, {vr(OOS + qb * 8 + i)}, {sr(S_RQ, 4)}, 0 offen nt",
                              V(R, 4) + V(OOS + qb * 8 + i) + S(S_RQ, 4))
 
-    def overflow_vote(self, sfx):
-        """Each wave: flag = any row's per-tile partial sum not below 65504 (a P overflowed
-        fp16); the workgroup's OR of the four flags -> SCC (after a barrier)."""
-        p, s = self.p, self.s
-        C0, C1, F = S_TMP, S_TMP + 2, S_TMP + 4
-        p.valu(f"v_mov_b32_e32 {vr(V_T + 2)}, 0x477fe000", [], V(V_T + 2))
-        for qb, c in ((0, C0), (1, C1)):
-            p.valu(f"v_cmp_gt_f32_e64 {sr(c, 2)}, {vr(V_T + 2)}, {vr(V_LMAX + qb)}", V(V_T + 2) + V(V_LMAX + qb), S(c, 2))
-        s(f"s_and_b64 {sr(C0, 2)}, {sr(C0, 2)}, {sr(C1, 2)}", S(C0, 2) + S(C1, 2), S(C0, 2))
-        s(f"s_andn2_b64 {sr(C0, 2)}, exec, {sr(C0, 2)}", S(C0, 2) + [("exec", 0)], S(C0, 2))
-        s(f"s_cmp_lg_u64 {sr(C0, 2)}, 0", S(C0, 2), [("scc", 0)])
-        s(f"s_cselect_b32 {sr(F)}, 1, 0", [("scc", 0)], S(F))
-        s(f"s_lshl_b32 {sr(F + 1)}, {sr(S_WAVE)}, 2", S(S_WAVE), S(F + 1))
-        s(f"s_add_u32 {sr(F + 1)}, {sr(F + 1)}, {LDS_FLAG}", S(F + 1), S(F + 1))
-        p.valu(f"v_mov_b32_e32 {vr(V_T)}, {sr(F)}", S(F), V(V_T))
-        p.valu(f"v_mov_b32_e32 {vr(V_T + 1)}, {sr(F + 1)}", S(F + 1), V(V_T + 1))
-        p.ds_write(f"ds_write_b32 {vr(V_T + 1)}, {vr(V_T)}", V(V_T + 1) + V(V_T))
-        p.waitcnt(lgkm=0)
-        p.barrier()
-        p.valu(f"v_mov_b32_e32 {vr(V_T)}, {LDS_FLAG}", [], V(V_T))
-        p.ds_read(f"ds_read_b128 {vr(V_P, 4)}, {vr(V_T)}", V(V_P, 4), V(V_T))
-        p.valu(f"v_or_b32_e32 {vr(V_P)}, {vr(V_P)}, {vr(V_P + 1)}", V(V_P, 2), V(V_P))
-        p.valu(f"v_or3_b32 {vr(V_P)}, {vr(V_P)}, {vr(V_P + 2)}, {vr(V_P + 3)}", V(V_P, 4), V(V_P))
-        p.readlane(f"v_readfirstlane_b32 {sr(F)}, {vr(V_P)}", V(V_P), S(F))
-        s(f"s_cmp_lg_u32 {sr(F)}, 0", S(F), [("scc", 0)])
-
 
 def build(check_ldb: int = 12288) -> str:
     p = Prog()
@@ -907,8 +961,9 @@ def build(check_ldb: int = 12288) -> str:
     # The wave's Q rows are requested first and K(0) next, so that S(0) waits only for those
     # while K(1) and V(0) are still arriving (every workgroup requests its first rows at once,
     # and HBM serves them roughly in order).
-    for r in (S_KA, S_KD, S_PASS):
+    for r in (S_KA, S_KD):
         sal(f"s_mov_b32 {sr(r)}, 0", [], S(r))
+    sal(f"s_mov_b32 {sr(S_THR)}, {np.float32(RESCALE_LOG2).view(np.uint32):#x}", [], S(S_THR))
     b.item_index(S_KA, S_TMP + 15, S_TMP + 12)
     b.decode_a(S_TMP + 15, "p")
     b.q_loads(S_BA, S_HA, S_Q0, A_Q)                         # 16 loads
@@ -917,13 +972,11 @@ def build(check_ldb: int = 12288) -> str:
     b.reset_acc()
     p.waitcnt(vm=8)                                          # the Q rows, this wave's part of K(0)
     p.barrier()
-    b.start_item(0, "p", False, drain=True)
+    b.start_item(0, "p", drain=True)
     for u in range(2):
         _dispatch(b, u)
     for u in range(2):
         _boundary(b, u)
-    for u in range(2):
-        _redo(b, u)
     p.label(".Lexit")
     p.waitcnt(vm=0, lgkm=0)
     p.emit("s_endpgm", BRANCH)
@@ -966,18 +1019,13 @@ def _dispatch(b: Body, u: int):
 
 
 def _boundary(b: Body, u: int):
-    """End of the current item (the next tile has stream parity u): overflow vote (first
-    pass), O and LSE out, then the next item (or stop): its Q, S(0) from K buffer u."""
+    """End of the current item (the next tile has stream parity u): O and LSE out, then the
+    next item (or stop): its Q, S(0) from K buffer u."""
     p, s = b.p, b.s
     I = S_TMP + 15
     p.label(f".Lbnd{u}")
     p.nop(16)
     p.waitcnt(lgkm=0)
-    s(f"s_cmp_eq_u32 {sr(S_PASS)}, 0", S(S_PASS), [("scc", 0)])
-    p.branch(f"s_cbranch_scc0 .Lnov{u}", [("scc", 0)], skip_xdl=ACC)
-    b.overflow_vote(f"b{u}")
-    p.branch(f"s_cbranch_scc1 .Lredo{u}", [("scc", 0)], skip_xdl=ACC)
-    p.label(f".Lnov{u}")
     b.epilogue()
     s(f"s_add_u32 {sr(S_KA)}, {sr(S_KA)}, 1", S(S_KA), S(S_KA))
     b.item_index(S_KA, I, S_TMP + 12)
@@ -985,65 +1033,7 @@ def _boundary(b: Body, u: int):
     p.branch("s_cbranch_scc1 .Lexit", [("scc", 0)], skip_xdl=ACC)
     p.comment("next q")
     b.decode_a(I, f"b{u}")
-    s(f"s_mov_b32 {sr(S_PASS)}, 0", [], S(S_PASS))
-    b.start_item(u, f"b{u}", False, next_q=True)
-
-
-def _redo(b: Body, u: int):
-    """Some P of the item overflowed fp16: exact row max over the item's keys (K tiles
-    through K buffer 0, one at a time), then the stream rewound to the item's first tile
-    and the item repeated with m fixed (the stream then runs on into the next item)."""
-    p, s = b.p, b.s
-    KBA, T = S_TMP + 16, S_TMP + 18
-    p.label(f".Lredo{u}")
-    p.waitcnt(vm=0)
-    p.barrier()
-    # K row 0 of the item's kv head
-    T0, COL, LO, HI = S_TMP + 12, S_TMP + 13, S_TMP + 14, S_TMP + 15
-    s(f"s_mul_i32 {sr(T0)}, {sr(S_BA)}, {sr(S_SEQ)}", S(S_BA) + S(S_SEQ), S(T0))
-    s(f"s_add_u32 {sr(COL)}, {sr(S_HQ)}, {sr(S_KVHA)}", S(S_HQ) + S(S_KVHA), S(COL))
-    s(f"s_lshl_b32 {sr(COL)}, {sr(COL)}, 8", S(COL), S(COL))
-    b.add64(KBA, S_QKV, T0, S_LDB, COL, LO, HI)
-    MX = (V_P, V_P + 1)
-    for m_ in MX:
-        p.valu(f"v_mov_b32_e32 {vr(m_)}, {vr(V_NINF)}", V(V_NINF), V(m_))
-    s(f"s_mov_b32 {sr(T)}, 0", [], S(T))
-    p.label(f".Lx{u}")
-    s(f"s_cmp_ge_u32 {sr(T)}, {sr(S_NT)}", S(T) + S(S_NT), [("scc", 0)])
-    p.branch(f"s_cbranch_scc1 .Lxd{u}", [("scc", 0)], skip_xdl=ACC)
-    b.rsrc_tile(S_RK, KBA, T, S_KVEND, S_TMP)
-    b.dma_tile(S_RK, LDS_K[0])
-    p.waitcnt(vm=0)
-    p.barrier()
-    s(f"s_cmp_lt_u32 {sr(T)}, {sr(S_ACTEND)}", S(T) + S(S_ACTEND), [("scc", 0)])
-    p.branch(f"s_cbranch_scc0 .Lxs{u}", [("scc", 0)], skip_xdl=ACC)
-    b.stage_s(0, LDS_K[0])
-    s(f"s_cmp_lt_u32 {sr(T)}, {sr(S_MASKB)}", S(T) + S(S_MASKB), [("scc", 0)])
-    p.branch(f"s_cbranch_scc1 .Lxn{u}", [("scc", 0)], skip_xdl=ACC)
-    b.stage_mask(0, T)
-    p.label(f".Lxn{u}")
-    b.tile_max_into(0, MX)
-    p.label(f".Lxs{u}")
-    p.waitcnt(lgkm=0)
-    p.barrier()
-    s(f"s_add_u32 {sr(T)}, {sr(T)}, 1", S(T), S(T))
-    p.branch(f"s_branch .Lx{u}", skip_xdl=ACC)
-    p.label(f".Lxd{u}")
-    for qb in range(2):
-        mx = MX[qb]
-        p.valu(f"v_cmp_eq_f32_e32 vcc, {vr(V_NINF)}, {vr(mx)}", V(V_NINF) + V(mx), [("vcc", 0)])
-        p.valu(f"v_cndmask_b32_e64 {vr(mx)}, {vr(mx)}, 0, vcc", V(mx) + [("vcc", 0)], V(mx))
-        b.set_negm(qb, mx)
-    b.reset_acc()
-    # the stream back to the item's tile 0, its first requests into the buffers of parity u
-    s(f"s_mov_b32 {sr(S_KD)}, {sr(S_KA)}", S(S_KA), S(S_KD))
-    b.decode_d(f"r{u}")
-    b.stream_start(u, f"r{u}")
-    p.waitcnt(vm=0)
-    p.barrier()
-    s(f"s_mov_b32 {sr(S_PASS)}, 1", [], S(S_PASS))
-    s(f"s_mov_b32 {sr(S_IT)}, 0", [], S(S_IT))
-    b.start_item(u, f"r{u}", True, prefetch=False)
+    b.start_item(u, f"b{u}", next_q=True)
 
 
 def main(path: str) -> None:
