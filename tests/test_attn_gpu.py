@@ -271,31 +271,36 @@ def test_deterministic(gpu):
 
 @pytest.mark.parametrize("causal,kv_len", [(True, None), (False, None), (False, 450), (True, 450)],
                          ids=["causal", "full", "full-kv450", "causal-kv450"])
-@pytest.mark.parametrize("dtype", ["f16", "bf16"])
-def test_growing_scores_move_m(gpu, causal, kv_len, dtype):
-    """Scores that grow by ~40 nats along the keys: the max from the first tile is stale by
-    far more than the 16-bit range.  The fp16 D = 128 forward raises m and rescales O and the
-    row sums as the scores grow; the HIP forward (bf16) sees a P overflow and recomputes its
-    rows with the exact row max.  With kv_len = 450 the largest scores lie past the visible
+@pytest.mark.parametrize("dtype,D,ramp", [("f16", 128, 40), ("bf16", 128, 40), ("f16", 64, 40),
+                                          ("f16", 128, 90), ("bf16", 128, 90), ("bf16", 64, 90)],
+                         ids=["f16", "bf16", "f16-d64", "f16-steep", "bf16-steep", "bf16-d64-steep"])
+def test_growing_scores_move_m(gpu, causal, kv_len, dtype, D, ramp):
+    """Scores that grow by ~40 or ~90 nats along the keys: the max from the first tile is stale
+    by far more than the fp16 range.  The fp16 D = 128 assembly forward raises m and rescales O
+    and the row sums as the scores grow, before a P can overflow; the HIP forward (fp16 D = 64)
+    sees a tile's packed P overflow, rescales and repeats that tile's exp2; in bf16 the growth
+    stays inside the type's range at 40 nats, and at 90 nats (2^130 over the first tile) the HIP
+    forward moves m when a tile's packed P sum reaches 65504.  With kv_len = 450 the largest
+    scores lie past the visible
     keys, in the masked part of the last tile and beyond: m must follow the visible keys only
     (a rescale from unmasked scores would push every visible P below the fp16 range).  Must
     still match the oracle, and the rescale model (tests/attn_cases.py) must see m move."""
     import torch
     from tokamak_amd import attn
     from attn_cases import fp16_forward_rescales
-    B, S, H, D = 1, 700, 2, 128
+    B, S, H = 1, 700, 2
     rng = np.random.default_rng(7)
     u = rng.standard_normal(D)
     u /= np.linalg.norm(u)
     x = np.zeros((B, S, 3 * H, D), dtype=np.float32)
-    ramp = np.linspace(0.0, 1.0, S)
+    lin = np.linspace(0.0, 1.0, S)
     for h in range(H):
         x[0, :, h] = 8.0 * u + 0.3 * rng.standard_normal((S, D))                      # Q
-        x[0, :, H + h] = (ramp[:, None] * 40.0 * np.sqrt(D) / 8.0) * u \
+        x[0, :, H + h] = (lin[:, None] * ramp * np.sqrt(D) / 8.0) * u \
             + 0.3 * rng.standard_normal((S, D))                                        # K
         x[0, :, 2 * H + h] = rng.standard_normal((S, D))                               # V
     qkv_r, bits = oracle.round_to(x.reshape(B, S, -1), dtype)
-    log(f"[case] growing scores S{S} {dtype} causal={int(causal)} kv_len={kv_len}")
+    log(f"[case] growing scores S{S} D{D} {dtype} ramp {ramp} causal={int(causal)} kv_len={kv_len}")
     qkv = to_device(bits, dtype, gpu)
     kvl = None if kv_len is None else torch.tensor([kv_len], dtype=torch.int32, device=gpu)
     o, lse = attn.gqa_fwd(qkv, B, S, H, H, D, causal=causal, kv_len=kvl)
@@ -310,11 +315,46 @@ def test_growing_scores_move_m(gpu, causal, kv_len, dtype):
     if kv_len is not None:
         sc[:, kv_len:] = -np.inf
     assert float((sc.max(axis=1) - sc[:, :64].max(axis=1)).max()) > 20.0
-    if kv_len is None:
+    if kv_len is None and D == 128:
         tested, rescaled, _ = fp16_forward_rescales(qkv_r, B, S, H, H, D, causal)
         log(f"    rescale model: {rescaled} of {tested} (wave, tile) steps move m")
         assert rescaled > 0
     res = [compare("O", from_device(o), o_ref, TOL_FWD), compare("LSE", from_device(lse), lse_ref, TOL_FWD)]
+    for st in res:
+        log(f"    {st['name']}: max_abs={st['max_abs']:.3e} bad={st['n_bad']}")
+    _assert_ok(res)
+
+
+@pytest.mark.parametrize("dtype,D", [("bf16", 64), ("bf16", 128), ("f16", 64), ("f16", 128)])
+def test_single_key_jump_keeps_o_finite(gpu, dtype, D):
+    """One key whose score is 2^126 above every earlier score (87.3 nats) and whose V row is
+    8: P V reaches 2^129, past fp32, while a bf16 P of 2^126 and a lane's row sum stay finite.
+    The HIP forward must move m before that tile's PV product (it does when a lane's packed P
+    sum reaches 65504; an earlier bound at infinity left O infinite, which a bf16 training
+    run of BASELINE config 4's decoder hit), and the assembly forward (fp16 D = 128) when the
+    score exceeds m by 15 log2 units.  Rows from the key on then take O = V of that key."""
+    import torch
+    from tokamak_amd import attn
+    B, S, H, j = 1, 256, 2, 100
+    rng = np.random.default_rng(3)
+    u = rng.standard_normal(D)
+    u /= np.linalg.norm(u)
+    x = np.zeros((B, S, 3 * H, D), dtype=np.float32)
+    for h in range(H):
+        x[0, :, h] = 8.0 * u                                                            # Q
+        x[0, :, H + h] = 0.05 * rng.standard_normal((S, D))                             # K
+        x[0, j, H + h] = (87.3 * np.sqrt(D) / 8.0) * u
+        x[0, :, 2 * H + h] = rng.standard_normal((S, D))                                # V
+        x[0, j, 2 * H + h] = 8.0
+    qkv_r, bits = oracle.round_to(x.reshape(B, S, -1), dtype)
+    log(f"[case] single key jump S{S} D{D} {dtype}")
+    qkv = to_device(bits, dtype, gpu)
+    o, lse = attn.gqa_fwd(qkv, B, S, H, H, D, causal=True)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = oracle.fwd(qkv_r, B, S, H, H, D, causal=True, f64=True)
+    got = from_device(o)
+    assert np.all(np.isfinite(got)) and np.all(np.isfinite(from_device(lse)))
+    res = [compare("O", got, o_ref, TOL_FWD), compare("LSE", from_device(lse), lse_ref, TOL_FWD)]
     for st in res:
         log(f"    {st['name']}: max_abs={st['max_abs']:.3e} bad={st['n_bad']}")
     _assert_ok(res)

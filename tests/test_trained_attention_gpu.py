@@ -1,23 +1,27 @@
 """The attention kernels on trained weights (GPU).
 
-The fp16 D = 128 forward starts each row's softmax offset m at the row maximum of the item's
-first 64-key tile and raises it only when a later tile has a score more than RESCALE_LOG2 = 15
-log2 units above it (a lazy rescale of O and the row sums, tokamak_amd/asmgen/attn_fwd.py).  Random
-N(0,1) inputs never rescale; trained attention that singles out a far key does.  This test trains tests/golden/models/induction.tkm
-(two layers, GQA 4:2, head dim 128, causal, fp16) on an induction task -- the second half of
-every sequence repeats the first, so the loss of the second half can only fall through
-attention to the key half a sequence back -- and then, on each attention layer's actual input
-rows:
+The forwards start each row's softmax offset m at the row maximum of the first 64-key tile and
+move it only when they must: the fp16 D = 128 assembly forward when a later tile has a score
+more than RESCALE_LOG2 = 15 log2 units above m (tokamak_amd/asmgen/attn_fwd.py), the HIP
+forward (D = 64, bf16) when a tile's packed P overflows its 16-bit type
+(tokamak_amd/csrc/attn_fwd.hip); both then rescale O and the row sums.  Random N(0,1) inputs
+never do; trained attention that singles out a far key does.  This test trains, with the
+runtime, tests/golden/models/induction.tkm (two layers, GQA 4:2, head dim 128, causal, fp16)
+and BASELINE config 4's decoder (tests/golden/models/cfg4_llama.tkm: 8 heads of 64, causal,
+in fp16 and in bf16) on an induction task -- the second half of every sequence repeats the
+first, so the loss of the second half can only fall through attention to the key half a
+sequence back -- and then, on the actual input rows of its attention layers (all of the
+induction model's, the first and last of config 4's):
 
 - counts the (wave, tile) steps whose test moves m, by evaluating the kernel's own test on the
   CPU (scores (q . k) * scale * log2 e in fp32, m from the first tile, raised per wave), and
   reports the largest growth of a row's score over its first-tile maximum;
 - checks the forward against the CPU oracle with the plain bar;
-- checks the backward on the oracle's state (its O rounded to fp16 and its LSE, the inputs
+- checks the backward on the oracle's state (its O rounded to 16 bits and its LSE, the inputs
   tkm_attn_bwd receives) against the oracle's backward, and the backward on the GPU forward's
   own O and LSE against the oracle's backward on that same state.  Both use the plain bar
   widened by 16-bit rounding in a cancelling sum, atol + rtol |r| + 4 u sqrt(sum of the
-  element's squared terms), u = 2^-11: a trained head that puts nearly all of a row's weight
+  element's squared terms), u = 2^-11 (fp16) or 2^-8 (bf16): a trained head that puts nearly all of a row's weight
   on one key makes dS_ij = P_ij (dP_ij - O_i . dO_i) cancel, and the fp16 rounding of dS
   before its GEMM (tkm_gpu.cu:552 rounds it too) is then of the order of the bar.  The chain
   is not compared with the oracle's backward on the oracle's O: there the fp16 store of O
@@ -75,15 +79,24 @@ def _time_fwd(qkv, B, S, Hq, Hkv, D, n=20):
     return (time.perf_counter() - t0) / n * 1e6
 
 
-def test_trained_induction_attention(gpu):
+MODELS = [
+    # name, storage type, vocabulary, steps, learning rate, forward kernel, attention layers checked
+    ("induction", "f16", 256, 600, 0.05, "fwd_asm", None),
+    ("cfg4", "f16", 8192, 300, 0.01, "fwd_hip", (0, -1)),
+    ("cfg4", "bf16", 8192, 300, 0.01, "fwd_hip", (0, -1)),
+]
+
+
+@pytest.mark.parametrize("name,dtype,V,steps,lr,kernel,pick", MODELS, ids=[f"{m[0]}-{m[1]}" for m in MODELS])
+def test_trained_attention(gpu, name, dtype, V, steps, lr, kernel, pick):
     import torch
     from tokamak_amd.asmgen.attn_fwd import RESCALE_LOG2
     from tokamak_amd import attn
     from tokamak_amd import runtime as R
-    buf, js = _fixture("induction")
-    B, S, V = js["batch_size"], js["nodes"][0]["W"], 256
+    buf, js = _fixture(name)
+    B, S = js["batch_size"], js["nodes"][0]["W"]
     C0 = js["nodes"][0]["C"]
-    rt = R.Runtime(buf, token_labels=True, init_seed=3)
+    rt = R.Runtime(buf, dtype=attn.F16 if dtype == "f16" else attn.BF16, token_labels=True, init_seed=3)
     rng = np.random.default_rng(5)
     emb = rng.standard_normal((V, C0)).astype(np.float32)
     half = S // 2
@@ -94,12 +107,11 @@ def test_trained_induction_attention(gpu):
         y = np.concatenate([tok[:, 1:], np.zeros((B, 1), np.int64)], axis=1).astype(np.int32)
         return emb[tok].reshape(-1), y.reshape(-1), tok
 
-    steps = 600
-    log(f"[case] induction.tkm: {steps} training steps, B{B} S{S}")
+    log(f"[case] {name}.tkm {dtype}: {steps} training steps, B{B} S{S}")
     losses = []
     for k in range(steps):
         x, y, _ = batch()
-        losses.append(rt.step(x, y, 0.05 if k < 400 else 0.02))
+        losses.append(rt.step(x, y, lr if k < 2 * steps // 3 else 0.4 * lr))
     log(f"    loss: first {np.mean(losses[:10]):.3f}, last {np.mean(losses[-10:]):.3f} "
         f"(uniform guess {np.log(V):.3f}; the repeated half alone bounds it near {np.log(V) / 2:.3f})")
     assert np.all(np.isfinite(losses)) and np.mean(losses[-10:]) < np.mean(losses[:10]) - 0.5
@@ -107,29 +119,32 @@ def test_trained_induction_attention(gpu):
     x, y, _ = batch()
     rt.step(x, y, 0.0)                       # the activations of one more batch, weights unchanged
     layers = [(i, n) for i, n in enumerate(js["nodes"]) if n["op"] == OP_GQA and not n["dead"]]
-    assert len(layers) == 2
+    if pick is not None:
+        layers = [layers[i] for i in pick]
     dev = torch.device("cuda:0")
+    u = 2.0 ** -11 if dtype == "f16" else 2.0 ** -8
     for li, (nid, n) in enumerate(layers):
         Hq, Hkv, D = n["q_heads"], n["kv_heads"], n["head_dim"]
         C = (Hq + 2 * Hkv) * D
         bits = _read16(rt.node_device(n["in0"]), B * S * C)
-        xq = oracle.widen(bits, "f16").reshape(B, S, C)
+        xq = oracle.widen(bits, dtype).reshape(B, S, C)
         tested, rescaled, growth = fp16_forward_rescales(xq, B, S, Hq, Hkv, D, bool(n["causal"]))
-        log(f"    layer {li}: {rescaled} of {tested} tested (wave, tile) steps move m; largest score "
-            f"growth over the first tile's maximum {growth:.2f} (log2 units; a move needs {RESCALE_LOG2})")
-        qkv = to_device(bits, "f16", dev)
+        log(f"    layer {li}: largest score growth over the first tile's maximum {growth:.2f} log2 units; "
+            f"the assembly forward's test would move m on {rescaled} of {tested} (wave, tile) steps "
+            f"(threshold {RESCALE_LOG2})")
+        qkv = to_device(bits, dtype, dev)
         o, lse = attn.gqa_fwd(qkv, B, S, Hq, Hkv, D, causal=True)
-        assert attn.last_kernels() == ["fwd_asm"]
+        assert attn.last_kernels() == [kernel]
         dout_f = rng.standard_normal((B, S, Hq * D)).astype(np.float32)
-        dout_r, dout_bits = oracle.round_to(dout_f, "f16")
+        dout_r, dout_bits = oracle.round_to(dout_f, dtype)
         o_ref, l_ref = oracle.fwd(xq, B, S, Hq, Hkv, D, causal=True, f64=True)
         res = [compare("O", from_device(o), o_ref, TOL_FWD), compare("LSE", from_device(lse), l_ref, TOL_FWD)]
         for st in res:
             log(f"      {st['name']:>3}: max_abs={st['max_abs']:.3e} bad={st['n_bad']}/{st['n']}")
         assert not any(st["n_bad"] for st in res)
-        o_st, o_bits = oracle.round_to(o_ref, "f16")
-        dout = to_device(dout_bits, "f16", dev)
-        states = (("oracle state", o_st, l_ref, to_device(o_bits, "f16", dev), torch.from_numpy(np.ascontiguousarray(l_ref, np.float32)).to(dev)),
+        o_st, o_bits = oracle.round_to(o_ref, dtype)
+        dout = to_device(dout_bits, dtype, dev)
+        states = (("oracle state", o_st, l_ref, to_device(o_bits, dtype, dev), torch.from_numpy(np.ascontiguousarray(l_ref, np.float32)).to(dev)),
                   ("forward's state", from_device(o), from_device(lse), o, lse))
         for tag, o_np, l_np, o_dev, l_dev in states:
             dqkv = attn.gqa_bwd(qkv, o_dev, dout, l_dev, B, S, Hq, Hkv, D, causal=True)
@@ -140,12 +155,12 @@ def test_trained_induction_attention(gpu):
                                       split_dqkv(d_ref, B, S, Hq, Hkv, D), rms):
                 st = compare(nm, g_, r_, TOL_BWD)
                 err = np.abs(g_ - r_)
-                worst = float((err / (TOL_BWD[0] + TOL_BWD[1] * np.abs(r_) + 4 * 2.0 ** -11 * m_)).max())
+                worst = float((err / (TOL_BWD[0] + TOL_BWD[1] * np.abs(r_) + 4 * u * m_)).max())
                 log(f"      {nm} on the {tag}: max_abs={err.max():.3e} plain-bar misses={st['n_bad']} "
                     f"worst |g-r|/bound={worst:.3f}")
                 assert worst <= 1.0, (tag, nm, worst)
         t_trained = _time_fwd(qkv, B, S, Hq, Hkv, D)
-        rand = torch.randn((B, S, C), device=dev).half()
+        rand = torch.randn((B, S, C), device=dev).to(qkv.dtype)
         t_rand = _time_fwd(rand, B, S, Hq, Hkv, D)
         log(f"      forward on these rows {t_trained:.1f} us, on random rows of the same shape {t_rand:.1f} us")
     rt.close()

@@ -28,10 +28,11 @@
 // Scores are the unscaled 16-bit products summed in fp32; scale*log2e and -m are applied in
 // fp32 with one FMA per score, P = exp2(fma(s, c, -m)), as the reference's kernel scales in
 // fp32 (a scale folded into Q and rounded to 16 bits would move a score s by up to
-// |s|*2^-12, which trained attention logits turn into errors past the bars).  m is set from
-// the first tile and never moved: rows whose max later grows beyond the 16-bit range (an
-// overflowing P, i.e. a growth of more than 2^15 for fp16) make the workgroup redo its rows
-// with the exact row max from an extra pass.
+// |s|*2^-12, which trained attention logits turn into errors past the bars).  m starts as
+// the row max of the first tile and moves only when it must (a lazy online softmax): when a
+// later tile's packed P sum reaches fp16's largest value (a P past the fp16 range gives an
+// infinite sum), the wave raises m of its rows to max(m, the tile's row max), multiplies O and
+// the row sums by 2^(m_old - m_new) and repeats the tile's exp2 before its PV product.
 // Causal: tiles above the diagonal are neither loaded nor computed, tiles crossing the
 // diagonal (or the kv_len / S edge) are masked, heaviest query blocks are launched first.
 #include <type_traits>
@@ -42,9 +43,13 @@
 
 namespace tkm {
 
+// A lane's packed P sum over a tile at or above this moves m (see softmax_next): fp16's
+// largest finite value, so no P that reaches a PV product exceeds it, in either type.
+constexpr float P_SUM_MAX = 65504.0f;
+
 // KSPLIT = 2 (grids of at most one workgroup per CU): 8 waves in two groups of 4 over the same
 // query rows; group g walks its own half of the block's key tiles through its own buffers, with
-// its own fixed m (and its own exact redo), and group 1 hands (m, l, O) to group 0 through LDS
+// its own m, and group 1 hands (m, l, O) to group 0 through LDS
 // at the end, which merges them (rescaling each side by 2^(m_side - m)) and writes O and LSE.
 // The heaviest causal block then walks half its tiles, at two waves per SIMD.
 template <int D, int DT, int QB, int KSPLIT>
@@ -67,7 +72,6 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
     constexpr int NI = BN / RPI / NW;  // DMA instructions per wave, per tile and tensor
     constexpr int NL = SPL ? PKS : 1;
     __shared__ __attribute__((aligned(1024))) char smem[KSPLIT][2][2][TILEB];  // [group][K, V][buffer]
-    __shared__ int redo;  // set when a P overflowed: recompute with the exact row max
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -253,7 +257,7 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
             mx[qb] = half_max(v);
         }
     };
-    // Tile 0: establishes m (log2 units), which then stays fixed.
+    // The group's first tile: m (log2 units) from its row max.
     auto softmax_first = [&](auto Jc) __attribute__((always_inline)) {
         float mx[QB];
         row_max(Jc, mx);
@@ -264,27 +268,42 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
         }
         stage_exp(Jc, m, lsum);
     };
-    // Later tiles, against the fixed m.  An overflowing P (the row max grew beyond the
-    // 16-bit range) cannot be repaired in place without keeping O in VALU-addressable
-    // registers; the wave flags the workgroup instead, which redoes its rows with the exact
-    // row max (below).  lsum is not used once the flag is set.
+    // Later tiles, against m.  A lane whose packed row sum of the tile reaches P_SUM_MAX (some
+    // P near or past fp16's range, where the fp16 pack gives an infinite sum) makes the wave
+    // raise m of its rows to max(m, the tile's row max), rescale O and the row sums by
+    // 2^(m_old - m_new) (exactly 1 for rows whose m stays) and repeat the tile's exp2 and
+    // packing, all before the tile's PV.  The bound holds for bf16 too: bf16 P would not
+    // overflow until 2^128, but O = sum P V would overflow first.  Inputs whose scores stay
+    // near the first tile's never take that path.
     auto softmax_next = [&](auto Jc) __attribute__((always_inline)) {
         float lt[QB];
         stage_exp(Jc, m, lt);
         bool bad = false;
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            bad |= !(lt[qb] < INFINITY);
-            lsum[qb] += lt[qb];
+        for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] < P_SUM_MAX);
+        if (__builtin_expect(__any(bad), 0)) {
+            float mx[QB];
+            row_max(Jc, mx);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                const float mn = fmaxf(m[qb], mx[qb] * sl2);
+                const float a = fast_exp2(m[qb] - mn);
+                lsum[qb] *= a;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) o[db][qb] *= a;
+                m[qb] = mn;
+            }
+            stage_exp(Jc, m, lt);
         }
-        return bad;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) lsum[qb] += lt[qb];
     };
 
     // Tile loop.  Tile t: S(t), softmax, PV(t), with the DMA of K(t+1) and V(t+1) in flight
     // into the other buffers (K(j), V(j) live in buffers j&1).  The loop is unrolled by two
     // so buffer indices are constants.  The two waves sharing a SIMD (different workgroups)
     // overlap each other's phases.
-    auto iteration = [&](auto Pc, int i, bool fixed) __attribute__((always_inline)) {
+    auto iteration = [&](auto Pc, int i) __attribute__((always_inline)) {
         constexpr int P = decltype(Pc)::value;  // = i & 1
         const int t = tb + i;
         if (t + 1 < te) {
@@ -294,59 +313,22 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
         if (t < te && t < n_act) {
             stage_s(smem[grp][0][P], I0{});
             if (t >= n_plain) stage_mask(t, I0{});
-            bool bad = false;
-            if (t == tb && !fixed) softmax_first(I0{});
-            else bad = softmax_next(I0{});
-            if (__any(bad) && lane == 0) redo = 1;
+            if (t == tb) softmax_first(I0{});
+            else softmax_next(I0{});
             stage_pv(smem[grp][1][P], I0{});
         }
         wait_dma();
         __syncthreads();
     };
-    auto main_loop = [&](bool fixed) __attribute__((always_inline)) {
-        if (tb < te) {
-            issue(tb, 0, 0);
-            issue(tb, 1, 0);
-        }
-        wait_dma();
-        __syncthreads();
-        for (int i = 0; i < nit; i += 2) {
-            iteration(I0{}, i, fixed);
-            if (i + 1 < nit) iteration(I1{}, i + 1, fixed);
-        }
-    };
-
-    if (tid == 0) redo = 0;
-    main_loop(false);
-    if (redo) {
-        // Exact path (rare): pass 1 computes the row max over all visible keys, pass 2
-        // repeats the main loop with m fixed to it (every P <= 1, nothing can overflow).
-        float mx[QB];
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) mx[qb] = -INFINITY;
-        for (int i = 0; i < nit; ++i) {
-            const int t = tb + i;
-            if (t < te) issue(t, 0, 0);
-            wait_dma();
-            __syncthreads();
-            if (t < te && t < n_act) {
-                stage_s(smem[grp][0][0], I0{});
-                if (t >= n_plain) stage_mask(t, I0{});
-                float tm[QB];
-                row_max(I0{}, tm);
-#pragma unroll
-                for (int qb = 0; qb < QB; ++qb) mx[qb] = fmaxf(mx[qb], tm[qb] * sl2);
-            }
-            __syncthreads();
-        }
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            m[qb] = (mx[qb] == -INFINITY) ? 0.f : mx[qb];
-            lsum[qb] = 0.f;
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) o[db][qb] = f32x16{};
-        }
-        main_loop(true);
+    if (tb < te) {
+        issue(tb, 0, 0);
+        issue(tb, 1, 0);
+    }
+    wait_dma();
+    __syncthreads();
+    for (int i = 0; i < nit; i += 2) {
+        iteration(I0{}, i);
+        if (i + 1 < nit) iteration(I1{}, i + 1);
     }
 
     if constexpr (KSPLIT == 2) {
