@@ -91,33 +91,39 @@ __global__ __launch_bounds__(256) void fa_bwd_delta_kernel(const uint16_t* __res
 //   dV^T += dO^T P,  dK^T += Q^T dS the P / dS accumulators are the B operands in place,
 //                                  dO^T and Q^T come from transposed LDS reads
 // dK (times scale) and dV are written once; no atomics.
-// KSPLIT = 2 (grids of at most one workgroup per CU): 8 waves in two groups of 4 over the same
-// keys; group g walks every other query tile of the key block's list through its own buffers
-// (its waves load the same K; group 0 moves the V rows both read), and group 1 adds its dK and
-// dV accumulators into group 0's through LDS before group 0 writes them.
-template <int D, int DT, int KSPLIT>
-__global__ __launch_bounds__(256 * KSPLIT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// KSPLIT = 2 (small grids): two groups of NW waves over the same keys; group g walks every
+// other query tile of the key block's list through its own buffers (its waves load the same
+// K; group 0 moves the V rows both read), and group 1 adds its dK and dV accumulators into
+// group 0's through LDS before group 0 writes them.  NW = 4: blocks of 128 keys (one
+// workgroup of 8 waves per CU).  NW = 2 (causal): blocks of 64 keys, two workgroups of 4 waves
+// per CU, numbered so that the workgroups the dispatcher puts on one CU (blocks i and
+// i + grid/2) pair a heavy (early) key block with a light one.
+template <int D, int DT, int KSPLIT, int NW = 4>
+__global__ __launch_bounds__(64 * NW * KSPLIT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ dout,
                         const float* __restrict__ lse, const float* __restrict__ delta,
                         uint16_t* __restrict__ dqkv, const int32_t* __restrict__ kv_len, int B,
                         int S, int Hq, int Hkv, float scale, float sl2, int causal) {
-    constexpr int BN = 128, BM = 32;
+    constexpr int BN = 32 * NW, BM = 32;
     constexpr int KS = D / 16;    // k-steps over the head dim (S, dP)
     constexpr int NDB = D / 32;   // 32-wide head-dim blocks of dK, dV
     constexpr int PKS = BM / 16;  // k-steps over queries (dK, dV)
     constexpr int ROWB = D * 2, CPR = D / 8, TILEB = BM * ROWB;
     constexpr int RPI = 64 / CPR;     // rows per DMA instruction
-    constexpr int NI = BM / RPI / 4;  // DMA instructions per wave, per tile and tensor
+    constexpr int NI = BM / RPI / NW;  // DMA instructions per wave, per tile and tensor
     __shared__ __attribute__((aligned(1024))) char smem[KSPLIT][2][2][TILEB];  // [group][buffer][Q, dO]
-    __shared__ __attribute__((aligned(1024))) char sV[4][32 * ROWB];   // V rows of each wave
+    __shared__ __attribute__((aligned(1024))) char sV[NW][32 * ROWB];  // V rows of each wave
     __shared__ __attribute__((aligned(16))) float sLD[KSPLIT][2][2][64];       // [group][buffer][LSE, D]
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-    const int grp = wv >> 2, wave = wv & 3;                    // key-split group, wave in it
+    const int grp = wv / NW, wave = wv % NW;                   // key-split group, wave in it
     const int l32 = lane & 31, hi = lane >> 5;
     const int nh = B * Hkv;
-    const int kblk = blockIdx.x / nh;  // ascending key block = most query tiles first (causal)
+    // ascending key block = most query tiles first (causal); NW = 2: the heavy half ascending,
+    // then the light half from the last block down
+    const int n_kblk = (S + BN - 1) / BN, kq = blockIdx.x / nh, n_heavy = (n_kblk + 1) / 2;
+    const int kblk = (NW == 2 && causal && kq >= n_heavy) ? n_kblk - 1 - (kq - n_heavy) : kq;
     const int bh = blockIdx.x % nh, b = bh / Hkv, kvh = bh % Hkv;
     const int g = Hq / Hkv;
     const size_t ld = (size_t)(Hq + 2 * Hkv) * D, ldo = (size_t)Hq * D;
@@ -282,10 +288,10 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
     if constexpr (KSPLIT == 2) {
         // Group 1's dK^T then dV^T accumulators into group 0's, through the Q/dO buffers (free
         // once the last iteration ended with every DMA done and a barrier): element r of block
-        // db of wave w's lane at float ((db*16 + r)*4 + w)*64 + lane.
+        // db of wave w's lane at float ((db*16 + r)*NW + w)*64 + lane.
         float* xs = reinterpret_cast<float*>(&smem[0][0][0][0]);
-        static_assert(NDB * 16 * 4 * 64 * 4 <= (int)sizeof(smem), "one accumulator set fits the buffers");
-        auto at = [&](int db, int r) -> float& { return xs[((db * 16 + r) * 4 + wave) * 64 + lane]; };
+        static_assert(NDB * 16 * NW * 64 * 4 <= (int)sizeof(smem), "one accumulator set fits the buffers");
+        auto at = [&](int db, int r) -> float& { return xs[((db * 16 + r) * NW + wave) * 64 + lane]; };
 #pragma unroll
         for (int pass = 0; pass < 2; ++pass) {
             f32x16(&acc)[NDB] = pass ? dv : dk;
@@ -562,7 +568,19 @@ static int launch_dkdv_t(const BwdArgs& a) {
     const int n_kblk = (a.S + BN - 1) / BN;
     const long long n_wg = (long long)a.B * a.Hkv * n_kblk;
     dim3 grid((unsigned)n_wg);
-    // At most one workgroup per CU: split each key block's query tiles over two groups of waves.
+    // At most one workgroup of 128 keys per CU: split each key block's query tiles over two
+    // groups of waves.  Causal D = 64: blocks of 64 keys instead, two workgroups per CU
+    // (2 x 48 KB of LDS) pairing heavy and light key blocks.
+    if constexpr (D == 64) {
+        if (n_wg <= compute_units_bwd() && a.causal) {
+            dim3 grid64((unsigned)((long long)a.B * a.Hkv * ((a.S + 63) / 64)));
+            hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, DT, 2, 2>), grid64, dim3(256), 0, (hipStream_t)a.stream,
+                               (const uint16_t*)a.qkv, (const uint16_t*)a.dout, a.lse, (const float*)a.delta,
+                               (uint16_t*)a.dqkv, a.kv_len, a.B, a.S, a.Hq, a.Hkv, a.scale,
+                               a.scale * 1.4426950408889634f, a.causal);
+            return hipGetLastError() == hipSuccess ? 0 : -1;
+        }
+    }
     if (n_wg <= compute_units_bwd())
         hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, DT, 2>), grid, dim3(512), 0, (hipStream_t)a.stream,
                            (const uint16_t*)a.qkv, (const uint16_t*)a.dout, a.lse, (const float*)a.delta,

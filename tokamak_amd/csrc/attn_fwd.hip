@@ -47,18 +47,19 @@ namespace tkm {
 // largest finite value, so no P that reaches a PV product exceeds it, in either type.
 constexpr float P_SUM_MAX = 65504.0f;
 
-// KSPLIT = 2 (grids of at most one workgroup per CU): 8 waves in two groups of 4 over the same
-// query rows; group g walks its own half of the block's key tiles through its own buffers, with
-// its own m, and group 1 hands (m, l, O) to group 0 through LDS
-// at the end, which merges them (rescaling each side by 2^(m_side - m)) and writes O and LSE.
-// The heaviest causal block then walks half its tiles, at two waves per SIMD.
-template <int D, int DT, int QB, int KSPLIT>
-__global__ __launch_bounds__(256 * KSPLIT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// KSPLIT = 2 (small grids): two groups of NW waves over the same query rows; group g walks its
+// own half of the block's key tiles through its own buffers, with its own m, and group 1 hands
+// (m, l, O) to group 0 through LDS at the end, which merges them (rescaling each side by
+// 2^(m_side - m)) and writes O and LSE.  The heaviest causal block then walks half its tiles.
+// NW = 4: blocks of 128 rows (one workgroup of 8 waves per CU).  NW = 2 (causal): blocks of 64
+// rows, two workgroups of 4 waves per CU, numbered so that the workgroups the dispatcher puts
+// on one CU (blocks i and i + grid/2) pair a heavy block with a light one.
+template <int D, int DT, int QB, int KSPLIT, int NW = 4>
+__global__ __launch_bounds__(64 * NW * KSPLIT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
                    float* __restrict__ lse, const int32_t* __restrict__ kv_len, int B, int S,
                    int Hq, int Hkv, float sl2, int causal, int n_qblk) {
     constexpr bool SPL = Split<DT>::on;   // bf16: P as hi + lo
-    constexpr int NW = 4;                 // waves per group (two workgroups, or one of two groups, per CU)
     constexpr int WR = 32 * QB;           // query rows per wave
     constexpr int BM = NW * WR, BN = 64;
     constexpr int KS = D / 16;    // k-steps over the head dim (S^T)
@@ -75,11 +76,15 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-    const int grp = wave >> 2, gw = wave & 3;                    // key-split group, wave in it
+    const int grp = wave / NW, gw = wave % NW;                   // key-split group, wave in it
     const int l32 = lane & 31, hi = lane >> 5;
     const int nh = B * Hq;
     const int bid = blockIdx.x;
-    const int qblk = causal ? (n_qblk - 1 - bid / nh) : (bid / nh);
+    // causal: heaviest blocks first, or (NW = 2) the heavy half descending, then the light half
+    // ascending, so that blocks i and i + grid/2 carry about the same number of tiles together
+    const int kq = bid / nh, n_heavy = (n_qblk + 1) / 2;
+    const int qblk = !causal ? kq
+                   : (NW == 2 ? (kq < n_heavy ? n_qblk - 1 - kq : kq - n_heavy) : n_qblk - 1 - kq);
     const int bh = bid % nh, b = bh / Hq, h = bh % Hq;
     const int kvh = h / (Hq / Hkv);
     const size_t ld = (size_t)(Hq + 2 * Hkv) * D;
@@ -334,11 +339,11 @@ void fa_fwd_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ out,
     if constexpr (KSPLIT == 2) {
         // Group 1's m, partial row sums and O^T accumulators to group 0 (the buffers are free:
         // the last iteration ended with every DMA done and a barrier).  Element j of the
-        // state of wave gw's lane sits at float (j*4 + gw)*64 + lane.
+        // state of wave gw's lane sits at float (j*NW + gw)*64 + lane.
         constexpr int NV = QB * (2 + NDB * 16);
         float* xs = reinterpret_cast<float*>(&smem[0][0][0][0]);
-        static_assert(NV * 4 * 64 * 4 <= (int)sizeof(smem), "merge state fits the tile buffers");
-        auto at = [&](int j) -> float& { return xs[(j * 4 + gw) * 64 + lane]; };
+        static_assert(NV * NW * 64 * 4 <= (int)sizeof(smem), "merge state fits the tile buffers");
+        auto at = [&](int j) -> float& { return xs[(j * NW + gw) * 64 + lane]; };
         if (grp == 1) {
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
@@ -415,8 +420,21 @@ static int launch_fwd_t(const FwdArgs& a) {
     const int n_qblk = (a.S + BM - 1) / BM;
     const long long n_wg = (long long)a.B * a.Hq * n_qblk;
     dim3 grid((unsigned)n_wg);
-    // At most one workgroup per CU: split each block's keys over two groups of waves (the
-    // critical causal block walks half its tiles, and every SIMD holds two waves).
+    // At most one workgroup of 128 rows per CU: split each block's keys over two groups of
+    // waves (the critical causal block walks half its tiles, and every SIMD holds two waves).
+    // Causal D = 64: blocks of 64 rows instead, two workgroups per CU (2 x 64 KB of LDS)
+    // pairing heavy and light blocks, so that no CU holds more than about the mean number of
+    // tiles.  (At D = 128 two such workgroups would need 256 KB of LDS.)
+    if constexpr (D == 64) {
+        if (n_wg <= compute_units() && a.causal) {
+            const int n_qblk64 = (a.S + 63) / 64;
+            dim3 grid64((unsigned)((long long)a.B * a.Hq * n_qblk64));
+            hipLaunchKernelGGL((fa_fwd_kernel<D, DT, QB, 2, 2>), grid64, dim3(256), 0, (hipStream_t)a.stream,
+                               (const uint16_t*)a.qkv, (uint16_t*)a.o, a.lse, a.kv_len, a.B, a.S, a.Hq,
+                               a.Hkv, a.scale * 1.4426950408889634f, a.causal, n_qblk64);
+            return hipGetLastError() == hipSuccess ? 0 : -1;
+        }
+    }
     if (n_wg <= compute_units()) {
         hipLaunchKernelGGL((fa_fwd_kernel<D, DT, QB, 2>), grid, dim3(512), 0, (hipStream_t)a.stream,
                            (const uint16_t*)a.qkv, (uint16_t*)a.o, a.lse, a.kv_len, a.B, a.S, a.Hq,
