@@ -341,26 +341,34 @@ void fa_bwd_dkdv_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __rest
 //   dS^T = P^T (dP^T - D),  dQ^T += K^T dS^T  (K^T from transposed LDS reads)
 // WD: D of the wave's rows is computed here (fp32 sum of O * dO over the lane pair that holds
 // the row) and written to delta instead of read from it.
-template <int D, int DT, bool WD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// KSPLIT = 2, NW = 2 (causal D = 64, small grids): blocks of 64 queries, two groups of two
+// waves over the same rows, group g walking its half of the key tiles through its own
+// buffers (both form D from the O rows; group 0 writes it); group 1 adds its dQ accumulators
+// into group 0's through LDS.  Two workgroups per CU, numbered so that blocks i and
+// i + grid/2 pair a heavy (late) query block with a light one.
+template <int D, int DT, bool WD, int KSPLIT = 1, int NW = 4>
+__global__ __launch_bounds__(64 * NW * KSPLIT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ o,
                       const uint16_t* __restrict__ dout, const float* __restrict__ lse,
                       float* __restrict__ delta, float* __restrict__ quads,
                       uint16_t* __restrict__ dqkv,
                       const int32_t* __restrict__ kv_len, int B, int S, int Hq, int Hkv,
                       float scale, float sl2, int causal, int n_qblk) {
-    constexpr int BM = 128, BN = 64;
+    constexpr int BM = 32 * NW, BN = 64;
     constexpr int KS = D / 16, NKB = BN / 32, NDB = D / 32, PKS = BN / 16;
     constexpr int ROWB = D * 2, CPR = D / 8, TILEB = BN * ROWB;
-    constexpr int RPI = 64 / CPR, NI = BN / RPI / 4;
-    __shared__ __attribute__((aligned(1024))) char smem[2][2][TILEB];  // [buffer][K, V]
+    constexpr int RPI = 64 / CPR, NI = BN / RPI / NW;
+    __shared__ __attribute__((aligned(1024))) char smem[KSPLIT][2][2][TILEB];  // [group][buffer][K, V]
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+    const int grp = wv / NW, wave = wv % NW;                   // key-split group, wave in it
     const int l32 = lane & 31, hi = lane >> 5;
     const int nh = B * Hq;
     const int bid = blockIdx.x;
-    const int qblk = causal ? (n_qblk - 1 - bid / nh) : (bid / nh);
+    const int kq = bid / nh, n_heavy = (n_qblk + 1) / 2;
+    const int qblk = !causal ? kq
+                   : (NW == 2 ? (kq < n_heavy ? n_qblk - 1 - kq : kq - n_heavy) : n_qblk - 1 - kq);
     const int bh = bid % nh, b = bh / Hq, h = bh % Hq;
     const int kvh = h / (Hq / Hkv);
     const size_t ld = (size_t)(Hq + 2 * Hkv) * D, ldo = (size_t)Hq * D;
@@ -408,9 +416,9 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
             }
         }
         Dl = acc + xor32(acc);
-        if (q < S && hi == 0) delta[li] = Dl;
+        if (q < S && hi == 0 && grp == 0) delta[li] = Dl;
         const int SP = (S + 31) & ~31;
-        if (q < SP && hi == 0) {  // rows S..SP-1: zeros (nl2 = Dl = 0 there)
+        if (q < SP && hi == 0 && grp == 0) {  // rows S..SP-1: zeros (nl2 = Dl = 0 there)
             float* qd = quads + row_tile_index((size_t)b * Hq + h, SP, q);
             qd[0] = nl2;
             qd[32] = -Dl;
@@ -420,6 +428,9 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
     int kv_end = kvl;
     if (causal) kv_end = min(kv_end, qblk * BM + BM);
     const int ntiles = (kv_end + BN - 1) / BN;
+    // this group's tiles [tb, te); every group runs nit iterations (barriers stay matched)
+    const int nit = KSPLIT == 2 ? (ntiles + 1) / 2 : ntiles;
+    const int tb = grp == 0 ? 0 : nit, te = grp == 0 ? nit : ntiles;
 
     const int dma_r = lane / CPR, dma_p = lane % CPR;
     auto issue = [&](int t, int buf) __attribute__((always_inline)) {
@@ -431,8 +442,8 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
         for (int i = 0; i < NI; ++i) {
             const int r0 = (wave * NI + i) * RPI, r = r0 + dma_r;
             const uint32_t voff = (uint32_t)r * ldb + (uint32_t)((dma_p ^ swz<D>(r)) << 4);
-            dma16(rk, &smem[buf][0][r0 * ROWB], voff);
-            dma16(rv, &smem[buf][1][r0 * ROWB], voff);
+            dma16(rk, &smem[grp][buf][0][r0 * ROWB], voff);
+            dma16(rv, &smem[grp][buf][1][r0 * ROWB], voff);
         }
     };
     const int fk = swz<D>(l32);
@@ -443,18 +454,19 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
 #pragma unroll
     for (int db = 0; db < NDB; ++db) dq[db] = f32x16{};
 
-    if (ntiles > 0) issue(0, 0);
+    if (tb < te) issue(tb, 0);
     wait_dma();
     __syncthreads();
 
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
+    for (int i = 0; i < nit; ++i) {
+        const int t = tb + i;
+        const int buf = i & 1;
         const int k0 = t * BN;
-        if (t + 1 < ntiles) issue(t + 1, buf ^ 1);
-        const bool active = !causal || (k0 <= q0 + 31);
+        if (t + 1 < te) issue(t + 1, buf ^ 1);
+        const bool active = t < te && (!causal || (k0 <= q0 + 31));
         if (active) {
-            const char* kt = smem[buf][0];
-            const char* vt = smem[buf][1];
+            const char* kt = smem[grp][buf][0];
+            const char* vt = smem[grp][buf][1];
             f32x16 s[NKB], dp[NKB];
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb) s[kb] = dp[kb] = f32x16{};
@@ -516,27 +528,54 @@ void fa_bwd_dq_kernel(const uint16_t* __restrict__ qkv, const uint16_t* __restri
         __syncthreads();
     }
 
+    if constexpr (KSPLIT == 2) {
+        // Group 1's dQ^T accumulators into group 0's through the K/V buffers (free after the
+        // loop's last barrier): element r of block db of wave w's lane at float
+        // ((db*16 + r)*NW + w)*64 + lane.
+        float* xs = reinterpret_cast<float*>(&smem[0][0][0][0]);
+        static_assert(NDB * 16 * NW * 64 * 4 <= (int)sizeof(smem), "one accumulator set fits the buffers");
+        auto at = [&](int db, int r) -> float& { return xs[((db * 16 + r) * NW + wave) * 64 + lane]; };
+        if (grp == 1) {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) at(db, r) = dq[db][r];
+        }
+        __syncthreads();
+        if (grp == 0) {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) dq[db][r] += at(db, r);
+        }
+        __syncthreads();
+    }
+
     // dQ (times scale) leaves through LDS: a lane holds query q, d = db*32 + g4*8 + hi*4 + 0..3;
     // the wave's rows go to LDS row-major (rows padded by 16 bytes against bank conflicts, the
     // K/V tiles are free after the loop's last barrier) and come back 16 bytes per lane, so
     // each store writes whole rows instead of 8 bytes in each of 32 rows.
     constexpr int SROW = ROWB + 16, RPP = 64 / CPR;  // staging row bytes; rows per pass
-    char* stg = &smem[0][0][0] + wave * 32 * SROW;
+    char* stg = &smem[0][0][0][0] + wave * 32 * SROW;
+    if (grp == 0) {  // (KSPLIT = 2: group 1's sums are in group 0's accumulators)
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+        for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-            u32x2 w = {pack2<DT>(dq[db][g4 * 4 + 0] * scale, dq[db][g4 * 4 + 1] * scale),
-                       pack2<DT>(dq[db][g4 * 4 + 2] * scale, dq[db][g4 * 4 + 3] * scale)};
-            *reinterpret_cast<u32x2*>(stg + l32 * SROW + (db * 4 + g4) * 16 + hi * 8) = w;
-        }
+            for (int g4 = 0; g4 < 4; ++g4) {
+                u32x2 w = {pack2<DT>(dq[db][g4 * 4 + 0] * scale, dq[db][g4 * 4 + 1] * scale),
+                           pack2<DT>(dq[db][g4 * 4 + 2] * scale, dq[db][g4 * 4 + 3] * scale)};
+                *reinterpret_cast<u32x2*>(stg + l32 * SROW + (db * 4 + g4) * 16 + hi * 8) = w;
+            }
+    }
     __syncthreads();
+    if (grp == 0) {
 #pragma unroll
-    for (int i = 0; i < 32 / RPP; ++i) {
-        const int row = i * RPP + lane / CPR, chunk = lane % CPR;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * SROW + chunk * 16);
-        if (q0 + row < S)
-            *reinterpret_cast<u32x4*>(dqkv + ((size_t)b * S + q0 + row) * ld + (size_t)h * D + chunk * 8) = v;
+        for (int i = 0; i < 32 / RPP; ++i) {
+            const int row = i * RPP + lane / CPR, chunk = lane % CPR;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * SROW + chunk * 16);
+            if (q0 + row < S)
+                *reinterpret_cast<u32x4*>(dqkv + ((size_t)b * S + q0 + row) * ld + (size_t)h * D + chunk * 8) = v;
+        }
     }
 }
 
@@ -598,6 +637,19 @@ template <int D, int DT, bool WD>
 static int launch_dq_t(const BwdArgs& a) {
     constexpr int BM = 128;
     const int n_qblk = (a.S + BM - 1) / BM;
+    // Causal D = 64 with at most one 128-row block per CU: 64-row blocks over two groups of
+    // two waves (each walks half the key tiles), two workgroups per CU pairing heavy and light.
+    if constexpr (D == 64) {
+        if (a.causal && (long long)a.B * a.Hq * n_qblk <= compute_units_bwd()) {
+            const int n_qblk64 = (a.S + 63) / 64;
+            hipLaunchKernelGGL((fa_bwd_dq_kernel<D, DT, WD, 2, 2>), dim3((unsigned)(a.B * a.Hq * n_qblk64)),
+                               dim3(256), 0, (hipStream_t)a.stream,
+                               (const uint16_t*)a.qkv, (const uint16_t*)a.o, (const uint16_t*)a.dout, a.lse,
+                               a.delta, a.ld, (uint16_t*)a.dqkv, a.kv_len, a.B, a.S, a.Hq, a.Hkv, a.scale,
+                               a.scale * 1.4426950408889634f, a.causal, n_qblk64);
+            return hipGetLastError() == hipSuccess ? 0 : -1;
+        }
+    }
     dim3 grid((unsigned)(a.B * a.Hq * n_qblk)), block(256);
     hipLaunchKernelGGL((fa_bwd_dq_kernel<D, DT, WD>), grid, block, 0, (hipStream_t)a.stream,
                        (const uint16_t*)a.qkv, (const uint16_t*)a.o, (const uint16_t*)a.dout, a.lse,
