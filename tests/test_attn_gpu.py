@@ -325,6 +325,30 @@ def test_growing_scores_move_m(gpu, causal, kv_len, dtype, D, ramp):
     _assert_ok(res)
 
 
+def test_growing_scores_many_items(gpu):
+    """Growing scores at config 3's size with GQA (B4 Hq16 Hkv4 S2048 D128, fp16, causal):
+    512 work items over the persistent workgroups, so each walks several items in which m
+    moves, through the DMA stream that runs across items.  Forward and backward against the
+    oracle."""
+    B, S, Hq, Hkv, D = 4, 2048, 16, 4, 128
+    u = np.random.default_rng(11).standard_normal(D).astype(np.float32)
+    u /= np.linalg.norm(u)
+    lin = np.linspace(0.0, 1.0, S, dtype=np.float32)
+
+    def grow(q, k, v):
+        q = (0.3 * q.reshape(B, S, Hq, D) + 8.0 * u).reshape(B, S, Hq * D)
+        k = (0.3 * k.reshape(B, S, Hkv, D) + (lin[None, :, None, None] * 40.0 * np.sqrt(D) / 8.0) * u)
+        return q, k.reshape(B, S, Hkv * D).astype(np.float32), v
+
+    from attn_cases import fp16_forward_rescales
+    x = oracle.make_inputs(B, S, Hq, Hkv, D, "f16", seed_qkv=21, with_dout=False, transform=grow)["qkv"]
+    x = x.reshape(B, S, Hq + 2 * Hkv, D)[:1, :, [0, Hq, Hq + Hkv]]       # batch 0, q-head 0 and its K, V
+    tested, rescaled, growth = fp16_forward_rescales(x, 1, S, 1, 1, D, True)
+    log(f"    head 0: m moves on {rescaled} of {tested} (wave, tile) steps; growth {growth:.1f} log2 units")
+    assert rescaled > 0
+    _assert_ok(run_gpu_case(gpu, B, S, Hq, Hkv, D, dtype="f16", causal=True, seed=21, transform=grow))
+
+
 @pytest.mark.parametrize("dtype,D", [("bf16", 64), ("bf16", 128), ("f16", 64), ("f16", 128)])
 def test_single_key_jump_keeps_o_finite(gpu, dtype, D):
     """One key whose score is 2^126 above every earlier score (87.3 nats) and whose V row is
