@@ -7,14 +7,16 @@
 //   (!causal || j <= i).
 //
 // Work decomposition: one workgroup = 4 waves = one (batch, q-head, block of 128 query
-// rows); two workgroups share a CU (2 waves per SIMD).  Each wave keeps its 32 query rows
+// rows); two workgroups share a CU (2 waves per SIMD).  Small grids split a block's key tiles
+// over two groups of waves, and causal D = 64 takes blocks of 64 rows paired heavy with light
+// on a CU (fa_fwd_kernel's KSPLIT and NW below).  Each wave keeps its 32 query rows
 // of Q in registers and walks the key range in tiles of 64 keys that the workgroup moves
 // HBM -> LDS by buffer DMA (rows past the valid range read as zero), stored row-major with
 // an XOR chunk swizzle.
 //
 // Per tile and wave:
 //   S^T = K Q^T        32 keys x 32 queries per MFMA block; lane = query row.
-//   P^T = exp2(S^T * scale*log2e - m) with m the running row max (log2 units); the row sum
+//   P^T = exp2(S^T * scale*log2e - m) with m the row offset (log2 units, below); the row sum
 //                      is an fp32 dot of the rounded P per lane, lane halves combined at the
 //                      end.
 //   O^T += V^T P^T     the P^T accumulator, rounded to 16 bits, is the B operand in place;
