@@ -69,6 +69,9 @@ def parse():
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters of a profiling run)")
+    ap.add_argument("--flush-mib", type=int, default=512,
+                    help="cold-cache figure after the timed region: each step preceded by a write "
+                         "of this many MiB (more than the 256 MB Infinity Cache); 0 skips it")
     return ap.parse_args()
 
 
@@ -619,6 +622,27 @@ def main():
         torch.cuda.synchronize()
         kernel_path[name] = attn.last_kernels()
 
+    # Cold cache: the inputs (config 3: qkv, O, dO, LSE, about 168 MB) fit in the 256 MB
+    # Infinity Cache, so the figure above runs on whatever it holds.  Here every step follows a
+    # write of flush_mib MiB.  No event sits between the flush and the step (an event between
+    # two kernels idles the GPU for several us): K (flush + step) and K flushes alone are each
+    # timed as one region, and the step's cold time is their difference over K.
+    cold = None
+    if args.flush_mib and not use_graph:
+        junk = torch.empty(args.flush_mib << 20, dtype=torch.uint8, device=dev)
+
+        def flush():
+            junk.fill_(7)
+        all_fns = [fn for _, fn in stages]
+        timed([flush] + all_fns, 2)
+        with_ms = timed([flush] + all_fns, K)[0]
+        flush_ms = timed([flush], K)[0]
+        cold_ms = (with_ms - flush_ms) / K
+        cold = {"flush_mib": args.flush_mib, "ms_per_step": round(cold_ms, 5),
+                "tflops": None, "flush_ms": round(flush_ms / K, 5),
+                "method": "(K x (flush + step) - K x flush) / K, each one timed region"}
+        del junk
+
     f_fwd = attn.attention_flops(B, S, Hq, D, causal, kv_len, "fwd")
     f_total = f_fwd * (3.5 if backward else 1.0)
     # Algorithmic FLOPs credited to each kernel (sums to F_fwd + 2.5 F_fwd):
@@ -653,6 +677,8 @@ def main():
                 "avg_ms": round(dom_avg, 5)}
 
     value = f_total / (ms_step * 1e-3) / 1e12
+    if cold is not None:
+        cold["tflops"] = round(f_total / (cold["ms_per_step"] * 1e-3) / 1e12, 2)
     fwd_ms = per["attn_fwd"]
     res = {
         "metric": METRIC if args.config == "cfg3" else f"FlashAttn TFLOP/s ({args.config})",
@@ -678,6 +704,7 @@ def main():
         "timed_as": "one replay of a captured hipGraph of the K steps" if use_graph else "eager launches",
         "kernel_path": kernel_path,
         "roofline": roof,
+        "cold_cache": cold,
         "wall_s": round(wall, 3),
     }
     if not args.no_cpu_baseline:

@@ -38,6 +38,10 @@ def test_bench_line_contract():
     assert ro["kernel"] in d["kernels"] and isinstance(ro["traffic"], (int, float))
     assert "profiles/attn_cfg3_traffic.md" in ro["traffic_source"]
     assert d["kernel_path"] == {"attn_fwd": ["fwd_asm"], "bwd_dq": ["dq_asm"], "bwd_dkdv": ["dkdv_asm"]}
+    # cold cache: a separate figure after the timed region, never the value
+    cc = d["cold_cache"]
+    assert cc["flush_mib"] == 512 and cc["ms_per_step"] > 0 and cc["flush_ms"] > 0
+    assert cc["tflops"] == pytest.approx(flops / (cc["ms_per_step"] * 1e-3) / 1e12, rel=2e-3)
     cb = d["cpu_baseline"]
     assert cb["kind"] == "port" and cb["unit"] == "TFLOP/s" and cb["value"] > 0
     assert 1 <= cb["cores"] <= 16 and cb["sample"]
