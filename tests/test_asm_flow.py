@@ -25,8 +25,9 @@ def reciprocal(d, limit):
 _lines = {}
 
 
-def fwd_lines():
-    if "fwd" not in _lines:
+def fwd_lines(dt="f16"):
+    key = "fwd-" + dt
+    if key not in _lines:
         captured = []
         orig = gfx950.Prog.finalize
 
@@ -36,14 +37,14 @@ def fwd_lines():
             return out
         gfx950.Prog.finalize = finalize
         try:
-            attn_fwd.build()
+            attn_fwd.build(dt=dt)
         finally:
             gfx950.Prog.finalize = orig
-        _lines["fwd"] = captured[-1]
-    return _lines["fwd"]
+        _lines[key] = captured[-1]
+    return _lines[key]
 
 
-def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, vcmp_lanes=M64):
+def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, vcmp_lanes=M64, dt="f16"):
     n_qblk = (S + 255) // 256
     bhq, G = B * Hq, Hq // Hkv
     n_items = n_qblk * bhq
@@ -122,7 +123,7 @@ def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, vcmp_lanes=M64):
                 raise Fail(f"next-item Q loads of another head: {sorted({base for _, base in loads})}")
             checked[0] += 1
 
-    sim = Sim(fwd_lines(), args, mem, kv, n_wg, expect, on_event, vcmp_lanes=vcmp_lanes, max_steps=8_000_000)
+    sim = Sim(fwd_lines(dt), args, mem, kv, n_wg, expect, on_event, vcmp_lanes=vcmp_lanes, max_steps=8_000_000)
     sim.run()
     want = {(b, h, 256 * z + 64 * wv) for b in range(B) for h in range(Hq) for z in range(n_qblk) for wv in range(4)}
     assert set(stored) == want and all(c == 1 for c in stored.values()), \
@@ -149,6 +150,17 @@ def run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, vcmp_lanes=M64):
 ])
 def test_fwd_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg):
     run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg)
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", [
+    (2, 700, 4, 2, True, None, 5),
+    (2, 1000, 2, 2, False, [1000, 333], 3),
+    (1, 512, 4, 2, True, None, 8),
+])
+def test_fwd_bf16_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg):
+    """The bf16 kernel (96-slot bodies, P in two halves) has the fp16 kernel's scalar flow."""
+    run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, dt="bf16")
+    run_fwd(B, S, Hq, Hkv, causal, kv_len, n_wg, vcmp_lanes=0, dt="bf16")
 
 
 def test_fwd_scalar_flow_without_rescale():
@@ -400,7 +412,7 @@ def test_descriptors_end_at_the_tensor_end(monkeypatch, gen):
         self.s(f"s_mul_i32 {gfx950.sr(dst)}, {gfx950.sr(rows)}, {gfx950.sr(stride)}",
                gfx950.S(rows) + gfx950.S(stride), gfx950.S(dst))
     monkeypatch.setattr(mod.Body, "nrec_rows", whole_rows)
-    key = "fwd" if gen == "fwd" else mod.NAME
+    key = "fwd-f16" if gen == "fwd" else mod.NAME
     good = _lines.pop(key)
     try:
         # (the forward's tile check, which compares each K/V tile's descriptor with the

@@ -11,10 +11,25 @@ import pytest
 from tokamak_amd import build as tb
 from tokamak_amd.asmgen import attn_dkdv, attn_dq, attn_fwd, gfx950
 
+class Gen:
+    """A generator with its element type: build() gives that kernel's text."""
+
+    def __init__(self, mod, dt):
+        self.mod, self.dt = mod, dt
+
+    def build(self):
+        return self.mod.build() if self.dt == "f16" else self.mod.build(dt=self.dt)
+
+    def __repr__(self):
+        return f"{self.mod.__name__.split('.')[-1]}-{self.dt}"
+
+
 # (generator, workgroup-id SGPRs, registers defined on entry: the kernel arguments)
-KERNELS = [(attn_fwd, (1, 0, 0), {("s", 8 + i) for i in range(24)}),
-           (attn_dkdv, (1, 0, 0), {("s", 8 + i) for i in range(24)} | {("s", 90), ("s", 91)}),
-           (attn_dq, (1, 0, 0), {("s", 8 + i) for i in range(34)})]
+KERNELS = [(Gen(attn_fwd, "f16"), (1, 0, 0), {("s", 8 + i) for i in range(24)}),
+           (Gen(attn_fwd, "bf16"), (1, 0, 0), {("s", 8 + i) for i in range(24)}),
+           (Gen(attn_dkdv, "f16"), (1, 0, 0), {("s", 8 + i) for i in range(24)} | {("s", 90), ("s", 91)}),
+           (Gen(attn_dq, "f16"), (1, 0, 0), {("s", 8 + i) for i in range(34)})]
+IDS = [repr(k[0]) for k in KERNELS]
 
 
 def _program(gen):
@@ -34,7 +49,7 @@ def _program(gen):
     return captured[-1], text
 
 
-@pytest.mark.parametrize("gen,wg_ids,kernargs", KERNELS, ids=lambda x: getattr(x, "NAME", ""))
+@pytest.mark.parametrize("gen,wg_ids,kernargs", KERNELS, ids=IDS)
 def test_no_read_before_write(gen, wg_ids, kernargs):
     prog, _ = _program(gen)
     defined = {("s", 0), ("s", 1), ("v", 0), ("exec", 0)}
@@ -50,7 +65,7 @@ def test_no_read_before_write(gen, wg_ids, kernargs):
     assert not undefined, undefined[:10]
 
 
-@pytest.mark.parametrize("gen,wg_ids,kernargs", KERNELS, ids=lambda x: getattr(x, "NAME", ""))
+@pytest.mark.parametrize("gen,wg_ids,kernargs", KERNELS, ids=IDS)
 def test_assembles(gen, wg_ids, kernargs):
     try:
         clang = tb.llvm_tool("clang")
@@ -110,7 +125,7 @@ def _dead_loads(prog):
     return bad
 
 
-@pytest.mark.parametrize("gen,wg_ids,kernargs", KERNELS, ids=lambda x: getattr(x, "NAME", ""))
+@pytest.mark.parametrize("gen,wg_ids,kernargs", KERNELS, ids=IDS)
 def test_no_dead_loads(gen, wg_ids, kernargs):
     prog, _ = _program(gen)
     bad = _dead_loads(prog)
@@ -121,5 +136,5 @@ def test_dead_load_check_catches_register_reuse(monkeypatch):
     """Six row reads in flight into four rotating registers (the lookahead above the number
     of read registers): the check must flag it."""
     monkeypatch.setattr(attn_dq, "LK", 6)
-    prog, _ = _program(attn_dq)
+    prog, _ = _program(Gen(attn_dq, "f16"))
     assert _dead_loads(prog)

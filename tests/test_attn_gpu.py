@@ -276,11 +276,11 @@ def test_deterministic(gpu):
                          ids=["f16", "bf16", "f16-d64", "f16-steep", "bf16-steep", "bf16-d64-steep"])
 def test_growing_scores_move_m(gpu, causal, kv_len, dtype, D, ramp):
     """Scores that grow by ~40 or ~90 nats along the keys: the max from the first tile is stale
-    by far more than the fp16 range.  The fp16 D = 128 assembly forward raises m and rescales O
-    and the row sums as the scores grow, before a P can overflow; the HIP forward (fp16 D = 64)
-    sees a tile's packed P overflow, rescales and repeats that tile's exp2; in bf16 the growth
-    stays inside the type's range at 40 nats, and at 90 nats (2^130 over the first tile) the HIP
-    forward moves m when a tile's packed P sum reaches 65504.  With kv_len = 450 the largest
+    by far more than the fp16 range.  The D = 128 assembly forwards (fp16 and bf16) raise m
+    and rescale O and the row sums as the scores grow, before a P can pass 2^15; the HIP
+    forward (D = 64) sees a tile's packed P overflow (fp16), or a tile's packed P sum reach
+    65504 (bf16, where a growth of 40 nats stays inside the type's range and 90 nats, 2^130
+    over the first tile, does not), rescales and repeats that tile's exp2.  With kv_len = 450 the largest
     scores lie past the visible
     keys, in the masked part of the last tile and beyond: m must follow the visible keys only
     (a rescale from unmasked scores would push every visible P below the fp16 range).  Must
@@ -355,8 +355,9 @@ def test_single_key_jump_keeps_o_finite(gpu, dtype, D):
     8: P V reaches 2^129, past fp32, while a bf16 P of 2^126 and a lane's row sum stay finite.
     The HIP forward must move m before that tile's PV product (it does when a lane's packed P
     sum reaches 65504; an earlier bound at infinity left O infinite, which a bf16 training
-    run of BASELINE config 4's decoder hit), and the assembly forward (fp16 D = 128) when the
-    score exceeds m by 15 log2 units.  Rows from the key on then take O = V of that key."""
+    run of BASELINE config 4's decoder hit), and the assembly forwards (D = 128, fp16 and
+    bf16) when the score exceeds m by 15 log2 units.  Rows from the key on then take O = V of
+    that key."""
     import torch
     from tokamak_amd import attn
     B, S, H, j = 1, 256, 2, 100
@@ -528,16 +529,16 @@ def test_backward_on_forward_state(gpu, B, S, Hq, Hkv, D, dtype, causal, kv_len,
 
 def test_kernel_paths(gpu):
     """Which kernels each configuration runs (tkm_attn_last_kernels): fp16 D=128 -- the
-    config-3 hot path -- takes the three gfx950 assembly kernels, and only it; bf16 and D=64
-    take the HIP kernels.  tkm_attn_init loads the code objects (the runtime calls it before
-    capturing a step)."""
+    config-3 hot path -- takes the three gfx950 assembly kernels; bf16 D=128 the assembly
+    forward and the HIP backward; D=64 the HIP kernels.  tkm_attn_init loads the code objects
+    (the runtime calls it before capturing a step)."""
     import torch
     from tokamak_amd import attn
     attn.init()
     assert attn.asm_available()
     B, S, Hq, Hkv = 1, 300, 4, 2
     cases = [(128, torch.float16, ["fwd_asm"], ["dq_asm", "dkdv_asm"]),
-             (128, torch.bfloat16, ["fwd_hip"], ["dq_hip", "dkdv_hip"]),
+             (128, torch.bfloat16, ["fwd_asm"], ["dq_hip", "dkdv_hip"]),
              (64, torch.float16, ["fwd_hip"], ["dq_hip", "dkdv_hip"]),
              (64, torch.bfloat16, ["fwd_hip"], ["dq_hip", "dkdv_hip"])]
     for D, dt, k_fwd, k_bwd in cases:

@@ -53,7 +53,7 @@ from .attn_dkdv import split_scalar
 from .common import Lanes, lane_basics, row_read_offsets, swz, tr_read_offsets, xcd_slot
 from .gfx950 import A, BRANCH, PERMLANE, Prog, S, V, ar, kernel_text, sr, vr
 
-NAME = "tkm_fa_fwd_d128_f16"
+NAME = "tkm_fa_fwd_d128_f16"        # the bf16 kernel: tkm_fa_fwd_d128_bf16 (build(dt="bf16"))
 D = 128
 ROWB = D * 2            # bytes per K/V row in LDS
 TILE = 64 * ROWB        # one 64-key tile
@@ -74,6 +74,15 @@ RESCALE_LOG2 = 15.0     # m moves when a score exceeds it by more than this (P <
 MAX_SLOTS = tuple(range(17, 33)) + tuple(range(44, 60))
 TEST_SLOT = 61
 MFMA = "v_mfma_f32_32x32x16_f16"
+MFMA_OF = {"f16": MFMA, "bf16": "v_mfma_f32_32x32x16_bf16"}
+PACK_OF = {"f16": "v_cvt_pk_f16_f32", "bf16": "v_cvt_pk_bf16_f32"}
+# bf16: P goes to the PV MFMAs as two bf16 halves, hi = bf16(P) and lo = bf16(P - hi) (about 16
+# significant bits; 8-bit P alone misses the O tolerance on rows with few keys), so every PV
+# step is two MFMAs on the same V operand and a body has 96 slots: S(t+1) in 0..31, PV in
+# 32..95 (k-step ks at 32 + 16ks), softmax step n at floor(5n/2).  The lo words of P[qb][ks]
+# go into the first four registers of the eight scores they come from (step w of the block
+# writes register w after steps 0..w-1 have read registers 0..2w-1), which the next S MFMAs
+# into that set overwrite only in the next body.
 
 # kernel arguments (byte offsets in the kernarg segment): qkv, out, lse, kv_len, then
 # S, Hq, Hkv, sl2, causal, n_qblk, ldb, ldo, group, n_wg, n_items, B*Hq and the reciprocals
@@ -104,6 +113,7 @@ V_NEGM = 128            # -m of the lane's row in log2 units, per qb
 V_MX = 130              # the lane's max unscaled score of the next tile, per qb
 V_RT = 132              # rescale temporaries (2)
 V_P = 160               # P[qb][ks] at 160 + (qb*4+ks)*4
+V_SPL = 134             # bf16: split temporaries (4)
 V_KBUF = 192
 V_VBUF = V_KBUF + 4 * NKB
 V_KOFF = V_VBUF + 4 * NVB   # 8
@@ -134,8 +144,12 @@ def sblk(J, kb, qb):
 
 
 class Body:
-    def __init__(self, p: Prog):
+    def __init__(self, p: Prog, dt: str = "f16"):
         self.p = p
+        self.dt = dt
+        self.mfma_op = MFMA_OF[dt]
+        self.pack_op = PACK_OF[dt]
+        self.split = dt == "bf16"
 
     def s(self, text, reads=(), writes=()):
         self.p.salu(text, reads, writes)
@@ -407,13 +421,22 @@ class Body:
         kb, ks = ri // 8, ri % 8
         dst = sblk(J, kb, qb)
         c = None if ks == 0 else dst
-        self.p.mfma(MFMA, dst, V_KBUF + (ri % NKB) * 4, qbase + (qb * 8 + ks) * 4, c, b_acc=True)
+        self.p.mfma(self.mfma_op, dst, V_KBUF + (ri % NKB) * 4, qbase + (qb * 8 + ks) * 4, c, b_acc=True)
 
-    def pv_mfma(self, j):
-        vi, qb = j // 2, j % 2
+    def pv_per_read(self):
+        """PV MFMAs per V operand read: one per block of 32 rows, twice with the bf16 split."""
+        return 4 if self.split else 2
+
+    def pv_mfma(self, j, J):
+        """PV MFMA j of set J's tile: V read vi = j // pv_per_read(), rows qb = j % 2; bf16:
+        hi (P) for j % 4 < 2, then lo (the residual, in set J's score registers), so that the
+        two MFMAs into one accumulator have another between them."""
+        n = self.pv_per_read()
+        vi, qb, lo = j // n, j % 2, (j % n) >= 2
         ks, db = vi // 4, vi % 4
         o = A_O + (db * 2 + qb) * 16
-        self.p.mfma(MFMA, o, V_VBUF + (vi % NVB) * 4, V_P + (qb * 4 + ks) * 4, o, dst_acc=True)
+        b = sblk(J, ks // 2, qb) + (ks % 2) * 8 if lo else V_P + (qb * 4 + ks) * 4
+        self.p.mfma(self.mfma_op, o, V_VBUF + (vi % NVB) * 4, b, o, dst_acc=True)
 
     # ---- softmax steps (n = 0..31), k-step major: step n covers P[qb][ks] word w with
     #      ks = n // 8, qb = (n % 8) // 4, w = n % 4, i.e. scores r0 + 2w, r0 + 2w + 1 of block
@@ -440,13 +463,23 @@ class Body:
     def sm_pack(self, J, n):
         x0, qb, ks, w = self.sm_regs(J, n)
         pw = V_P + (qb * 4 + ks) * 4 + w
-        self.p.valu(f"v_cvt_pk_f16_f32 {vr(pw)}, {vr(x0)}, {vr(x0 + 1)}", V(x0, 2), V(pw))
+        p = self.p
+        p.valu(f"{self.pack_op} {vr(pw)}, {vr(x0)}, {vr(x0 + 1)}", V(x0, 2), V(pw))
         for i in range(2):
             lt = V_LT + qb * 2 + i
             if ks == 0 and w == 0:   # first step of this block of rows in the tile
-                self.p.valu(f"v_mov_b32_e32 {vr(lt)}, {vr(x0 + i)}", V(x0 + i), V(lt))
+                p.valu(f"v_mov_b32_e32 {vr(lt)}, {vr(x0 + i)}", V(x0 + i), V(lt))
             else:
-                self.p.valu(f"v_add_f32_e32 {vr(lt)}, {vr(lt)}, {vr(x0 + i)}", V(lt) + V(x0 + i), V(lt))
+                p.valu(f"v_add_f32_e32 {vr(lt)}, {vr(lt)}, {vr(x0 + i)}", V(lt) + V(x0 + i), V(lt))
+        if self.split:
+            # lo = bf16(P - hi): hi's halves as fp32 are its words shifted up / masked
+            t0, t1 = V_SPL + 2 * (n % 2), V_SPL + 2 * (n % 2) + 1
+            pl = x0 - w          # register w of this block of eight scores
+            p.valu(f"v_lshlrev_b32_e32 {vr(t0)}, 16, {vr(pw)}", V(pw), V(t0))
+            p.valu(f"v_and_b32_e32 {vr(t1)}, 0xffff0000, {vr(pw)}", V(pw), V(t1))
+            p.valu(f"v_sub_f32_e32 {vr(x0)}, {vr(x0)}, {vr(t0)}", V(x0) + V(t0), V(x0))
+            p.valu(f"v_sub_f32_e32 {vr(x0 + 1)}, {vr(x0 + 1)}, {vr(t1)}", V(x0 + 1) + V(t1), V(x0 + 1))
+            p.valu(f"v_cvt_pk_bf16_f32 {vr(pl)}, {vr(x0)}, {vr(x0 + 1)}", V(x0, 2), V(pl))
 
     def sm_finish(self, qb):
         """Tile done: row sum += partial sum."""
@@ -551,23 +584,6 @@ class Body:
         for w in range(64):
             self.p.valu(f"v_accvgpr_mov_b32 {ar(A_Q + w)}, {ar(A_QN + w)}", A(A_QN + w), A(A_Q + w))
 
-    def stage_softmax(self, J):
-        for n in range(33):
-            if n < 32:
-                self.sm_exp(J, n)
-            if n >= 1:
-                self.sm_pack(J, n - 1)
-        for qb in range(2):
-            self.sm_finish(qb)
-
-    def stage_pv(self, vbase):
-        issued = 0
-        for j in range(32):
-            while issued < 16 and issued * 2 - LV <= j:
-                self.v_read(issued, vbase)
-                issued += 1
-            self.pv_mfma(j)
-
     def stage_softmax_pv(self, J, vbase):
         """Softmax of set J and O += V P from the V buffer at vbase, interleaved: PV k-step ks
         (MFMAs 8ks .. 8ks+7) needs only P[*][ks] (softmax steps 8ks .. 8ks+7), so the softmax
@@ -576,17 +592,20 @@ class Body:
             self.sm_exp(J, n)
             self.sm_pack(J, n)
         issued = 0
-        for j in range(32):
-            while issued < 16 and issued * 2 - LV <= j:
+        per = self.pv_per_read()
+        fin = (25, 27) if per == 2 else (49, 51)
+        for j in range(16 * per):
+            while issued < 16 and issued * per - LV <= j:
                 self.v_read(issued, vbase)
                 issued += 1
-            self.pv_mfma(j)
-            n = 8 + j            # softmax step of the next k-step, one per MFMA
-            if n < 32:
-                self.sm_exp(J, n)
-                self.sm_pack(J, n)
-            if j in (25, 27):
-                self.sm_finish((j - 25) // 2)
+            self.pv_mfma(j, J)
+            if j % (per // 2) == 0:
+                n = 8 + j // (per // 2)   # softmax step of the next k-step, one per PV k-pair
+                if n < 32:
+                    self.sm_exp(J, n)
+                    self.sm_pack(J, n)
+            if j in fin:
+                self.sm_finish(fin.index(j))
 
     def stage_mask(self, J, tsg):
         """Scores of set J, tile t (SGPR tsg), set to -inf where key > q (causal) or
@@ -655,23 +674,32 @@ class Body:
         follows at TEST_SLOT."""
         Jn = J ^ 1
         kbase, vbase = LDS_K[Jn], LDS_V[J]
+        per = self.pv_per_read()
+        nslot = 32 + 16 * per
         max_at = dict(zip(MAX_SLOTS, self.lane_max_steps(Jn)))
         assert len(max_at) == 32 and max(MAX_SLOTS) < TEST_SLOT < 64
         assert min(k for k, st in max_at.items() if st[2][-1] >= sblk(Jn, 1, 0)) >= 33
         assert min(max_at) >= 17
-        exp_at = {(7 * n) // 4: n for n in range(32)}
-        pack_at = {(7 * n) // 4 + 1: n for n in range(32)}
+        if per == 2:
+            exp_at = {(7 * n) // 4: n for n in range(32)}
+            fin_at = (57, 59)
+        else:
+            exp_at = {(5 * n) // 2: n for n in range(32)}
+            fin_at = (81, 83)
+        pack_at = {e + 1: n for e, n in exp_at.items()}
+        # P[*][ks] (softmax steps 8ks .. 8ks+7) is packed before PV k-step ks, at slot 32 + 8*per*ks
+        assert all(max(e + 1 for e, n in exp_at.items() if n // 8 == ks) < 32 + 8 * per * ks for ks in range(4))
         dma_at = {DMA0 + 4 * i: i for i in range(8)}
         kissued = 0
         while kissued * 2 - LK < 0:
             self.k_read(kissued, kbase)
             kissued += 1
         vissued = 0
-        for s_ in range(64):
+        for s_ in range(nslot):
             while kissued < 16 and kissued * 2 - LK <= s_:
                 self.k_read(kissued, kbase)
                 kissued += 1
-            while vissued < 16 and 32 + vissued * 2 - LV <= s_:
+            while vissued < 16 and 32 + vissued * per - LV <= s_:
                 self.v_read(vissued, vbase)
                 vissued += 1
             if s_ in dma_at:
@@ -680,14 +708,15 @@ class Body:
             if s_ < 32:
                 self.s_mfma(s_, Jn)
             else:
-                self.pv_mfma(s_ - 32)
-                self.p.ins.extend(h[s_ - 32])
+                self.pv_mfma(s_ - 32, J)
+                if s_ - 32 < len(h):
+                    self.p.ins.extend(h[s_ - 32])
             if s_ in exp_at:
                 self.sm_exp(J, exp_at[s_])
             if s_ in pack_at:
                 self.sm_pack(J, pack_at[s_])
-            if s_ in (57, 59):
-                self.sm_finish((s_ - 57) // 2)
+            if s_ in fin_at:
+                self.sm_finish(fin_at.index(s_))
             if s_ in max_at:
                 self.lane_max_step(max_at[s_])
             if s_ == TEST_SLOT:
@@ -907,8 +936,8 @@ class Body:
                         p.valu(f"v_accvgpr_read_b32 {vr(W + j)}, {ar(o + j)}", A(o + j), V(W + j))
                     for j in range(4):
                         p.valu(f"v_mul_f32_e32 {vr(W + j)}, {vr(W + j)}, {vr(INV)}", V(W + j) + V(INV), V(W + j))
-                    p.valu(f"v_cvt_pk_f16_f32 {vr(W + 4)}, {vr(W)}, {vr(W + 1)}", V(W, 2), V(W + 4))
-                    p.valu(f"v_cvt_pk_f16_f32 {vr(W + 5)}, {vr(W + 2)}, {vr(W + 3)}", V(W + 2, 2), V(W + 5))
+                    p.valu(f"{self.pack_op} {vr(W + 4)}, {vr(W)}, {vr(W + 1)}", V(W, 2), V(W + 4))
+                    p.valu(f"{self.pack_op} {vr(W + 5)}, {vr(W + 2)}, {vr(W + 3)}", V(W + 2, 2), V(W + 5))
                     p.ds_write(f"ds_write_b64 {vr(BW)}, {vr(W + 4, 2)} offset:{(db * 4 + g4) * 16}", V(BW) + V(W + 4, 2))
                     W = 8 if W == 16 else 16   # alternate register sets
             for i in range(8):   # LDS operations of a wave complete in order: reads see the rows
@@ -918,9 +947,10 @@ class Body:
                              V(R, 4) + V(OOS + qb * 8 + i) + S(S_RQ, 4))
 
 
-def build(check_ldb: int = 12288) -> str:
+def build(check_ldb: int = 12288, dt: str = "f16") -> str:
+    """The kernel's assembly text: tkm_fa_fwd_d128_f16 (dt "f16") or tkm_fa_fwd_d128_bf16."""
     p = Prog()
-    b = Body(p)
+    b = Body(p, dt)
     sal = p.salu
     # ------------------------------------------------------------------ prologue: scalars
     p.smem(f"s_load_dwordx16 {sr(8, 16)}, {sr(S_KARG, 2)}, 0x0", S(8, 16), S(S_KARG, 2))
@@ -980,8 +1010,12 @@ def build(check_ldb: int = 12288) -> str:
     p.label(".Lexit")
     p.waitcnt(vm=0, lgkm=0)
     p.emit("s_endpgm", BRANCH)
-    return kernel_text(NAME, p.finalize(), lds_bytes=LDS_BYTES, kernarg_bytes=KERNARG_BYTES,
+    return kernel_text(kernel_name(dt), p.finalize(), lds_bytes=LDS_BYTES, kernarg_bytes=KERNARG_BYTES,
                        next_free_sgpr=NEXT_FREE_SGPR, args=ARGS, wg_ids=(1, 0, 0))
+
+
+def kernel_name(dt: str = "f16") -> str:
+    return f"tkm_fa_fwd_d128_{dt}"
 
 
 def _check_lanes(L: Lanes, ldb: int):

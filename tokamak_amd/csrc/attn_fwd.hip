@@ -450,7 +450,7 @@ static int launch_fwd_t(const FwdArgs& a) {
 }
 
 int launch_fwd(const FwdArgs& a) {
-    const int rc = launch_fwd_asm(a);  // D = 128 fp16: hand-scheduled assembly kernel
+    const int rc = launch_fwd_asm(a);  // D = 128 fp16 and bf16: hand-scheduled assembly kernels
     if (rc != 1) {
         if (rc == 0) note_kernels(kFwdAsm);
         return rc;
