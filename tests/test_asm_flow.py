@@ -177,8 +177,8 @@ from tokamak_amd.asmgen import attn_dkdv, attn_dq  # noqa: E402
 O_, DOUT, QUADS, DELTA, DQKV = 0x20000000, 0x30000000, 0x50000000, 0x60000000, 0x80000000
 
 
-def _gen_lines(gen):
-    key = gen.NAME
+def _gen_lines(gen, dt="f16"):
+    key = gen.NAME if dt == "f16" else gen.NAME + "-" + dt
     if key not in _lines:
         captured = []
         orig = gfx950.Prog.finalize
@@ -189,7 +189,7 @@ def _gen_lines(gen):
             return out
         gfx950.Prog.finalize = finalize
         try:
-            gen.build()
+            gen.build() if dt == "f16" else gen.build(dt=dt)
         finally:
             gfx950.Prog.finalize = orig
         _lines[key] = captured[-1]
@@ -205,7 +205,7 @@ def _bwd_mem(B, S, Hq, Hkv, kv):
             "quads": (QUADS, B * Hq * sp * 8, 16, 16), "kv_len": (KVLEN, 4 * B, 4, 4)}
 
 
-def run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg):
+def run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg, dt="f16"):
     n_kblk, bh = (S + 127) // 128, B * Hkv
     n_items = n_kblk * bh
     n_wg = min(n_wg, n_items)
@@ -250,7 +250,7 @@ def run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg):
     for i in range(2):
         reach[attn_dkdv.V_DOFF + i] = tuple((8 * w + 4 * i + 3) * ldb + 255 for w in range(4))
         reach[attn_dkdv.V_DOFF + 2 + i] = tuple((8 * w + 4 * i + 3) * ldo + 255 for w in range(4))
-    sim = Sim(_gen_lines(attn_dkdv), args, _bwd_mem(B, S, Hq, Hkv, kv), kv, n_wg, None, on_event,
+    sim = Sim(_gen_lines(attn_dkdv, dt), args, _bwd_mem(B, S, Hq, Hkv, kv), kv, n_wg, None, on_event,
               wave_vgpr=attn_dkdv.V_PT, lane_max=reach)
     sim.run()
     want = {(b, h, 128 * z + 32 * w) for b in range(B) for h in range(Hkv) for z in range(n_kblk) for w in range(4)}
@@ -322,6 +322,13 @@ BWD_CASES = [(1, 512, 2, 1, True, None, 3), (2, 700, 4, 2, True, None, 5), (2, 7
 # unfixed dK/dV stream advanced one head per request, past the group's last, and read 256
 # bytes past the end of dO
 DKDV_PAST_END = [(1, 6, 4, 2, True, [2], 1), (2, 800, 4, 2, True, None, 8), (3, 131, 4, 2, True, None, 3)]
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", [BWD_CASES[1], BWD_CASES[4], DKDV_PAST_END[0],
+                                                          DKDV_PAST_END[1]])
+def test_dkdv_bf16_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg):
+    """The bf16 kernel (48-slot bodies, P and dS in two halves) has the fp16 kernel's flow."""
+    run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg, dt="bf16")
 
 
 @pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", BWD_CASES + DKDV_PAST_END)

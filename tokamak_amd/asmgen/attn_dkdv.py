@@ -47,6 +47,11 @@ from .gfx950 import A, BRANCH, Prog, S, V, ar, kernel_text, sr, vr
 
 NAME = "tkm_fa_bwd_dkdv_d128_f16"
 MFMA = "v_mfma_f32_32x32x16_f16"
+MFMA_OF = {"f16": MFMA, "bf16": "v_mfma_f32_32x32x16_bf16"}
+PACK_OF = {"f16": "v_cvt_pk_f16_f32", "bf16": "v_cvt_pk_bf16_f32"}
+# bf16 (build(dt="bf16"), tkm_fa_bwd_dkdv_d128_bf16): P and dS go to the dV / dK MFMAs as two
+# bf16 halves each, hi = bf16(x) and lo = bf16(x - hi) (about 16 significant bits), so each
+# transposed read feeds two MFMAs and a body has 48 slots: S/dP in 0..15, dV/dK in 16..47.
 ROWB = 256
 NBUF = 4
 TILE = 32 * ROWB                    # 8 KB: one 32-row tile of Q or dO
@@ -107,6 +112,9 @@ V_TK = V_HI4 + 1        # mask threshold of the current tile
 V_T = V_TK + 1          # temporaries
 V_PT = V_T + 8          # prologue lane scratch (13 registers)
 assert V_PT + 13 <= 256
+V_PL, V_DSL = 212, 220  # bf16: lo halves of P[ks][w], dS[ks][w]
+V_SPL = 228             # bf16: split temporaries (4)
+assert V_PT + 13 <= V_PL and V_SPL + 4 <= 256
 
 # ---- AGPRs
 A_DV, A_DK, A_K, A_V = 0, 64, 128, 160
@@ -159,8 +167,12 @@ def mask_c(r):
 
 
 class Body:
-    def __init__(self, p: Prog):
+    def __init__(self, p: Prog, dt: str = "f16"):
         self.p = p
+        self.dt = dt
+        self.mfma_op = MFMA_OF[dt]
+        self.pack_op = PACK_OF[dt]
+        self.split = dt == "bf16"
 
     def s(self, text, reads=(), writes=()):
         self.p.salu(text, reads, writes)
@@ -277,16 +289,32 @@ class Body:
         dst = V_SD[J] + 16 * which
         c = (None if which == 0 else V_CD) if ks == 0 else dst
         b = (A_K if which == 0 else A_V) + ks * 4
-        self.p.mfma(MFMA, dst, V_RB + (i % NRB) * 4, b, c, b_acc=True)
+        self.p.mfma(self.mfma_op, dst, V_RB + (i % NRB) * 4, b, c, b_acc=True)
 
-    def dvdk_mfma(self, j):
+    def dvdk_mfma(self, j, lo=False):
+        """dV or dK MFMA j (the operand of transposed read j); lo: the bf16 residual half."""
         ks, k8 = j // 8, j % 8
         db = k8 % 4
         if k8 < 4:
-            acc, b = A_DV + db * 16, V_P + ks * 4
+            acc, b = A_DV + db * 16, (V_PL if lo else V_P) + ks * 4
         else:
-            acc, b = A_DK + db * 16, V_DS + ks * 4
-        self.p.mfma(MFMA, acc, V_TB + (j % NTB) * 4, b, acc, dst_acc=True)
+            acc, b = A_DK + db * 16, (V_DSL if lo else V_DS) + ks * 4
+        self.p.mfma(self.mfma_op, acc, V_TB + (j % NTB) * 4, b, acc, dst_acc=True)
+
+    def dvdk_slots(self):
+        """(transposed read j, lo) of each dV/dK slot: j in order for fp16; bf16: for each
+        pair of reads (2a, 2a+1), hi 2a, hi 2a+1, lo 2a, lo 2a+1 (one MFMA between the two
+        into one accumulator)."""
+        if not self.split:
+            return [(j, False) for j in range(16)]
+        return [(4 * (k // 4) // 2 + k % 2, (k // 2) % 2 == 1) for k in range(32)]
+
+    def tr_first_use(self):
+        """Slot offset (from the first dV/dK slot) of each transposed read's first MFMA."""
+        first = {}
+        for k, (j, _) in enumerate(self.dvdk_slots()):
+            first.setdefault(j, k)
+        return [first[j] for j in range(16)]
 
     # ---------------------------------------------------------------- elementwise (set J)
     def ew_exp(self, J, n):
@@ -311,8 +339,17 @@ class Body:
                 p.valu(f"v_cndmask_b32_e64 {vr(x)}, {vr(x)}, 0, vcc", V(x) + [("vcc", 0)], V(x))
             p.valu(f"v_mul_f32_e32 {vr(dp)}, {vr(x)}, {vr(dp)}", V(x) + V(dp), V(dp))
         x, dp = V_SD[J] + 2 * n, V_SD[J] + 16 + 2 * n
-        p.valu(f"v_cvt_pk_f16_f32 {vr(V_P + ks * 4 + w)}, {vr(x)}, {vr(x + 1)}", V(x, 2), V(V_P + ks * 4 + w))
-        p.valu(f"v_cvt_pk_f16_f32 {vr(V_DS + ks * 4 + w)}, {vr(dp)}, {vr(dp + 1)}", V(dp, 2), V(V_DS + ks * 4 + w))
+        for src, hi, lo, t in ((x, V_P, V_PL, V_SPL), (dp, V_DS, V_DSL, V_SPL + 2)):
+            hw = hi + ks * 4 + w
+            p.valu(f"{self.pack_op} {vr(hw)}, {vr(src)}, {vr(src + 1)}", V(src, 2), V(hw))
+            if self.split:
+                # lo = bf16(x - hi): hi's halves as fp32 are its word shifted up / masked
+                p.valu(f"v_lshlrev_b32_e32 {vr(t)}, 16, {vr(hw)}", V(hw), V(t))
+                p.valu(f"v_and_b32_e32 {vr(t + 1)}, 0xffff0000, {vr(hw)}", V(hw), V(t + 1))
+                p.valu(f"v_sub_f32_e32 {vr(src)}, {vr(src)}, {vr(t)}", V(src) + V(t), V(src))
+                p.valu(f"v_sub_f32_e32 {vr(src + 1)}, {vr(src + 1)}, {vr(t + 1)}", V(src + 1) + V(t + 1), V(src + 1))
+                lw = lo + ks * 4 + w
+                p.valu(f"v_cvt_pk_bf16_f32 {vr(lw)}, {vr(src)}, {vr(src + 1)}", V(src, 2), V(lw))
 
     def mask_threshold(self, qt_sgpr):
         """tk = key >= kv_len ? 32 : (causal ? kw0 - qr0 + l32 - 4hi : -96); an element of
@@ -676,8 +713,8 @@ class Body:
                     if scale:
                         for j in range(4):
                             p.valu(f"v_mul_f32_e32 {vr(W + j)}, {sr(S_SCALE)}, {vr(W + j)}", V(W + j) + S(S_SCALE), V(W + j))
-                    p.valu(f"v_cvt_pk_f16_f32 {vr(W + 4)}, {vr(W)}, {vr(W + 1)}", V(W, 2), V(W + 4))
-                    p.valu(f"v_cvt_pk_f16_f32 {vr(W + 5)}, {vr(W + 2)}, {vr(W + 3)}", V(W + 2, 2), V(W + 5))
+                    p.valu(f"{self.pack_op} {vr(W + 4)}, {vr(W)}, {vr(W + 1)}", V(W, 2), V(W + 4))
+                    p.valu(f"{self.pack_op} {vr(W + 5)}, {vr(W + 2)}, {vr(W + 3)}", V(W + 2, 2), V(W + 5))
                     p.ds_write(f"ds_write_b64 {vr(BW)}, {vr(W + 4, 2)} offset:{(db * 4 + g4) * 16}", V(BW) + V(W + 4, 2))
                     W = 8 if W == 0 else 0
             for i in range(8):   # LDS operations of a wave complete in order: reads see the rows
@@ -724,13 +761,16 @@ class Body:
         tissued = 0
         if ew and masked:
             self.mask_threshold(S_QT0)
+        slots = self.dvdk_slots()
+        first = self.tr_first_use()
+        end = 16 + len(slots)
         if sdp:
             for s_ in range(16):
                 while rissued < 16 and rissued - LK <= s_:
                     self.row_read(rissued, jb1)
                     rissued += 1
                 if ew:
-                    while tissued < 16 and 16 + tissued - LV <= s_:
+                    while tissued < 16 and 16 + first[tissued] - LV <= s_:
                         self.tr_read(tissued, jb0)
                         tissued += 1
                 self.sdp_mfma(s_, J1)
@@ -760,19 +800,20 @@ class Body:
         p.barrier()
         # --- second half: dV/dK(it); start values of tile it+2; DMA of tile it+3
         dma_at = {17: 0, 20: 1, 23: 2, 26: 3, 29: 4}
-        for s_ in range(16, 32):
+        for s_ in range(16, end):
             if ew:
-                while tissued < 16 and 16 + tissued - LV <= s_:
+                while tissued < 16 and 16 + first[tissued] - LV <= s_:
                     self.tr_read(tissued, jb0)
                     tissued += 1
             if 16 <= s_ < 24:   # -LSE*log2e of tile it+1 (its exps, next body), -D of tile it+2
                 self.cinit_read(jb1 if s_ < 20 else jb2, s_ - 16)
-            p.ins.extend(h2[s_ - 16])
+            if s_ - 16 < len(h2):
+                p.ins.extend(h2[s_ - 16])
             if s_ in dma_at:
                 which, i = self.DMA_ORDER[dma_at[s_]]
                 self.dma_m0(which, jb3, i)
             if ew:
-                self.dvdk_mfma(s_ - 16)
+                self.dvdk_mfma(*slots[s_ - 16])
                 if EW_SPLIT and s_ < 24:   # pairs n = 4..7, ready for dV/dK MFMA 8 on
                     n = 4 + (s_ - 16) // 2
                     if s_ % 2 == 0:
@@ -782,8 +823,8 @@ class Body:
             if s_ in dma_at:
                 which, i = self.DMA_ORDER[dma_at[s_]]
                 self.dma_ld(which, i)
-            if s_ >= 32 - LK:   # first row reads of tile it+2 for the next body
-                self.row_read(s_ - (32 - LK), jb2)
+            if s_ >= end - LK:   # first row reads of tile it+2 for the next body
+                self.row_read(s_ - (end - LK), jb2)
         # --- into the next body: the common variant directly, else the dispatcher
         un = (u + 1) % 4
         p.salu(f"s_cmp_eq_u32 {sr(S_CODE)}, 6", S(S_CODE), [("scc", 0)])
@@ -791,10 +832,11 @@ class Body:
         p.branch(f"s_branch .Ldisp{un}", keep_lgkm=True, skip_xdl=ACC)
 
 
-def build(check_ldb: int = 12288, check_ldo: int = 4096) -> str:
+def build(check_ldb: int = 12288, check_ldo: int = 4096, dt: str = "f16") -> str:
+    """The kernel's assembly text: tkm_fa_bwd_dkdv_d128_f16 (dt "f16") or _bf16."""
     p = Prog(coalesce_lgkm=True)
     sal = p.salu
-    b = Body(p)
+    b = Body(p, dt)
     # ---------------------------------------------------------------- scalars
     p.smem(f"s_load_dwordx16 {sr(8, 16)}, {sr(0, 2)}, 0x0", S(8, 16), S(0, 2))
     p.smem(f"s_load_dwordx8 {sr(24, 8)}, {sr(0, 2)}, 0x40", S(24, 8), S(0, 2))
@@ -884,7 +926,7 @@ def build(check_ldb: int = 12288, check_ldo: int = 4096) -> str:
     p.label(".Lexit")
     p.waitcnt(vm=0, lgkm=0)   # DMA requests past the last item still write LDS
     p.emit("s_endpgm", BRANCH)
-    return kernel_text(NAME, p.finalize(), lds_bytes=LDS_BYTES, kernarg_bytes=KERNARG_BYTES,
+    return kernel_text(f"tkm_fa_bwd_dkdv_d128_{dt}", p.finalize(), lds_bytes=LDS_BYTES, kernarg_bytes=KERNARG_BYTES,
                        next_free_sgpr=NEXT_FREE_SGPR, args=ARGS, wg_ids=(1, 0, 0))
 
 
