@@ -261,7 +261,7 @@ def run_dkdv(B, S, Hq, Hkv, causal, kv_len, n_wg, dt="f16"):
     return sim
 
 
-def run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d):
+def run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d, dt="f16"):
     n_qblk, bhq, G = (S + 255) // 256, B * Hq, Hq // Hkv
     n_items = n_qblk * bhq
     n_wg = min(n_wg, n_items)
@@ -300,7 +300,7 @@ def run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, compute_d):
             w.loads.clear()
             checked[0] += 1
 
-    sim = Sim(_gen_lines(attn_dq), args, _bwd_mem(B, S, Hq, Hkv, kv), kv, n_wg, None, on_event,
+    sim = Sim(_gen_lines(attn_dq, dt), args, _bwd_mem(B, S, Hq, Hkv, kv), kv, n_wg, None, on_event,
               wave_vgpr=attn_dq.V_PT)
     sim.run()
     want = {(b, h, 256 * z + 64 * w) for b in range(B) for h in range(Hq) for z in range(n_qblk) for w in range(4)}
@@ -340,6 +340,13 @@ def test_dkdv_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg):
     ldb = (Hq + 2 * Hkv) * 256
     heads = {(base - DQKV) % ldb // 256 for _, _, m, base, _ in sim.stores if m}
     assert heads == set(range(Hq, Hq + 2 * Hkv))
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,causal,kv_len,n_wg", [BWD_CASES[1], BWD_CASES[4], BWD_CASES[5]])
+def test_dq_bf16_scalar_flow(B, S, Hq, Hkv, causal, kv_len, n_wg):
+    """The bf16 kernel (64-slot bodies, dS^T in two halves) has the fp16 kernel's flow."""
+    run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, True, dt="bf16")
+    run_dq(B, S, Hq, Hkv, causal, kv_len, n_wg, False, dt="bf16")
 
 
 @pytest.mark.parametrize("compute_d", [True, False])

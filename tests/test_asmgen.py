@@ -29,7 +29,8 @@ KERNELS = [(Gen(attn_fwd, "f16"), (1, 0, 0), {("s", 8 + i) for i in range(24)}),
            (Gen(attn_fwd, "bf16"), (1, 0, 0), {("s", 8 + i) for i in range(24)}),
            (Gen(attn_dkdv, "f16"), (1, 0, 0), {("s", 8 + i) for i in range(24)} | {("s", 90), ("s", 91)}),
            (Gen(attn_dkdv, "bf16"), (1, 0, 0), {("s", 8 + i) for i in range(24)} | {("s", 90), ("s", 91)}),
-           (Gen(attn_dq, "f16"), (1, 0, 0), {("s", 8 + i) for i in range(34)})]
+           (Gen(attn_dq, "f16"), (1, 0, 0), {("s", 8 + i) for i in range(34)}),
+           (Gen(attn_dq, "bf16"), (1, 0, 0), {("s", 8 + i) for i in range(34)})]
 IDS = [repr(k[0]) for k in KERNELS]
 
 

@@ -529,8 +529,8 @@ def test_backward_on_forward_state(gpu, B, S, Hq, Hkv, D, dtype, causal, kv_len,
 
 def test_kernel_paths(gpu):
     """Which kernels each configuration runs (tkm_attn_last_kernels): fp16 D=128 -- the
-    config-3 hot path -- takes the three gfx950 assembly kernels; bf16 D=128 the assembly
-    forward and dK/dV and the HIP dQ; D=64 the HIP kernels.  tkm_attn_init loads the code objects
+    config-3 hot path -- and bf16 D=128 take the three gfx950 assembly kernels; D=64 the HIP
+    kernels.  tkm_attn_init loads the code objects
     (the runtime calls it before capturing a step)."""
     import torch
     from tokamak_amd import attn
@@ -538,7 +538,7 @@ def test_kernel_paths(gpu):
     assert attn.asm_available()
     B, S, Hq, Hkv = 1, 300, 4, 2
     cases = [(128, torch.float16, ["fwd_asm"], ["dq_asm", "dkdv_asm"]),
-             (128, torch.bfloat16, ["fwd_asm"], ["dq_hip", "dkdv_asm"]),
+             (128, torch.bfloat16, ["fwd_asm"], ["dq_asm", "dkdv_asm"]),
              (64, torch.float16, ["fwd_hip"], ["dq_hip", "dkdv_hip"]),
              (64, torch.bfloat16, ["fwd_hip"], ["dq_hip", "dkdv_hip"])]
     for D, dt, k_fwd, k_bwd in cases:

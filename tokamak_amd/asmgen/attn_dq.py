@@ -40,6 +40,14 @@ from .gfx950 import A, BRANCH, PERMLANE, Prog, S, V, ar, kernel_text, sr, vr
 
 NAME = "tkm_fa_bwd_dq_d128_f16"
 MFMA = "v_mfma_f32_32x32x16_f16"
+MFMA_OF = {"f16": MFMA, "bf16": "v_mfma_f32_32x32x16_bf16"}
+PACK_OF = {"f16": "v_cvt_pk_f16_f32", "bf16": "v_cvt_pk_bf16_f32"}
+# bf16 (build(dt="bf16"), tkm_fa_bwd_dq_d128_bf16): dS^T goes to the dQ^T MFMAs as two bf16
+# halves, hi = bf16(dS) in dP^T's registers (as fp16 dS^T) and lo = bf16(dS - hi) in S^T's
+# registers at the same places (word 4ks + w of the block, written after the steps that read
+# registers 0 .. 8ks+2w+1), so each K^T read feeds four MFMAs and a body has 64 slots: S^T/dP^T
+# in 0..31, dQ^T in 32..63.  D sums the products of bf16 O and dO halves (unpacked by shift and
+# mask) in fp32.
 ROWB = 256
 NBUF = 4
 TILE = 32 * ROWB                    # 8 KB: one 32-key tile of K or V
@@ -86,6 +94,8 @@ V_HI4 = V_L32 + 1
 V_TK = V_HI4 + 1        # mask thresholds per qb (2)
 V_T = V_TK + 2          # temporaries (8); D of the lane's row per qb in V_T+1, V_T+2 at an item start
 V_ND = V_T + 1
+V_SPL = V_CS + 1        # bf16 split temporaries (5): in a body only V_CS and V_CS + 16 of the
+                        # start-value range are live (the rest serves the item boundary)
 assert V_T + 8 <= 256
 V_PT = 100              # prologue lane scratch (score set 1, free until the first body)
 EPI_BASE = V_CD[0]      # epilogue temporaries at an item boundary (the start values are rebuilt
@@ -110,8 +120,12 @@ def sblk(J, which, qb):
 
 
 class Body:
-    def __init__(self, p: Prog):
+    def __init__(self, p: Prog, dt: str = "f16"):
         self.p = p
+        self.dt = dt
+        self.mfma_op = MFMA_OF[dt]
+        self.pack_op = PACK_OF[dt]
+        self.split = dt == "bf16"
 
     def s(self, text, reads=(), writes=()):
         self.p.salu(text, reads, writes)
@@ -357,19 +371,31 @@ class Body:
         else:
             c = dst
         b = (A_Q if which == 0 else A_O) + (qb * 8 + ks) * 4
-        self.p.mfma(MFMA, dst, V_RB + ((2 * ks + which) % NRB) * 4, b, c, b_acc=True)
+        self.p.mfma(self.mfma_op, dst, V_RB + ((2 * ks + which) % NRB) * 4, b, c, b_acc=True)
 
     @staticmethod
     def ds_reg(J, qb, ks):
         """First of the four registers of packed dS^T (qb, ks) of set J (in dP^T qb's registers)."""
         return sblk(J, 1, qb) + 4 * ks
 
+    @staticmethod
+    def ds_lo_reg(J, qb, ks):
+        """bf16: first of the four registers of the lo halves of dS^T (qb, ks) (in S^T qb's)."""
+        return sblk(J, 0, qb) + 4 * ks
+
+    def dq_per_read(self):
+        """dQ^T MFMAs per K^T read: one per block of 32 rows, twice with the bf16 split."""
+        return 4 if self.split else 2
+
     def dq_mfma(self, j, J):
-        """Slot j of dQ^T from set J: vi = j // 2 (ks = vi // 4, db = vi % 4), qb = j % 2."""
-        vi, qb = j // 2, j % 2
+        """Slot j of dQ^T from set J: vi = j // dq_per_read() (ks = vi // 4, db = vi % 4),
+        qb = j % 2; bf16: hi for j % 4 < 2, then lo."""
+        n = self.dq_per_read()
+        vi, qb, lo = j // n, j % 2, (j % n) >= 2
         ks, db = vi // 4, vi % 4
         acc = A_DQ + (db * 2 + qb) * 16
-        self.p.mfma(MFMA, acc, V_TB + (vi % NTB) * 4, self.ds_reg(J, qb, ks), acc, dst_acc=True)
+        b = self.ds_lo_reg(J, qb, ks) if lo else self.ds_reg(J, qb, ks)
+        self.p.mfma(self.mfma_op, acc, V_TB + (vi % NTB) * 4, b, acc, dst_acc=True)
 
     # ---------------------------------------------------------------- elementwise (set J)
     @staticmethod
@@ -396,7 +422,24 @@ class Body:
             p.valu(f"v_mul_f32_e32 {vr(dp + k)}, {vr(x + k)}, {vr(dp + k)}", V(x + k) + V(dp + k), V(dp + k))
         # dS^T word (qb, ks, w) goes to register 4ks + w of dP^T qb: read by this step or an earlier one
         ds = self.ds_reg(J, qb, ks) + w
-        p.valu(f"v_cvt_pk_f16_f32 {vr(ds)}, {vr(dp)}, {vr(dp + 1)}", V(dp, 2), V(ds))
+        if not self.split:
+            p.valu(f"{self.pack_op} {vr(ds)}, {vr(dp)}, {vr(dp + 1)}", V(dp, 2), V(ds))
+            return
+        # bf16: hi = bf16(dS), lo = bf16(dS - hi); hi's halves as fp32 are its word shifted up /
+        # masked.  The lo word goes to register 4ks + w of S^T qb, which this step or an
+        # earlier one has read.  The hi word's register is this step's own dS (ks = w = 0), so
+        # there it is formed in a temporary and moved after the residuals.
+        t0, t1, th = V_SPL + 2 * (n % 2), V_SPL + 2 * (n % 2) + 1, V_SPL + 4
+        hw = th if ds in (dp, dp + 1) else ds
+        p.valu(f"v_cvt_pk_bf16_f32 {vr(hw)}, {vr(dp)}, {vr(dp + 1)}", V(dp, 2), V(hw))
+        p.valu(f"v_lshlrev_b32_e32 {vr(t0)}, 16, {vr(hw)}", V(hw), V(t0))
+        p.valu(f"v_and_b32_e32 {vr(t1)}, 0xffff0000, {vr(hw)}", V(hw), V(t1))
+        p.valu(f"v_sub_f32_e32 {vr(dp)}, {vr(dp)}, {vr(t0)}", V(dp) + V(t0), V(dp))
+        p.valu(f"v_sub_f32_e32 {vr(dp + 1)}, {vr(dp + 1)}, {vr(t1)}", V(dp + 1) + V(t1), V(dp + 1))
+        lw = self.ds_lo_reg(J, qb, ks) + w
+        p.valu(f"v_cvt_pk_bf16_f32 {vr(lw)}, {vr(dp)}, {vr(dp + 1)}", V(dp, 2), V(lw))
+        if hw != ds:
+            p.valu(f"v_mov_b32_e32 {vr(ds)}, {vr(hw)}", V(hw), V(ds))
 
     def mask_threshold(self):
         """Per qb: tq = min(causal ? q - k0 - 4hi : big, kvl - 1 - k0 - 4hi), k0 = 32*IT, q =
@@ -437,7 +480,7 @@ class Body:
                     self.row_read(rissued, jb1)
                     rissued += 1
                 if ew:
-                    while tissued < 8 and 32 + 2 * tissued - LV <= s_:
+                    while tissued < 8 and 32 + self.dq_per_read() * tissued - LV <= s_:
                         self.tr_read(tissued, jb0)
                         tissued += 1
                 self.sdp_mfma(s_, J1)
@@ -460,12 +503,15 @@ class Body:
         p.barrier()
         # --- dQ^T(it); DMA of tile it+3; first row reads of tile it+2
         dma_at = {34: 0, 38: 1, 42: 2, 46: 3}
-        for s_ in range(32, 48):
+        per = self.dq_per_read()
+        end = 32 + 8 * per
+        for s_ in range(32, end):
             if ew:
-                while tissued < 8 and 32 + 2 * tissued - LV <= s_:
+                while tissued < 8 and 32 + per * tissued - LV <= s_:
                     self.tr_read(tissued, jb0)
                     tissued += 1
-            p.ins.extend(h2[s_ - 32])
+            if s_ - 32 < len(h2):
+                p.ins.extend(h2[s_ - 32])
             if s_ in dma_at:
                 which, i = self.DMA_ORDER[dma_at[s_]]
                 self.dma_m0(which, jb3, i)
@@ -474,8 +520,8 @@ class Body:
             if s_ in dma_at:
                 which, i = self.DMA_ORDER[dma_at[s_]]
                 self.dma_ld(which, i)
-            if s_ >= 48 - LK:
-                self.row_read(s_ - (48 - LK), jb2)
+            if s_ >= end - LK:
+                self.row_read(s_ - (end - LK), jb2)
         un = (u + 1) % 4
         p.salu(f"s_cmp_eq_u32 {sr(S_CODE)}, 6", S(S_CODE), [("scc", 0)])
         p.branch(f"s_cbranch_scc1 .Lfull{un}", [("scc", 0)], keep_lgkm=True, skip_xdl=ACC)
@@ -568,6 +614,13 @@ class Body:
                         dv = dt
                     else:
                         dv = 64 + r
+                    if self.split:
+                        t0, t1 = V_TB + 4, V_TB + 5   # free at an item start (zeroed after)
+                        for op in ("v_lshlrev_b32_e32 {d}, 16, {s}", "v_and_b32_e32 {d}, 0xffff0000, {s}"):
+                            p.valu(op.format(d=vr(t0), s=vr(ob + r)), V(ob + r), V(t0))
+                            p.valu(op.format(d=vr(t1), s=vr(dv)), V(dv), V(t1))
+                            p.valu(f"v_fmac_f32_e32 {vr(acc)}, {vr(t0)}, {vr(t1)}", V(t0) + V(t1) + V(acc), V(acc))
+                        continue
                     for half in ("op_sel_hi:[1,1,0]", "op_sel:[1,1,0] op_sel_hi:[1,1,0]"):
                         p.valu(f"v_fma_mix_f32 {vr(acc)}, {vr(ob + r)}, {vr(dv)}, {vr(acc)} {half}",
                                V(ob + r) + V(dv) + V(acc), V(acc))
@@ -711,8 +764,8 @@ class Body:
                         p.valu(f"v_accvgpr_read_b32 {vr(W + j)}, {ar(a0 + j)}", A(a0 + j), V(W + j))
                     for j in range(4):
                         p.valu(f"v_mul_f32_e32 {vr(W + j)}, {sr(S_SCALE)}, {vr(W + j)}", V(W + j) + S(S_SCALE), V(W + j))
-                    p.valu(f"v_cvt_pk_f16_f32 {vr(W + 4)}, {vr(W)}, {vr(W + 1)}", V(W, 2), V(W + 4))
-                    p.valu(f"v_cvt_pk_f16_f32 {vr(W + 5)}, {vr(W + 2)}, {vr(W + 3)}", V(W + 2, 2), V(W + 5))
+                    p.valu(f"{self.pack_op} {vr(W + 4)}, {vr(W)}, {vr(W + 1)}", V(W, 2), V(W + 4))
+                    p.valu(f"{self.pack_op} {vr(W + 5)}, {vr(W + 2)}, {vr(W + 3)}", V(W + 2, 2), V(W + 5))
                     p.ds_write(f"ds_write_b64 {vr(BW)}, {vr(W + 4, 2)} offset:{(db * 4 + g4) * 16}", V(BW) + V(W + 4, 2))
                     W = W0 if W == W0 + 8 else W0 + 8
             for i in range(8):   # LDS operations of a wave complete in order: reads see the rows
@@ -740,10 +793,11 @@ class Body:
         p.branch(f"s_branch .Ldisp{u}", keep_lgkm=True, skip_xdl=ACC)
 
 
-def build(check_ldb: int = 12288) -> str:
+def build(check_ldb: int = 12288, dt: str = "f16") -> str:
+    """The kernel's assembly text: tkm_fa_bwd_dq_d128_f16 (dt "f16") or _bf16."""
     p = Prog(coalesce_lgkm=True)
     sal = p.salu
-    b = Body(p)
+    b = Body(p, dt)
     p.smem(f"s_load_dwordx16 {sr(8, 16)}, {sr(0, 2)}, 0x0", S(8, 16), S(0, 2))
     p.smem(f"s_load_dwordx16 {sr(24, 16)}, {sr(0, 2)}, 0x40", S(24, 16), S(0, 2))
     p.smem(f"s_load_dwordx2 {sr(S_MAGG, 2)}, {sr(0, 2)}, 0x80", S(S_MAGG, 2), S(0, 2))
@@ -808,7 +862,7 @@ def build(check_ldb: int = 12288) -> str:
     p.label(".Lexit")
     p.waitcnt(vm=0, lgkm=0)
     p.emit("s_endpgm", BRANCH)
-    return kernel_text(NAME, p.finalize(), lds_bytes=LDS_BYTES, kernarg_bytes=KERNARG_BYTES,
+    return kernel_text(f"tkm_fa_bwd_dq_d128_{dt}", p.finalize(), lds_bytes=LDS_BYTES, kernarg_bytes=KERNARG_BYTES,
                        next_free_sgpr=NEXT_FREE_SGPR, args=ARGS, wg_ids=(1, 0, 0))
 
 
