@@ -1,12 +1,13 @@
 """The attention kernels on trained weights (GPU).
 
 The forwards start each row's softmax offset m at the row maximum of the first 64-key tile and
-move it only when they must: the fp16 D = 128 assembly forward when a later tile has a score
-more than RESCALE_LOG2 = 15 log2 units above m (tokamak_amd/asmgen/attn_fwd.py), the HIP
-forward (D = 64, bf16) when a tile's packed P overflows its 16-bit type
-(tokamak_amd/csrc/attn_fwd.hip); both then rescale O and the row sums.  Random N(0,1) inputs
+move it only when they must: the D = 128 assembly forwards (fp16, bf16) when a later tile has a
+score more than RESCALE_LOG2 = 15 log2 units above m (tokamak_amd/asmgen/attn_fwd.py), the HIP
+forward (D = 64) when a tile's packed P overflows its 16-bit type or, in bf16, its packed P sum
+reaches 65504 (tokamak_amd/csrc/attn_fwd.hip); both then rescale O and the row sums.  Random N(0,1) inputs
 never do; trained attention that singles out a far key does.  This test trains, with the
-runtime, tests/golden/models/induction.tkm (two layers, GQA 4:2, head dim 128, causal, fp16)
+runtime, tests/golden/models/induction.tkm (two layers, GQA 4:2, head dim 128, causal, in fp16
+and in bf16)
 and BASELINE config 4's decoder (tests/golden/models/cfg4_llama.tkm: 8 heads of 64, causal,
 in fp16 and in bf16) on an induction task -- the second half of every sequence repeats the
 first, so the loss of the second half can only fall through attention to the key half a
@@ -82,6 +83,7 @@ def _time_fwd(qkv, B, S, Hq, Hkv, D, n=20):
 MODELS = [
     # name, storage type, vocabulary, steps, learning rate, forward kernel, attention layers checked
     ("induction", "f16", 256, 600, 0.05, "fwd_asm", None),
+    ("induction", "bf16", 256, 600, 0.05, "fwd_asm", None),
     ("cfg4", "f16", 8192, 300, 0.01, "fwd_hip", (0, -1)),
     ("cfg4", "bf16", 8192, 300, 0.01, "fwd_hip", (0, -1)),
 ]
