@@ -60,14 +60,15 @@ OUTPUTS = ("qkv", "xhat", "istd", "o", "lse", "dqkv", "din", "dgamma", "dbias")
 
 
 @pytest.mark.parametrize("shape,dtype", [((2, 384, 4, 2, 64), "f16"), ((2, 384, 4, 2, 64), "bf16"),
-                                         ((8, 512, 8, 8, 64), "bf16"), ((2, 512, 4, 2, 128), "f16")],
-                         ids=["gqa-f16", "gqa-bf16", "config4-bf16", "gqa-f16-d128-asm"])
+                                         ((8, 512, 8, 8, 64), "bf16"), ((2, 512, 4, 2, 128), "f16"),
+                                         ((2, 512, 4, 2, 128), "bf16")],
+                         ids=["gqa-f16", "gqa-bf16", "config4-bf16", "gqa-f16-d128-asm", "gqa-bf16-d128-asm"])
 def test_layer_step_graph_replays_match_eager(gpu, shape, dtype):
     """The layer step (qkv-prep forward, attention forward and backward, qkv-prep backward)
     captured once and replayed: every replay bit-equal to the eager step, both within the
     oracles' tolerances.  The third case is BASELINE config 4's attention layer: batch 8,
-    sequence 512, 8 heads of 64, bf16; the last one captures the gfx950 assembly kernels
-    (fp16, D = 128, launched through hipModuleLaunchKernel)."""
+    sequence 512, 8 heads of 64, bf16; the last two capture the gfx950 assembly kernels
+    (D = 128, fp16 and bf16, launched through hipModuleLaunchKernel)."""
     import torch
     from tokamak_amd import prep
     B, S, Hq, Hkv, D = shape
@@ -78,7 +79,7 @@ def test_layer_step_graph_replays_match_eager(gpu, shape, dtype):
         step(stream)
     torch.cuda.synchronize()
     eager = {k: buf[k].clone() for k in OUTPUTS}
-    if D == 128 and dtype == "f16":
+    if D == 128:
         from tokamak_amd import attn
         assert attn.last_kernels() == ["dq_asm", "dkdv_asm"], attn.last_kernels()
 
