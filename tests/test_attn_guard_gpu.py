@@ -7,8 +7,8 @@ After the forward and the backward:
   - the results match the oracle, which fails on any NaN (an out-of-bounds read whose value
     reaches a result, or an output element or workspace byte some kernel should have written
     and did not, would show as NaN).
-Shapes cover both kernel families (the assembly kernels for fp16 D=128, the HIP kernels
-otherwise), GQA, ragged S, per-batch key lengths with 0, and the causal diagonal."""
+Shapes cover both kernel families (the assembly kernels for D=128, fp16 and bf16, the HIP
+kernels for D=64), GQA, ragged S, per-batch key lengths with 0, and the causal diagonal."""
 import pytest
 
 import oracle
@@ -22,6 +22,8 @@ CASES = [  # B, S, Hq, Hkv, D, dtype, causal, kv_len
     (3, 131, 4, 2, 128, "f16", True, None),
     (2, 200, 4, 4, 64, "f16", True, [77, 200]),
     (2, 129, 6, 2, 128, "bf16", True, None),
+    (2, 333, 8, 2, 128, "bf16", False, [333, 0]),
+    (1, 6, 4, 2, 128, "bf16", True, [2]),
     (1, 517, 2, 1, 64, "bf16", False, [300]),
 ]
 
