@@ -113,7 +113,7 @@ TKM_ATTN_API int tkm_attn_bwd_stage(int stage, const void *qkv, const void *o, c
                                     int dtype, void *workspace, size_t workspace_bytes,
                                     void *stream);
 
-/* Loads this library's gfx950 assembly kernels (fp16, D = 128) on the current device.  Call
+/* Loads this library's gfx950 assembly kernels (D = 128, fp16 and bf16) on the current device.  Call
  * it once per device before capturing a graph, as the runtime does at ignite; otherwise the
  * first call on a device loads them (inside a capture, with the thread's capture mode
  * relaxed so that nothing is recorded).  Returns TKM_ATTN_OK (also on a device that is not

@@ -112,7 +112,7 @@ def gradient_term_rms(qkv, o_stored, dout, lse, B, S, Hq, Hkv, D, causal=True, k
 
 
 def fp16_forward_rescales(qkv, B, S, Hq, Hkv, D, causal, threshold=None):
-    """The fp16 D = 128 assembly forward's lazy rescale (tokamak_amd/asmgen/attn_fwd.py:
+    """The D = 128 assembly forwards' lazy rescale (tokamak_amd/asmgen/attn_fwd.py:
     rescale_test, rescale_if), evaluated on the CPU.  Per wave (64 query rows of one q-head):
     m_row starts as the row max over the first 64-key tile of s' = (q . k) * sl2 (fp32, log2
     units, visible keys only; 0 for a row with none there); each later tile the wave uses is

@@ -1,4 +1,5 @@
-"""GPU parity of the HIP attention path (through the C ABI) against the CPU oracle.
+"""GPU parity of the attention kernels (the gfx950 assembly kernels for D=128, the HIP kernels
+for D=64; through the C ABI) against the CPU oracle.
 
 Every case generates seeded inputs (oracle.make_inputs), runs tkm_attn_fwd / tkm_attn_bwd
 on cuda:0 and the oracle on the identical rounded values, and checks
@@ -408,7 +409,7 @@ def _random_cases(seed, n):
 @pytest.mark.parametrize("B,S,Hq,Hkv,D,dtype,causal,kv_len,seed", _random_cases(11, 20))
 def test_random_shapes(gpu, B, S, Hq, Hkv, D, dtype, causal, kv_len, seed):
     """Forward and backward of seeded random shapes against the oracle (the assembly kernels
-    for fp16 D=128, the HIP kernels otherwise)."""
+    for D=128, the HIP kernels for D=64)."""
     _assert_ok(run_gpu_case(gpu, B, S, Hq, Hkv, D, dtype=dtype, causal=causal, kv_len=kv_len, seed=seed))
 
 
@@ -528,7 +529,7 @@ def test_backward_on_forward_state(gpu, B, S, Hq, Hkv, D, dtype, causal, kv_len,
 
 
 def test_kernel_paths(gpu):
-    """Which kernels each configuration runs (tkm_attn_last_kernels): fp16 D=128 -- the
+    """Which kernels each configuration runs (tkm_attn_last_kernels): D=128 -- in fp16 the
     config-3 hot path -- and bf16 D=128 take the three gfx950 assembly kernels; D=64 the HIP
     kernels.  tkm_attn_init loads the code objects
     (the runtime calls it before capturing a step)."""
